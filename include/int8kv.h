@@ -1,0 +1,148 @@
+/*
+ * int8kv.h -- C ABI of the MI355X (gfx950) INT8 KV-cache library, libint8kv.so.
+ *
+ * Two hot operations of a static per-head symmetric INT8 KV cache:
+ *   1. the paged cache write (slot_mapping scatter, RNE quantisation, clamp to [-127, 127]);
+ *   2. PagedAttention decode over an INT8 cache (or a 16-bit cache, same kernel family),
+ *      split over fixed-size token chunks with online-softmax partials and a merge pass.
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers except the `*_strides` arrays, which are host arrays.
+ *   - Strides are in ELEMENTS of the tensor they describe (torch's Tensor.stride()).
+ *   - `stream` is a hipStream_t passed as void* (NULL = the legacy default stream).
+ *   - Nothing here allocates, frees or synchronises; every launch is enqueued on `stream`.
+ *   - The return value is 0 on success, a negative INT8KV_E* code for a rejected argument
+ *     (nothing was launched), or a positive hipError_t from the launch.
+ *   - No C++ exception crosses this boundary.
+ *
+ * Reference interfaces replaced (paths relative to the cjsmt/Int8-kvcache checkout):
+ *   int8kv_cache_write   <- src/triton_ops/int8_cache_write.py:85-149  (int8_kv_cache_write)
+ *   int8kv_paged_decode  <- src/triton_ops/int8_paged_attention.py:683-769 (int8_paged_attention,
+ *                           the V4 kernel :61-327 plus the split merge :330-388) and
+ *                           src/triton_ops/bf16_paged_attention.py:118-165 (bf16_paged_attention)
+ *   int8kv_decode_workspace_bytes <- the partial-buffer allocation of
+ *                           src/triton_ops/int8_paged_attention.py:594-603
+ */
+#ifndef INT8KV_H
+#define INT8KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type codes. */
+enum int8kv_dtype {
+  INT8KV_F32 = 0,
+  INT8KV_F16 = 1,
+  INT8KV_BF16 = 2,
+  INT8KV_I8 = 3,
+  INT8KV_I32 = 4,
+  INT8KV_I64 = 5
+};
+
+/* Argument errors (negative return values). */
+#define INT8KV_OK 0
+#define INT8KV_E_NULL (-1)      /* a required pointer is NULL */
+#define INT8KV_E_DTYPE (-2)     /* unsupported element type for this argument */
+#define INT8KV_E_SHAPE (-3)     /* unsupported or inconsistent size */
+#define INT8KV_E_STRIDE (-4)    /* innermost stride != 1 or rows not 16-byte aligned */
+#define INT8KV_E_WORKSPACE (-5) /* workspace missing or smaller than required */
+
+/* Flags of int8kv_paged_decode. */
+#define INT8KV_DECODE_MAIN 1u   /* run the chunked decode kernel */
+#define INT8KV_DECODE_MERGE 2u  /* run the split merge kernel */
+#define INT8KV_DECODE_ALL 3u
+
+/*
+ * Static per-head INT8 quantisation of K and V plus the slot_mapping scatter into the paged
+ * caches (replaces src/triton_ops/int8_cache_write.py:85-149 and its kernel :6-82).
+ *
+ *   for every token t with s = slot_mapping[t] in [0, num_blocks * block_size):
+ *     key_cache[s / block_size, s % block_size, h, :] =
+ *         clamp(rint(float(key[t, h, :]) / max(k_scale[h], 1e-6)), -127, 127)   (IEEE fp32 divide)
+ *   (value likewise with v_scale).  Tokens with s < 0 are skipped; slots at or beyond
+ *   num_blocks * block_size are skipped as well so that no access leaves the caches.
+ *
+ *   key/value:      [num_tokens, num_kv_heads, head_dim] of src_dtype (F32, F16, BF16),
+ *                   innermost stride 1, each (token, head) row 16-byte aligned.
+ *   key_cache/value_cache: int8 [num_blocks, block_size, num_kv_heads, head_dim],
+ *                   innermost stride 1, rows 8-byte aligned.
+ *   slot_mapping:   [num_tokens] of slot_dtype (I32 or I64), contiguous.
+ *   k_scale/v_scale: fp32 [num_kv_heads], contiguous.
+ *   head_dim must be a multiple of 8.
+ */
+int int8kv_cache_write(const void* key, const void* value, int src_dtype, int64_t num_tokens,
+                       int32_t num_kv_heads, int32_t head_dim, const int64_t key_strides[3],
+                       const int64_t value_strides[3], void* key_cache, void* value_cache,
+                       int64_t num_blocks, int32_t block_size, const int64_t key_cache_strides[4],
+                       const int64_t value_cache_strides[4], const void* slot_mapping,
+                       int slot_dtype, const float* k_scale, const float* v_scale, void* stream);
+
+/*
+ * Bytes of device workspace int8kv_paged_decode needs for these sizes (the split partials:
+ * one running max, one running sum and one head_dim accumulator per chunk and query head).
+ * chunk_tokens is the value that will be passed to int8kv_paged_decode (0 = automatic).
+ * Returns 0 for sizes int8kv_paged_decode would reject.
+ */
+size_t int8kv_decode_workspace_bytes(int64_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                     int32_t head_dim, int64_t table_width, int32_t block_size,
+                                     int32_t chunk_tokens);
+
+/*
+ * The chunk size in tokens int8kv_paged_decode uses for these sizes when chunk_tokens = 0.
+ */
+int32_t int8kv_decode_auto_chunk_tokens(int64_t batch, int32_t num_kv_heads, int64_t table_width,
+                                        int32_t block_size);
+
+/*
+ * Paged decode attention, one query token per sequence, GQA group = num_q_heads / num_kv_heads
+ * (replaces int8_paged_attention, src/triton_ops/int8_paged_attention.py:683-769, and
+ * bf16_paged_attention, src/triton_ops/bf16_paged_attention.py:118-165):
+ *
+ *   out[b, h, :] = sum_{t < L_b} softmax_t(<q[b, h], k_t> * ks * sm_scale) * v_t * vs
+ *   with g = h / group, k_t = key_cache[block_tables[b, t / bs], t % bs, g, :],
+ *   ks = max(k_scale[g], 1e-6), vs = max(v_scale[g], 1e-6) for an I8 cache and ks = vs = 1 for
+ *   a 16-bit cache, L_b = clamp(seq_lens[b], 0, table_width * block_size).  L_b = 0 gives 0.
+ *
+ *   query:        [batch, num_q_heads, head_dim] of query_dtype (F32, F16, BF16), innermost
+ *                 stride 1, rows 16-byte aligned.
+ *   key_cache/value_cache: [num_blocks, block_size, num_kv_heads, head_dim] of cache_dtype
+ *                 (I8, BF16 or F16), innermost stride 1, rows 16-byte aligned.
+ *   block_tables: [batch, table_width] of table_dtype (I32 or I64), any strides; entries for
+ *                 the blocks a sequence covers must lie in [0, num_blocks) (others are clamped
+ *                 into range so that every access stays inside the caches).
+ *   seq_lens:     [batch] of seq_lens_dtype (I32 or I64), contiguous.
+ *   k_scale/v_scale: fp32 [num_kv_heads] for an I8 cache; ignored (may be NULL) otherwise.
+ *   out:          [batch, num_q_heads, head_dim] of query_dtype, innermost stride 1.
+ *   workspace:    at least int8kv_decode_workspace_bytes(...) bytes, 16-byte aligned; it needs
+ *                 no initialisation and may be NULL when that size is 0.
+ *   chunk_tokens: tokens per work item (a multiple of 32, or 0 = automatic).  A sequence
+ *                 longer than one chunk is merged by the split merge kernel.
+ *   flags:        INT8KV_DECODE_ALL normally; MAIN and MERGE separately let a caller time the
+ *                 two kernels on their own (MERGE must follow MAIN with identical arguments).
+ *
+ * Supported sizes: head_dim = 128, block_size = 16, group = num_q_heads / num_kv_heads in
+ * [1, 16].  Other sizes return INT8KV_E_SHAPE.
+ */
+int int8kv_paged_decode(const void* query, int query_dtype, int64_t batch, int32_t num_q_heads,
+                        int32_t head_dim, const int64_t query_strides[3], const void* key_cache,
+                        const void* value_cache, int cache_dtype, int64_t num_blocks,
+                        int32_t block_size, int32_t num_kv_heads,
+                        const int64_t key_cache_strides[4], const int64_t value_cache_strides[4],
+                        const void* block_tables, int table_dtype, int64_t table_width,
+                        const int64_t table_strides[2], const void* seq_lens, int seq_lens_dtype,
+                        const float* k_scale, const float* v_scale, float sm_scale, void* out,
+                        const int64_t out_strides[3], void* workspace, size_t workspace_bytes,
+                        int32_t chunk_tokens, uint32_t flags, void* stream);
+
+/* Library version string, e.g. "int8kv 0.1.0 gfx950". */
+const char* int8kv_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INT8KV_H */

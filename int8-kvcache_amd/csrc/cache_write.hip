@@ -1,0 +1,172 @@
+// Static per-head INT8 KV-cache write for gfx950.
+//
+// Replaces the Triton kernel src/triton_ops/int8_cache_write.py:6-82 and its wrapper :85-149.
+// Numerics follow the reference's own oracle (src/quant.py:37-40 and the torch reference
+// src/triton_ops/int8_cache_write.py:172-181): an IEEE fp32 quotient x / scale, rounded half to
+// even (torch.round), clamped to [-127, 127].  The Triton kernel itself rounds half away from
+// zero (:59-63); this kernel deliberately does not.  The scale is clamped to >= 1e-6 as the
+// Triton kernel does (:50-51); calibrated scales already satisfy that (scripts/04 :55-65).
+//
+// Mapping: one lane owns 8 consecutive head_dim elements of one (token, kv-head) row of both
+// K and V, so a wave64 covers a whole 4 x 128 token row with 16-byte loads and 8-byte stores
+// (fully coalesced 128-byte segments per head).  The slot index and the two scales are
+// wave-uniform for head_dim * num_kv_heads = 512.
+
+#include "int8kv_common.h"
+
+namespace int8kv {
+
+struct WriteArgs {
+  const char* key;
+  const char* value;
+  int8_t* kc;
+  int8_t* vc;
+  const void* slots;
+  const float* k_scale;
+  const float* v_scale;
+  int64_t k_st, k_sh;  // element strides of key (token, head)
+  int64_t v_st, v_sh;
+  int64_t kc_sb, kc_ss, kc_sh;  // element (= byte) strides of the int8 caches
+  int64_t vc_sb, vc_ss, vc_sh;
+  int64_t num_tokens;
+  int64_t capacity;  // num_blocks * block_size
+  int32_t num_kv_heads;
+  int32_t vecs_per_row;  // head_dim / 8
+  int32_t block_size;
+  int32_t slots_is64;
+};
+
+__device__ __forceinline__ uint32_t quant4(const float* x, float s) {
+  uint32_t w = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // x / s is the correctly rounded IEEE quotient (hipcc's default fp32 division lowering,
+    // not a reciprocal multiply); rintf is round-half-to-even.
+    float q = rintf(x[i] / s);
+    q = fminf(fmaxf(q, -127.0f), 127.0f);
+    w |= ((uint32_t)((int32_t)q) & 0xffu) << (8 * i);
+  }
+  return w;
+}
+
+template <int SRC>
+__global__ __launch_bounds__(256) void cache_write_kernel(WriteArgs a) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t rows = a.num_tokens * a.num_kv_heads;
+  const int64_t row = gid / a.vecs_per_row;
+  if (row >= rows) return;
+  const int dv = (int)(gid - row * a.vecs_per_row);
+  const int h = (int)(row % a.num_kv_heads);
+  const int64_t t = row / a.num_kv_heads;
+
+  const int64_t slot = load_index(a.slots, t, a.slots_is64);
+  if (slot < 0 || slot >= a.capacity) return;
+  const int64_t blk = slot / a.block_size;
+  const int64_t off = slot - blk * a.block_size;
+
+  constexpr int esize = SRC == kF32 ? 4 : 2;
+  const float ks = fmaxf(a.k_scale[h], 1e-6f);
+  const float vs = fmaxf(a.v_scale[h], 1e-6f);
+
+  float x[8];
+  load8_f32<SRC>(a.key + (t * a.k_st + h * a.k_sh + 8 * dv) * esize, x);
+  u32x2 kq;
+  kq[0] = quant4(x, ks);
+  kq[1] = quant4(x + 4, ks);
+  load8_f32<SRC>(a.value + (t * a.v_st + h * a.v_sh + 8 * dv) * esize, x);
+  u32x2 vq;
+  vq[0] = quant4(x, vs);
+  vq[1] = quant4(x + 4, vs);
+
+  *reinterpret_cast<u32x2*>(a.kc + blk * a.kc_sb + off * a.kc_ss + h * a.kc_sh + 8 * dv) = kq;
+  *reinterpret_cast<u32x2*>(a.vc + blk * a.vc_sb + off * a.vc_ss + h * a.vc_sh + 8 * dv) = vq;
+}
+
+}  // namespace int8kv
+
+using namespace int8kv;
+
+static bool aligned(const void* p, int64_t stride_bytes, int64_t align) {
+  return ((uintptr_t)p % align) == 0 && (stride_bytes % align) == 0;
+}
+
+extern "C" int int8kv_cache_write(const void* key, const void* value, int src_dtype,
+                                  int64_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                                  const int64_t key_strides[3], const int64_t value_strides[3],
+                                  void* key_cache, void* value_cache, int64_t num_blocks,
+                                  int32_t block_size, const int64_t key_cache_strides[4],
+                                  const int64_t value_cache_strides[4], const void* slot_mapping,
+                                  int slot_dtype, const float* k_scale, const float* v_scale,
+                                  void* stream) {
+  if (!key_strides || !value_strides || !key_cache_strides || !value_cache_strides)
+    return INT8KV_E_NULL;
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 8 != 0 ||
+      num_blocks < 0 || block_size <= 0)
+    return INT8KV_E_SHAPE;
+  if (src_dtype != INT8KV_F32 && src_dtype != INT8KV_F16 && src_dtype != INT8KV_BF16)
+    return INT8KV_E_DTYPE;
+  if (slot_dtype != INT8KV_I32 && slot_dtype != INT8KV_I64) return INT8KV_E_DTYPE;
+  if (num_tokens == 0) return INT8KV_OK;
+  if (!key || !value || !key_cache || !value_cache || !slot_mapping || !k_scale || !v_scale)
+    return INT8KV_E_NULL;
+
+  // Each lane loads 8 source elements with 16-byte vector loads.
+  const int64_t esize = src_dtype == INT8KV_F32 ? 4 : 2;
+  if (key_strides[2] != 1 || value_strides[2] != 1 || key_cache_strides[3] != 1 ||
+      value_cache_strides[3] != 1)
+    return INT8KV_E_STRIDE;
+  if (!aligned(key, key_strides[0] * esize, 16) || !aligned(key, key_strides[1] * esize, 16) ||
+      !aligned(value, value_strides[0] * esize, 16) ||
+      !aligned(value, value_strides[1] * esize, 16))
+    return INT8KV_E_STRIDE;
+  for (int i = 0; i < 3; ++i) {
+    if (!aligned(key_cache, key_cache_strides[i], 8) ||
+        !aligned(value_cache, value_cache_strides[i], 8))
+      return INT8KV_E_STRIDE;
+  }
+
+  WriteArgs a;
+  a.key = static_cast<const char*>(key);
+  a.value = static_cast<const char*>(value);
+  a.kc = static_cast<int8_t*>(key_cache);
+  a.vc = static_cast<int8_t*>(value_cache);
+  a.slots = slot_mapping;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
+  a.k_st = key_strides[0];
+  a.k_sh = key_strides[1];
+  a.v_st = value_strides[0];
+  a.v_sh = value_strides[1];
+  a.kc_sb = key_cache_strides[0];
+  a.kc_ss = key_cache_strides[1];
+  a.kc_sh = key_cache_strides[2];
+  a.vc_sb = value_cache_strides[0];
+  a.vc_ss = value_cache_strides[1];
+  a.vc_sh = value_cache_strides[2];
+  a.num_tokens = num_tokens;
+  a.capacity = num_blocks * (int64_t)block_size;
+  a.num_kv_heads = num_kv_heads;
+  a.vecs_per_row = head_dim / 8;
+  a.block_size = block_size;
+  a.slots_is64 = slot_dtype == INT8KV_I64;
+
+  const int64_t lanes = num_tokens * num_kv_heads * (int64_t)a.vecs_per_row;
+  const int threads = 256;
+  const int64_t blocks = (lanes + threads - 1) / threads;
+  if (blocks > 0x7fffffffLL) return INT8KV_E_SHAPE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (src_dtype) {
+    case INT8KV_F32:
+      hipLaunchKernelGGL(cache_write_kernel<kF32>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+      break;
+    case INT8KV_F16:
+      hipLaunchKernelGGL(cache_write_kernel<kF16>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL(cache_write_kernel<kBF16>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+      break;
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" const char* int8kv_version(void) { return "int8kv 0.1.0 gfx950"; }

@@ -1,0 +1,109 @@
+"""Shared launcher of the paged decode kernel family (INT8 and 16-bit caches)."""
+
+from __future__ import annotations
+
+import math
+import os
+
+import torch
+
+from . import _lib
+
+QUERY_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+# When set, the op also runs the reference's host-synchronising input checks
+# (src/triton_ops/int8_paged_attention.py:720-723) and checks block ids; off by default because
+# each check is a device-to-host copy.
+DEBUG_CHECKS = os.environ.get("INT8KV_DEBUG", "0") not in ("", "0")
+
+
+def _aligned16(t: torch.Tensor, dims) -> bool:
+    e = t.element_size()
+    if t.data_ptr() % 16 or t.stride(-1) != 1:
+        return False
+    return all((t.stride(d) * e) % 16 == 0 for d in dims)
+
+
+def chunk_tokens_for(table_width: int, block_size: int, num_splits) -> int:
+    """Chunk size for a forced split count (0 = let the library choose)."""
+    if num_splits is None:
+        return 0
+    splits = max(1, int(num_splits))
+    tokens = table_width * block_size
+    per = -(-tokens // splits)
+    return max(32, -(-per // 32) * 32)
+
+
+def debug_check(block_tables, seq_lens, num_blocks, block_size, require_positive) -> None:
+    lens = seq_lens.to("cpu", torch.int64)
+    if require_positive:
+        assert int(lens.min()) > 0
+    need = -(-int(lens.max()) // block_size) if lens.numel() else 0
+    assert block_tables.shape[1] >= need
+    bt = block_tables.to("cpu", torch.int64)
+    for b, n in enumerate(lens.tolist()):
+        ids = bt[b, : -(-n // block_size)]
+        assert bool(((ids >= 0) & (ids < num_blocks)).all()), f"block id out of range in row {b}"
+
+
+def paged_decode(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    k_scale,
+    v_scale,
+    out: torch.Tensor,
+    chunk_tokens: int = 0,
+    flags: int = _lib.DECODE_ALL,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Launches int8kv_paged_decode on torch's current stream; returns ``out``."""
+    B, Hq, D = query.shape
+    num_blocks, block_size, Hkv, _ = key_cache.shape
+    width = block_tables.shape[1]
+    dev = query.device
+    if B == 0:
+        return out
+    if not _aligned16(query, (0, 1)):
+        query = query.contiguous()
+    seq_lens = seq_lens.contiguous()
+    lib = _lib.load()
+    need = lib.int8kv_decode_workspace_bytes(B, Hq, Hkv, D, width, block_size, chunk_tokens)
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    status = lib.int8kv_paged_decode(
+        query.data_ptr(),
+        _lib.DTYPE_CODE[query.dtype],
+        B,
+        Hq,
+        D,
+        _lib.strides(query),
+        key_cache.data_ptr(),
+        value_cache.data_ptr(),
+        _lib.DTYPE_CODE[key_cache.dtype],
+        num_blocks,
+        block_size,
+        Hkv,
+        _lib.strides(key_cache),
+        _lib.strides(value_cache),
+        block_tables.data_ptr(),
+        _lib.DTYPE_CODE[block_tables.dtype],
+        width,
+        _lib.strides(block_tables),
+        seq_lens.data_ptr(),
+        _lib.DTYPE_CODE[seq_lens.dtype],
+        k_scale.data_ptr() if k_scale is not None else None,
+        v_scale.data_ptr() if v_scale is not None else None,
+        1.0 / math.sqrt(D),
+        out.data_ptr(),
+        _lib.strides(out),
+        workspace.data_ptr() if need else None,
+        need,
+        chunk_tokens,
+        flags,
+        _lib.stream_handle(dev),
+    )
+    _lib.check(status, "int8kv_paged_decode")
+    return out

@@ -1,0 +1,90 @@
+"""ctypes binding of libint8kv.so (the C ABI declared in include/int8kv.h).
+
+The library is required: if it is missing every operator raises instead of computing anything
+elsewhere.  Torch is used only to read tensor metadata (pointers, strides, the current stream).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libint8kv.so"
+
+# enum int8kv_dtype
+F32, F16, BF16, I8, I32, I64 = 0, 1, 2, 3, 4, 5
+DTYPE_CODE = {
+    torch.float32: F32,
+    torch.float16: F16,
+    torch.bfloat16: BF16,
+    torch.int8: I8,
+    torch.int32: I32,
+    torch.int64: I64,
+}
+
+DECODE_MAIN, DECODE_MERGE, DECODE_ALL = 1, 2, 3
+
+ERRORS = {
+    -1: "INT8KV_E_NULL (a required pointer is NULL)",
+    -2: "INT8KV_E_DTYPE (unsupported element type)",
+    -3: "INT8KV_E_SHAPE (unsupported or inconsistent size)",
+    -4: "INT8KV_E_STRIDE (innermost stride != 1 or rows not 16-byte aligned)",
+    -5: "INT8KV_E_WORKSPACE (workspace missing or too small)",
+}
+
+_c_i64p = ctypes.POINTER(ctypes.c_int64)
+_vp = ctypes.c_void_p
+_lib = None
+
+
+class Int8KVError(RuntimeError):
+    """A non-zero status returned by libint8kv.so."""
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is not built; run `python -m int8kv._build` or "
+            "__graft_entry__.build() first (there is no non-HIP implementation)"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    i32, i64, u32, f32, sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_float, ctypes.c_size_t
+    lib.int8kv_cache_write.restype = ctypes.c_int
+    lib.int8kv_cache_write.argtypes = [
+        _vp, _vp, ctypes.c_int, i64, i32, i32, _c_i64p, _c_i64p, _vp, _vp, i64, i32,
+        _c_i64p, _c_i64p, _vp, ctypes.c_int, _vp, _vp, _vp,
+    ]
+    lib.int8kv_decode_workspace_bytes.restype = sz
+    lib.int8kv_decode_workspace_bytes.argtypes = [i64, i32, i32, i32, i64, i32, i32]
+    lib.int8kv_decode_auto_chunk_tokens.restype = i32
+    lib.int8kv_decode_auto_chunk_tokens.argtypes = [i64, i32, i64, i32]
+    lib.int8kv_paged_decode.restype = ctypes.c_int
+    lib.int8kv_paged_decode.argtypes = [
+        _vp, ctypes.c_int, i64, i32, i32, _c_i64p, _vp, _vp, ctypes.c_int, i64, i32, i32,
+        _c_i64p, _c_i64p, _vp, ctypes.c_int, i64, _c_i64p, _vp, ctypes.c_int, _vp, _vp, f32,
+        _vp, _c_i64p, _vp, sz, i32, u32, _vp,
+    ]
+    lib.int8kv_version.restype = ctypes.c_char_p
+    lib.int8kv_version.argtypes = []
+    _lib = lib
+    return lib
+
+
+def strides(t: torch.Tensor):
+    st = t.stride()
+    return (ctypes.c_int64 * len(st))(*st)
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = ERRORS.get(status, f"hipError_t {status}")
+        raise Int8KVError(f"{what} failed: {msg}")
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

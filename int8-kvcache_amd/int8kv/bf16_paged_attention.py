@@ -1,0 +1,47 @@
+"""BF16 PagedAttention decode (drop-in for src/triton_ops/bf16_paged_attention.py).
+
+Same kernel family as the INT8 path with the dequantisation compiled out: the cache operands
+feed the bf16 (or fp16) matrix cores directly.  Signature and output convention follow
+src/triton_ops/bf16_paged_attention.py:118-165 (output shaped and typed like ``query``).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _decode
+
+
+def bf16_paged_attention(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    *,
+    num_splits: int | None = None,
+) -> torch.Tensor:
+    """Paged decode on a 16-bit KV cache [num_blocks, BS, Hkv, D] (bf16 or fp16)."""
+    assert query.ndim == 3 and key_cache.ndim == 4 and value_cache.ndim == 4
+    assert block_tables.ndim == 2 and seq_lens.ndim == 1
+    assert query.dtype in _decode.QUERY_DTYPES
+    assert key_cache.dtype in (torch.bfloat16, torch.float16)
+    assert value_cache.dtype == key_cache.dtype
+    assert block_tables.dtype in (torch.int32, torch.int64)
+    assert seq_lens.dtype in (torch.int32, torch.int64)
+    B, Hq, D = query.shape
+    num_blocks, block_size, Hkv, cache_D = key_cache.shape
+    assert value_cache.shape == key_cache.shape
+    assert cache_D == D and Hq % Hkv == 0
+    assert block_tables.shape[0] == B and seq_lens.numel() == B
+    assert key_cache.stride(-1) == 1 and value_cache.stride(-1) == 1
+    tensors = (query, key_cache, value_cache, block_tables, seq_lens)
+    assert all(t.is_cuda for t in tensors), "bf16_paged_attention needs GPU tensors"
+    assert all(t.device == query.device for t in tensors), "all tensors must be on one device"
+    if _decode.DEBUG_CHECKS:
+        _decode.debug_check(block_tables, seq_lens, num_blocks, block_size, False)
+    chunk = _decode.chunk_tokens_for(block_tables.shape[1], block_size, num_splits)
+    output = torch.empty((B, Hq, D), device=query.device, dtype=query.dtype)
+    return _decode.paged_decode(
+        query, key_cache, value_cache, block_tables, seq_lens, None, None, output, chunk
+    )

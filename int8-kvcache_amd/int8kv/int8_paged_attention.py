@@ -1,0 +1,74 @@
+"""INT8 PagedAttention decode (drop-in for src/triton_ops/int8_paged_attention.py).
+
+``int8_paged_attention`` keeps the reference signature, keyword semantics and validation
+(src/triton_ops/int8_paged_attention.py:683-769) and runs the gfx950 kernel family of
+libint8kv.so.  Differences that a caller can observe:
+
+* No host synchronisation: the reference's ``seq_lens.min()/max().item()`` checks (:720-723)
+  only run when the environment variable INT8KV_DEBUG=1 is set.  The kernel bounds every
+  sequence by ``block_tables.shape[1] * block_size`` instead and writes 0 for empty sequences.
+* ``impl``: "v4" and "auto" run the group-shared kernel with automatic chunking; "v3" (one
+  pass per sequence in the reference, :393-504) runs the same kernel with one chunk per
+  sequence.  Any other value raises ValueError, as in the reference (:767-768).
+* ``num_splits``: an integer forces that many chunks over the block-table width (the
+  reference splits the logical blocks of the longest sequence into that many ranges, :156-162).
+* ``num_warps`` is accepted and ignored; ``quantize_q=True`` raises NotImplementedError.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _decode
+
+
+def int8_paged_attention(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    k_scale: torch.Tensor,
+    v_scale: torch.Tensor,
+    *,
+    quantize_q: bool = False,
+    num_warps: int = 4,
+    impl: str = "auto",
+    num_splits: int | None = None,
+) -> torch.Tensor:
+    """Paged decode on an INT8 KV cache.  Returns [B, Hq, D] in query.dtype."""
+    # Validation mirrors src/triton_ops/int8_paged_attention.py:698-719.
+    assert query.ndim == 3 and key_cache.ndim == 4 and value_cache.ndim == 4
+    assert block_tables.ndim == 2 and seq_lens.ndim == 1
+    assert query.dtype in _decode.QUERY_DTYPES
+    assert key_cache.dtype == torch.int8 and value_cache.dtype == torch.int8
+    assert block_tables.dtype in (torch.int32, torch.int64)
+    assert seq_lens.dtype in (torch.int32, torch.int64)
+    B, Hq, D = query.shape
+    num_blocks, block_size, Hkv, cache_D = key_cache.shape
+    assert value_cache.shape == key_cache.shape
+    assert cache_D == D and Hq % Hkv == 0
+    assert block_tables.shape[0] == B and seq_lens.numel() == B
+    assert k_scale.ndim == 1 and v_scale.ndim == 1
+    assert k_scale.numel() == Hkv and v_scale.numel() == Hkv
+    assert key_cache.stride(-1) == 1 and value_cache.stride(-1) == 1
+    tensors = (query, key_cache, value_cache, block_tables, seq_lens, k_scale, v_scale)
+    assert all(t.is_cuda for t in tensors), "int8_paged_attention needs GPU tensors"
+    assert all(t.device == query.device for t in tensors), "all tensors must be on one device"
+    if impl not in ("auto", "v3", "v4"):
+        raise ValueError(f"Unknown impl={impl!r}; expected 'auto', 'v3' or 'v4'")
+    if quantize_q:
+        raise NotImplementedError("quantize_q=True is not implemented by the HIP kernels yet")
+    if _decode.DEBUG_CHECKS:
+        _decode.debug_check(block_tables, seq_lens, num_blocks, block_size, True)
+
+    k_scale = k_scale.to(torch.float32).contiguous()
+    v_scale = v_scale.to(torch.float32).contiguous()
+    width = block_tables.shape[1]
+    if impl == "v3" and num_splits is None:
+        num_splits = 1
+    chunk = _decode.chunk_tokens_for(width, block_size, num_splits)
+    output = torch.empty((B, Hq, D), device=query.device, dtype=query.dtype)
+    return _decode.paged_decode(
+        query, key_cache, value_cache, block_tables, seq_lens, k_scale, v_scale, output, chunk
+    )

@@ -1,0 +1,152 @@
+"""GPU parity of the static INT8 cache write: bit-exact against the oracle.
+
+Mirrors the reference's write tests (tests/test_int8_paged_attention.py:183-210,
+tests/test_cache_write.py, tests/test_runtime_cache_write.py) with the stricter bar the build
+targets: every int8 byte equal to the round-half-even oracle (the reference tolerated |diff| <= 1
+because its Triton kernel rounds half away from zero).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import int8kv
+from int8kv import synthetic as syn
+from oracle import int8kv_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = 0x5A
+
+
+def _run(key, value, slots, ks, vs, nb, dev, sentinel=SENTINEL, kc=None, vc=None):
+    hkv, d = key.shape[1], key.shape[2]
+    if kc is None:
+        kc = torch.full((nb, 16, hkv, d), sentinel, dtype=torch.int8, device=dev)
+        vc = torch.full_like(kc, sentinel)
+    int8kv.int8_kv_cache_write(key.to(dev), value.to(dev), kc, vc, slots.to(dev), ks.to(dev), vs.to(dev))
+    torch.cuda.synchronize()
+    kr = np.full((nb, 16, hkv, d), sentinel, np.int8)
+    vr = np.full_like(kr, sentinel)
+    O.int8_kv_cache_write(key.float().cpu().numpy(), value.float().cpu().numpy(), kr, vr,
+                          slots.cpu().numpy(), ks.cpu().numpy(), vs.cpu().numpy())
+    return kc, vc, kr, vr
+
+
+def _assert_equal(kc, vc, kr, vr):
+    kg, vg = kc.cpu().numpy(), vc.cpu().numpy()
+    nk = int((kg != kr).sum())
+    nv = int((vg != vr).sum())
+    assert nk == 0 and nv == 0, f"{nk} K bytes and {nv} V bytes differ from the oracle"
+
+
+def test_write_config0_shape(cuda):
+    g = torch.Generator().manual_seed(0)
+    dist = syn.make_distribution(0)
+    ks, vs = syn.calibrate_scales(dist, seed=1)
+    k, v = syn.sample_kv(512, dist, g)
+    bt = syn.random_block_tables([512], 64, g)
+    slots = syn.slot_mapping_for(bt, [512])
+    _assert_equal(*_run(k, v, slots, ks, vs, 64, cuda))
+
+
+def test_write_config1_prefill_with_padding(cuda):
+    """8 x 2048 tokens into 2048 blocks x 16 via a random-permutation slot mapping, -1 pads."""
+    g = torch.Generator().manual_seed(11)
+    dist = syn.make_distribution(11)
+    ks, vs = syn.calibrate_scales(dist, seed=12)
+    n_tok, n_pad, nb = 16384, 512, 2048
+    k, v = syn.sample_kv(n_tok + n_pad, dist, g)
+    slots = torch.randperm(nb * 16, generator=g)[: n_tok + n_pad].to(torch.int64)
+    pad_rows = torch.randperm(n_tok + n_pad, generator=g)[:n_pad]
+    slots[pad_rows] = -1
+    kc, vc, kr, vr = _run(k, v, slots, ks, vs, nb, cuda)
+    _assert_equal(kc, vc, kr, vr)
+    untouched = np.ones(nb * 16, bool)
+    untouched[slots[slots >= 0].numpy()] = False
+    assert (kc.cpu().numpy().reshape(nb * 16, -1)[untouched] == SENTINEL).all()
+
+
+@pytest.mark.parametrize("src_dtype", [torch.float16, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("slot_dtype", [torch.int32, torch.int64])
+def test_write_dtypes(cuda, src_dtype, slot_dtype):
+    g = torch.Generator().manual_seed(3)
+    k = (torch.randn(300, 4, 128, generator=g) * 2).to(src_dtype)
+    v = torch.randn(300, 4, 128, generator=g).to(src_dtype)
+    ks = (k.float().abs().amax(dim=(0, 2)) / 127.0).clamp_min(1e-6)
+    vs = (v.float().abs().amax(dim=(0, 2)) / 127.0).clamp_min(1e-6)
+    slots = torch.randperm(40 * 16, generator=g)[:300].to(slot_dtype)
+    _assert_equal(*_run(k, v, slots, ks, vs, 40, cuda))
+
+
+def test_write_divide_and_tie_known_answers(cuda):
+    """IEEE fp32 quotients on exact .5 ties: -23, -21, -18 (a reciprocal multiply gives -22, -20,
+    -17; an fp64 divide gives -17 for the last one)."""
+    kats = [(-0.08251953125, 0.0036675346, -23), (-0.232421875, 0.011337652, -21),
+            (-0.9296875, 0.053125, -18)]
+    key = torch.zeros(2, 4, 128, dtype=torch.bfloat16)
+    ks = torch.ones(4)
+    for h, (x, s, _) in enumerate(kats):
+        key[0, h, :] = x
+        ks[h] = s
+    key[0, 3, :8] = torch.tensor([2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 300.0, -300.0])
+    key[1] = key[0]
+    value = key.clone()
+    slots = torch.tensor([5, 17], dtype=torch.int64)
+    kc, vc, kr, vr = _run(key, value, slots, ks, ks, 2, cuda)
+    _assert_equal(kc, vc, kr, vr)
+    got = kc.cpu()
+    for h, (_, _, want) in enumerate(kats):
+        assert (got[0, 5, h] == want).all() and (got[1, 1, h] == want).all()
+    assert got[0, 5, 3, :8].tolist() == [2, 4, -2, -4, 0, 0, 127, -127]
+
+
+def test_write_reference_fixed_scales_and_slots(cuda):
+    """tests/test_cache_write.py:21-38 (scales that clamp; slots 16..31, 64..79, 96..100) and
+    tests/test_runtime_cache_write.py:28-29 (slots 7..29 across a block boundary)."""
+    g = torch.Generator().manual_seed(41)
+    key = torch.randn(37, 4, 128, generator=g).to(torch.bfloat16)
+    value = torch.randn(37, 4, 128, generator=g).to(torch.bfloat16)
+    ks = torch.tensor([0.03, 0.025, 0.04, 0.035])
+    vs = torch.tensor([0.035, 0.03, 0.025, 0.04])
+    slots = torch.tensor(list(range(16, 32)) + list(range(64, 80)) + list(range(96, 101)))
+    _assert_equal(*_run(key, value, slots, ks, vs, 8, cuda, sentinel=0))
+    k23, v23 = key[:23], value[:23]
+    ks2 = (k23.float().abs().amax(dim=(0, 2)) / 127).clamp_min(1e-6)
+    vs2 = (v23.float().abs().amax(dim=(0, 2)) / 127).clamp_min(1e-6)
+    _assert_equal(*_run(k23, v23, torch.arange(7, 30), ks2, vs2, 16, cuda, sentinel=0))
+
+
+def test_write_strided_views(cuda):
+    """key/value as head-slices of a fused qkv projection and caches as views of the
+    [num_blocks, 2, BS, Hkv, D] split layout (vllm_shadow_cache_patch.py:26-43)."""
+    g = torch.Generator().manual_seed(5)
+    T, hq, hkv, d, nb = 77, 28, 4, 128, 12
+    qkv = torch.randn(T, (hq + 2 * hkv) * d, generator=g).to(torch.bfloat16).to(cuda)
+    key = qkv[:, hq * d:(hq + hkv) * d].view(T, hkv, d)
+    value = qkv[:, (hq + hkv) * d:].view(T, hkv, d)
+    assert not key.is_contiguous()
+    ks = (key.float().abs().amax(dim=(0, 2)) / 127).clamp_min(1e-6)
+    vs = (value.float().abs().amax(dim=(0, 2)) / 127).clamp_min(1e-6)
+    kv = torch.full((nb, 2, 16, hkv, d), SENTINEL, dtype=torch.int8, device=cuda)
+    slots = torch.randperm(nb * 16, generator=g)[:T]
+    kc, vc, kr, vr = _run(key, value, slots, ks, vs, nb, cuda, kc=kv[:, 0], vc=kv[:, 1])
+    _assert_equal(kc, vc, kr, vr)
+
+
+def test_write_empty_and_out_of_range(cuda):
+    k = torch.zeros(0, 4, 128, dtype=torch.bfloat16, device=cuda)
+    kc = torch.full((2, 16, 4, 128), SENTINEL, dtype=torch.int8, device=cuda)
+    vc = kc.clone()
+    s = torch.ones(4, device=cuda)
+    int8kv.int8_kv_cache_write(k, k, kc, vc, torch.zeros(0, dtype=torch.int64, device=cuda), s, s)
+    torch.cuda.synchronize()
+    assert (kc == SENTINEL).all()
+    # Slots beyond the cache are skipped (no write outside the allocation).
+    k = torch.ones(3, 4, 128, dtype=torch.bfloat16)
+    slots = torch.tensor([32, 1000, 3], dtype=torch.int64)
+    kc, vc, kr, vr = _run(k, k, slots, torch.ones(4), torch.ones(4), 2, cuda)
+    _assert_equal(kc, vc, kr, vr)
+    assert (kc.cpu()[0, 3] == 1).all()

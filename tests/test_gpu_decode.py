@@ -1,0 +1,202 @@
+"""GPU parity of INT8 / BF16 PagedAttention decode against the fp32 oracle.
+
+Bar: max |out - oracle| <= 2e-2 and cosine >= 0.9999, where the oracle is
+the reference's INT8 path run in fp32 (src/triton_ops/int8_paged_attention.py:776-814) on the
+same int8 cache bytes.  Cases mirror the reference's tests (tests/test_int8_paged_attention.py:
+108-323, tests/test_runtime_write_and_attention.py) plus the benchmark configurations, ragged
+batches, block and chunk boundaries, strided views and every supported dtype.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import int8kv
+from cases import bf16_caches, decode_case, oracle_int8, to_dev
+from conftest import MAX_ABS, MIN_COS, metrics
+from oracle import int8kv_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(out, ref, what=""):
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    err, cos, rel = metrics(got, ref)
+    print(f"{what}: max|diff|={err:.3e} cos={cos:.7f} relL2={rel:.3e}", flush=True)
+    assert err <= MAX_ABS and cos >= MIN_COS, f"{what}: max|diff|={err} cos={cos}"
+    return err, cos
+
+
+def _int8(case, dev, **kw):
+    q, kc, vc, bt, sl, ks, vs = to_dev(case, dev)
+    out = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("lens,seed", [([127, 301], 0), ([97, 256], 1)])
+@pytest.mark.parametrize("kw", [{}, {"impl": "v3"}, {"impl": "v4", "num_splits": 1},
+                                {"impl": "v4", "num_splits": 4}, {"impl": "auto"}])
+def test_reference_test_shapes(cuda, lens, seed, kw):
+    """tests/test_int8_paged_attention.py:108-323 shapes and options (randn K/V)."""
+    c = decode_case(lens, seed=seed, randn_kv=True, extra_blocks=20)
+    _check(_int8(c, cuda, **kw), oracle_int8(c), f"{lens} {kw}")
+
+
+def test_config0(cuda):
+    c = decode_case([512], seed=0, extra_blocks=32)
+    _check(_int8(c, cuda), oracle_int8(c), "cfg0")
+
+
+@pytest.mark.parametrize("B", [1, 2, 4, 8])
+@pytest.mark.parametrize("ctx", [512, 1024, 2048, 4096])
+def test_config2_sweep(cuda, B, ctx):
+    c = decode_case([ctx] * B, seed=B * 7 + ctx)
+    ref = oracle_int8(c)
+    _check(_int8(c, cuda), ref, f"B={B} ctx={ctx} auto")
+    _check(_int8(c, cuda, num_splits=1), ref, f"B={B} ctx={ctx} single-pass")
+
+
+@pytest.mark.parametrize("lens", [
+    [1], [2, 15, 16, 17], [31, 32, 33], [63, 64, 65], [127, 128, 129, 130],
+    [511, 512, 513], [1, 4096, 3, 777], [1023, 1024, 1025, 2047, 2048, 2049],
+])
+def test_tile_block_chunk_boundaries(cuda, lens):
+    c = decode_case(lens, seed=len(lens) * 31 + lens[0])
+    ref = oracle_int8(c)
+    for chunk in (None, 1, 3, 7):
+        _check(_int8(c, cuda, num_splits=chunk), ref, f"{lens} splits={chunk}")
+
+
+def test_one_token_sequences_return_v0(cuda):
+    c = decode_case([1, 1, 1], seed=4)
+    out = _int8(c, cuda).float().cpu().numpy()
+    for b in range(3):
+        blk = int(c.block_tables[b, 0])
+        v0 = c.vc[blk, 0].astype(np.float32) * c.v_scale.numpy()[:, None]  # [Hkv, D]
+        expect = np.repeat(v0, 7, axis=0)
+        assert np.abs(out[b] - expect).max() <= 4e-3 * np.abs(expect).max()
+
+
+def test_empty_sequence_gives_zeros(cuda):
+    c = decode_case([300, 5], seed=5)
+    sl = c.seq_lens.clone()
+    sl[1] = 0
+    q, kc, vc, bt, _, ks, vs = to_dev(c, cuda)
+    out = int8kv.int8_paged_attention(q, kc, vc, bt, sl.to(cuda), ks, vs)
+    torch.cuda.synchronize()
+    ref = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                sl.numpy(), c.k_scale.numpy(), c.v_scale.numpy())
+    assert (out[1] == 0).all()
+    _check(out, ref, "empty")
+
+
+@pytest.mark.parametrize("qdtype", [torch.float16, torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64])
+def test_dtypes(cuda, qdtype, idx_dtype):
+    c = decode_case([700, 33, 1500], seed=6)
+    q = c.query.to(qdtype)
+    q_d, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    out = int8kv.int8_paged_attention(q.to(cuda), kc, vc, bt.to(idx_dtype), sl.to(idx_dtype),
+                                      ks, vs)
+    torch.cuda.synchronize()
+    assert out.dtype == qdtype and out.shape == q.shape
+    _check(out, oracle_int8(c, query=q), f"q={qdtype} idx={idx_dtype}")
+
+
+def test_strided_views(cuda):
+    """Caches as views of the [num_blocks, 2, BS, Hkv, D] split layout, the query as a slice of a
+    padded batch (vllm_int8_attention_patch.py:126-127) and a wider block table."""
+    c = decode_case([400, 129, 1000], seed=8, width=80)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    kv = torch.empty((c.num_blocks, 2, 16, 4, 128), dtype=torch.int8, device=cuda)
+    kv[:, 0] = kc
+    kv[:, 1] = vc
+    qpad = torch.zeros((5, 28, 128), dtype=q.dtype, device=cuda)
+    qpad[:3] = q
+    bt_wide = torch.zeros((3, 2 * bt.shape[1]), dtype=bt.dtype, device=cuda)
+    bt_wide[:, ::2] = bt
+    bt_view = bt_wide[:, ::2]  # non-unit column stride
+    out = int8kv.int8_paged_attention(qpad[:3], kv[:, 0], kv[:, 1], bt_view, sl, ks, vs)
+    torch.cuda.synchronize()
+    _check(out, oracle_int8(c), "strided")
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 2), (32, 2), (12, 4)])
+def test_group_sizes(cuda, hq, hkv):
+    c = decode_case([333, 1200], seed=hq + hkv, hq=hq, hkv=hkv)
+    _check(_int8(c, cuda), oracle_int8(c), f"Hq={hq} Hkv={hkv}")
+
+
+def test_ragged_batch(cuda):
+    lens = torch.randint(1, 4097, (16,), generator=torch.Generator().manual_seed(9)).tolist()
+    c = decode_case(lens, seed=9)
+    ref = oracle_int8(c)
+    _check(_int8(c, cuda), ref, "ragged auto")
+    _check(_int8(c, cuda, num_splits=2), ref, "ragged splits=2")
+
+
+@pytest.mark.parametrize("cache_dtype", [torch.bfloat16, torch.float16])
+def test_bf16_kernel(cuda, cache_dtype):
+    lens = [127, 301, 1, 2048, 33]
+    c = decode_case(lens, seed=10)
+    kc, vc = bf16_caches(c, cache_dtype)
+    ref = O.paged_attention_ref(c.query.float().numpy(), kc.float().numpy(), vc.float().numpy(),
+                                c.block_tables.numpy(), c.seq_lens.numpy())
+    dev = cuda
+    for splits in (None, 1, 5):
+        out = int8kv.bf16_paged_attention(c.query.to(dev), kc.to(dev), vc.to(dev),
+                                          c.block_tables.to(dev), c.seq_lens.to(dev),
+                                          num_splits=splits)
+        torch.cuda.synchronize()
+        _check(out, ref, f"{cache_dtype} splits={splits}")
+
+
+def test_bf16_kernel_ignores_nonfinite_tail(cuda):
+    """Cache rows past a sequence's end may hold NaN/Inf: they must not reach the output."""
+    lens = [17, 40]
+    c = decode_case(lens, seed=12)
+    kc, vc = bf16_caches(c)
+    written = torch.zeros(c.num_blocks * 16, dtype=torch.bool)
+    written[c.slots] = True
+    kf, vf = kc.view(-1, 4, 128).clone(), vc.view(-1, 4, 128).clone()
+    kf[~written] = float("nan")
+    vf[~written] = float("inf")
+    kc, vc = kf.view_as(kc), vf.view_as(vc)
+    ref = O.paged_attention_ref(c.query.float().numpy(), kc.float().numpy(), vc.float().numpy(),
+                                c.block_tables.numpy(), c.seq_lens.numpy())
+    out = int8kv.bf16_paged_attention(c.query.to(cuda), kc.to(cuda), vc.to(cuda),
+                                      c.block_tables.to(cuda), c.seq_lens.to(cuda))
+    torch.cuda.synchronize()
+    _check(out, ref, "nan tail")
+
+
+def test_int8_vs_bf16_quantisation_error(cuda):
+    """INT8 path vs the BF16 kernel on the unquantised data: cos > 0.98
+    (tests/test_int8_paged_attention.py:245-270)."""
+    c = decode_case([127, 301], seed=0, randn_kv=True)
+    kc, vc = bf16_caches(c)
+    out8 = _int8(c, cuda).float().cpu().numpy()
+    out16 = int8kv.bf16_paged_attention(c.query.to(cuda), kc.to(cuda), vc.to(cuda),
+                                        c.block_tables.to(cuda), c.seq_lens.to(cuda))
+    _, cos, _ = metrics(out8, out16.float().cpu().numpy())
+    assert cos > 0.98
+
+
+def test_write_then_decode_end_to_end(cuda):
+    """runtime write -> decode (tests/test_runtime_write_and_attention.py:218-458)."""
+    c = decode_case([127, 301], seed=0, randn_kv=True)
+    kc = torch.zeros(c.num_blocks, 16, 4, 128, dtype=torch.int8, device=cuda)
+    vc = torch.zeros_like(kc)
+    int8kv.int8_kv_cache_write(c.key.to(cuda), c.value.to(cuda), kc, vc, c.slots.to(cuda),
+                               c.k_scale.to(cuda), c.v_scale.to(cuda))
+    out = int8kv.int8_paged_attention(c.query.to(cuda), kc, vc, c.block_tables.to(cuda),
+                                      c.seq_lens.to(cuda), c.k_scale.to(cuda), c.v_scale.to(cuda))
+    torch.cuda.synchronize()
+    ref = O.paged_attention_ref(c.query.float().numpy(), kc.cpu().numpy(), vc.cpu().numpy(),
+                                c.block_tables.numpy(), c.seq_lens.numpy(), c.k_scale.numpy(),
+                                c.v_scale.numpy())
+    _check(out, ref, "write->decode")

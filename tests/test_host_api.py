@@ -1,0 +1,110 @@
+"""CPU checks of the Python operator layer: reference-compatible validation and errors, and
+that nothing computes without the GPU library (no CPU fallback)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import int8kv
+from int8kv import _decode
+from int8kv import synthetic as syn
+
+
+def _attn_args(**over):
+    a = dict(
+        query=torch.zeros(2, 28, 128, dtype=torch.bfloat16),
+        key_cache=torch.zeros(8, 16, 4, 128, dtype=torch.int8),
+        value_cache=torch.zeros(8, 16, 4, 128, dtype=torch.int8),
+        block_tables=torch.zeros(2, 4, dtype=torch.int32),
+        seq_lens=torch.ones(2, dtype=torch.int32),
+        k_scale=torch.ones(4),
+        v_scale=torch.ones(4),
+    )
+    a.update(over)
+    return a
+
+
+@pytest.mark.parametrize("bad", [
+    dict(query=torch.zeros(2, 28, 128, dtype=torch.int32)),
+    dict(key_cache=torch.zeros(8, 16, 4, 128, dtype=torch.bfloat16)),
+    dict(block_tables=torch.zeros(2, 4, dtype=torch.float32)),
+    dict(seq_lens=torch.ones(3, dtype=torch.int32)),
+    dict(k_scale=torch.ones(3)),
+    dict(query=torch.zeros(2, 30, 128, dtype=torch.bfloat16)),
+    dict(key_cache=torch.zeros(8, 16, 4, 64, dtype=torch.int8)),
+    dict(block_tables=torch.zeros(4, dtype=torch.int32)),
+])
+def test_int8_attention_validation_matches_reference(bad):
+    """Same AssertionError conditions as src/triton_ops/int8_paged_attention.py:698-719."""
+    with pytest.raises(AssertionError):
+        int8kv.int8_paged_attention(**_attn_args(**bad))
+
+
+def test_int8_attention_needs_gpu_tensors():
+    with pytest.raises(AssertionError, match="GPU"):
+        int8kv.int8_paged_attention(**_attn_args())
+
+
+def test_bf16_attention_needs_gpu_tensors():
+    a = _attn_args(key_cache=torch.zeros(8, 16, 4, 128, dtype=torch.bfloat16),
+                   value_cache=torch.zeros(8, 16, 4, 128, dtype=torch.bfloat16))
+    a.pop("k_scale")
+    a.pop("v_scale")
+    with pytest.raises(AssertionError, match="GPU"):
+        int8kv.bf16_paged_attention(**a)
+
+
+def test_write_validation_and_gpu_requirement():
+    k = torch.zeros(3, 4, 128, dtype=torch.bfloat16)
+    kc = torch.zeros(2, 16, 4, 128, dtype=torch.int8)
+    s = torch.ones(4)
+    slots = torch.zeros(3, dtype=torch.int64)
+    with pytest.raises(AssertionError):
+        int8kv.int8_kv_cache_write(k, k, kc.float(), kc, slots, s, s)
+    with pytest.raises(AssertionError):
+        int8kv.int8_kv_cache_write(k, k, kc, kc, slots[:2], s, s)
+    with pytest.raises(AssertionError):
+        int8kv.int8_kv_cache_write(k, k, kc, kc, slots.float(), s, s)
+    with pytest.raises(AssertionError, match="GPU"):
+        int8kv.int8_kv_cache_write(k, k, kc, kc, slots, s, s)
+
+
+def test_dequantize_debug_helper():
+    c = torch.tensor([[[[1, -2], [3, 4]]]], dtype=torch.int8)  # [1, 1, 2, 2]
+    out = int8kv.dequantize_paged_cache_for_debug(c, torch.tensor([0.5, 2.0]))
+    assert out.tolist() == [[[[0.5, -1.0], [6.0, 8.0]]]]
+
+
+def test_chunk_tokens_for_forced_splits():
+    assert _decode.chunk_tokens_for(2048, 16, None) == 0
+    assert _decode.chunk_tokens_for(2048, 16, 1) == 32768
+    assert _decode.chunk_tokens_for(2048, 16, 4) == 8192
+    assert _decode.chunk_tokens_for(3, 16, 4) == 32  # at least one 32-token tile
+    assert _decode.chunk_tokens_for(19, 16, 4) == 96  # 304 tokens / 4 -> 76 -> 96
+
+
+def test_synthetic_generators():
+    g = torch.Generator().manual_seed(0)
+    dist = syn.make_distribution(0)
+    k, v = syn.sample_kv(4096, dist, g)
+    assert k.dtype == torch.bfloat16 and k.shape == (4096, 4, 128)
+    # outlier channels are ~8x wider than the rest
+    std = k.float().std(dim=0)
+    for h in range(4):
+        mask = torch.zeros(128, dtype=torch.bool)
+        mask[dist.outlier_channels[h]] = True
+        assert std[h, mask].min() > 5 * std[h, ~mask].max()
+    assert abs(float(v.float().std()) - 0.5) < 0.02
+    ks, vs = syn.calibrate_scales(dist, seed=1)
+    assert ks.shape == (4,) and (ks > 0).all() and (vs > 0).all()
+    lens = [5, 16, 17]
+    bt = syn.random_block_tables(lens, 10, g)
+    assert bt.shape == (3, 2)
+    used = torch.cat([bt[0, :1], bt[1, :1], bt[2, :2]])
+    assert len(set(used.tolist())) == 4
+    slots = syn.slot_mapping_for(bt, lens)
+    assert slots.shape == (38,)
+    assert int(slots[21]) == int(bt[2, 0]) * 16 + 0 and int(slots[37]) == int(bt[2, 1]) * 16 + 0
+    r = syn.ragged_lengths(64, 32768, 3)
+    assert r.min() >= 1 and r.max() <= 32768
