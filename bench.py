@@ -1,0 +1,303 @@
+#!/usr/bin/env python3
+"""Headline benchmark: INT8 PagedAttention decode on one MI355X (the large ragged batch).
+
+Workload (the configuration the headline metric is quoted on): one decode step of one layer,
+Qwen2.5-7B attention shape (28 query heads, 4 kv heads, head_dim 128, 16-token cache blocks),
+B = 64 sequences with context lengths drawn uniformly from [1, 32768], block tables shuffled
+over a shared pool of ~65.6k physical blocks (~1.07 GB of int8 K+V).  Inputs are synthetic
+(seeded), written into the int8 cache by this library's own cache-write kernel, and resident
+in HBM before the timed region starts.
+
+A "step" is one int8_paged_attention call (decode kernel + split merge).  Reported:
+  * value: whole-call algorithmic HBM GB/s (K+V bytes once, block-table entries, q, out,
+    seq_lens, scales) over the measured step time;
+  * roofline: the decode kernel alone, timed per launch with HIP events on the launch stream,
+    against the 8 TB/s HBM peak; ``traffic`` comes from committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE counters when present;
+  * the same-kernel BF16 path on the same data (bf16 cache), for the INT8-vs-BF16 comparison;
+  * cpu_baseline: the CPU oracle (a numpy restatement of the reference's torch path) timed on a
+    bounded sample of the same sequences on this host, one thread.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (REPO, REPO / "int8-kvcache_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "INT8 paged decode attn µs/call + achieved HBM GB/s (% peak), B=64 ctx≤32k"
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = REPO / "profiles" / "decode_int8_cfg3_traffic.json"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_workload(dev, batch=64, max_len=32768, seed=0):
+    """Seeded cfg3 inputs on ``dev``: int8 + bf16 caches holding the same K/V, tables, lens."""
+    import torch
+
+    import int8kv
+    from int8kv import synthetic as syn
+
+    lens = syn.ragged_lengths(batch, max_len, seed + 2)
+    width = (max_len + 15) // 16
+    need = int(((lens + 15) // 16).sum())
+    num_blocks = need + 64
+    g_cpu = torch.Generator().manual_seed(seed + 2)
+    bt = syn.random_block_tables(lens.tolist(), num_blocks, g_cpu, width=width, fill=0)
+    slots = syn.slot_mapping_for(bt, lens.tolist())
+    dist = syn.make_distribution(seed)
+    ks, vs = syn.calibrate_scales(dist, seed=seed + 1)
+
+    kc = torch.zeros(num_blocks, 16, 4, 128, dtype=torch.int8, device=dev)
+    vc = torch.zeros_like(kc)
+    kc16 = torch.zeros(num_blocks, 16, 4, 128, dtype=torch.bfloat16, device=dev)
+    vc16 = torch.zeros_like(kc16)
+    ks_d, vs_d = ks.to(dev), vs.to(dev)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    slots_d = slots.to(dev)
+    step = 1 << 17
+    for s0 in range(0, slots.numel(), step):
+        sl = slots_d[s0:s0 + step]
+        k, v = syn.sample_kv(sl.numel(), dist, g, device=dev)
+        int8kv.int8_kv_cache_write(k, v, kc, vc, sl, ks_d, vs_d)
+        kc16.view(-1, 4, 128)[sl] = k
+        vc16.view(-1, 4, 128)[sl] = v
+    q = syn.sample_query(batch, torch.Generator().manual_seed(seed + 3)).to(dev)
+    torch.cuda.synchronize()
+    return dict(q=q, kc=kc, vc=vc, kc16=kc16, vc16=vc16, bt=bt.to(dev), sl=lens.to(torch.int32).to(dev),
+                ks=ks_d, vs=vs_d, lens=lens, bt_cpu=bt, num_blocks=num_blocks)
+
+
+def time_loop(fn, steps: int, warmup: int) -> float:
+    """ms per call of ``fn`` over ``steps`` back-to-back calls (synchronised on both sides)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def time_events(fn, steps: int, warmup: int) -> float:
+    """Average device duration (ms) of one ``fn`` launch: a HIP event pair around each launch,
+    recorded on torch's current stream, which is the stream the library launches on."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    pairs = []
+    for _ in range(steps):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        pairs.append((a, b))
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
+
+
+def cpu_baseline(w, out_gpu, budget_s: float = 20.0):
+    """Times the CPU oracle on the first sequences of the workload until ``budget_s`` elapses;
+    also reports the agreement of the GPU output with it on those sequences."""
+    import numpy as np
+
+    from oracle import int8kv_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    kc = w["kc"].cpu().numpy()
+    vc = w["vc"].cpu().numpy()
+    q = w["q"].float().cpu().numpy()
+    bt = w["bt_cpu"].numpy()
+    lens = w["lens"].numpy()
+    ks, vs = w["ks"].cpu().numpy(), w["vs"].cpu().numpy()
+    got = out_gpu.float().cpu().numpy()
+    ctx = threadpool_limits(limits=1) if threadpool_limits else None
+    done, t_total, nbytes = 0, 0.0, 0
+    worst, dots, n1, n2 = 0.0, 0.0, 0.0, 0.0
+    try:
+        if ctx:
+            ctx.__enter__()
+        for b in range(len(lens)):
+            t0 = time.perf_counter()
+            ref = O.paged_attention_ref(q[b:b + 1], kc, vc, bt[b:b + 1], lens[b:b + 1], ks, vs)
+            t_total += time.perf_counter() - t0
+            nbytes += O.decode_bytes(lens[b:b + 1], 4, 128, 1, 1, 28)
+            done += 1
+            d = got[b:b + 1].astype(np.float64)
+            r = ref.astype(np.float64)
+            worst = max(worst, float(np.abs(d - r).max()))
+            dots += float((d * r).sum())
+            n1 += float((d * d).sum())
+            n2 += float((r * r).sum())
+            if t_total >= budget_s:
+                break
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    cos = dots / math.sqrt(n1 * n2) if n1 > 0 and n2 > 0 else 0.0
+    tokens = int(lens[:done].sum())
+    return {
+        "value": round(nbytes / t_total / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"first {done} of {len(lens)} sequences ({tokens} tokens), numpy oracle "
+                  f"(gather, dequantise, fp32 softmax attention), {t_total:.1f} s",
+        "us_per_call_extrapolated": round(t_total / max(tokens, 1) * int(lens.sum()) * 1e6, 1),
+    }, {"sequences": done, "max_abs": worst, "cos": cos}
+
+
+def read_traffic():
+    """HBM bytes per decode launch from the committed rocprofv3 counter summary (or None)."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    try:
+        d = json.loads(TRAFFIC_FILE.read_text())
+        return int(d["traffic_bytes_per_launch"])
+    except (ValueError, KeyError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-budget", type=float, default=20.0,
+                    help="seconds of CPU-oracle work for the cpu_baseline sample")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: the decode op has no multi-GPU path in this build "
+              "(sequences and kv heads shard across GPUs without any exchange); run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    import int8kv
+    from int8kv import _decode, _lib
+    from oracle import int8kv_oracle as O
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    _lib.load()
+    dev = torch.device("cuda:0")
+    log("building workload (B=64, ctx ~ U[1, 32768]) ...")
+    w = build_workload(dev, seed=args.seed)
+    lens = w["lens"]
+    nbytes8 = O.decode_bytes(lens.numpy(), 4, 128, 1, 64, 28)
+    nbytes16 = O.decode_bytes(lens.numpy(), 4, 128, 2, 64, 28)
+    log(f"tokens={int(lens.sum())} blocks={w['num_blocks']} int8 bytes/call={nbytes8}")
+
+    def int8_call():
+        return int8kv.int8_paged_attention(w["q"], w["kc"], w["vc"], w["bt"], w["sl"], w["ks"], w["vs"])
+
+    def bf16_call():
+        return int8kv.bf16_paged_attention(w["q"], w["kc16"], w["vc16"], w["bt"], w["sl"])
+
+    # Decode kernel alone (no merge), same arguments as int8_call, workspace preallocated.
+    chunk = 0
+    need = _lib.load().int8kv_decode_workspace_bytes(64, 28, 4, 128, w["bt"].shape[1], 16, chunk)
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    out_main = torch.empty_like(w["q"])
+
+    def main_kernel():
+        _decode.paged_decode(w["q"], w["kc"], w["vc"], w["bt"], w["sl"], w["ks"], w["vs"], out_main,
+                             chunk, _lib.DECODE_MAIN, ws)
+
+    def merge_kernel():
+        _decode.paged_decode(w["q"], w["kc"], w["vc"], w["bt"], w["sl"], w["ks"], w["vs"], out_main,
+                             chunk, _lib.DECODE_MERGE, ws)
+
+    out = int8_call()
+    torch.cuda.synchronize()
+    ms = time_loop(int8_call, args.steps, args.warmup)
+    ms_main = time_events(main_kernel, args.steps, args.warmup)
+    ms_merge = time_events(merge_kernel, args.steps, args.warmup)
+    ms16 = time_loop(bf16_call, args.steps, args.warmup)
+    ms16_main = None
+    value = nbytes8 / (ms * 1e-3) / 1e9
+    achieved = nbytes8 / (ms_main * 1e-3) / 1e9
+    log(f"int8 op: {ms * 1e3:.1f} us/call ({value:.0f} GB/s); decode kernel {ms_main * 1e3:.1f} us "
+        f"({achieved:.0f} GB/s); merge kernel {ms_merge * 1e3:.1f} us; bf16 op {ms16 * 1e3:.1f} us "
+        f"({nbytes16 / (ms16 * 1e-3) / 1e9:.0f} GB/s)")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded Qwen2.5-7B-shaped K/V with outlier channels; no checkpoint)",
+        "config": {
+            "workload": "cfg3: one-layer INT8 paged decode, B=64, ctx ~ U[1,32768] ragged, "
+                        "28q/4kv heads, head_dim 128, block 16, shuffled block pool",
+            "batch": 64,
+            "tokens": int(lens.sum()),
+            "max_ctx": int(lens.max()),
+            "algorithmic_bytes_per_call": int(nbytes8),
+            "us_per_call": round(ms * 1e3, 2),
+            "bf16_us_per_call": round(ms16 * 1e3, 2),
+            "bf16_algorithmic_bytes_per_call": int(nbytes16),
+            "int8_speedup_vs_bf16": round(ms16 / ms, 3),
+            "decode_kernel_us": round(ms_main * 1e3, 2),
+            "merge_kernel_us": round(ms_merge * 1e3, 2),
+            "frac_of_hbm_peak_whole_call": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": read_traffic(),
+            "kernel": "decode_kernel<int8 cache, bf16 query>",
+        },
+        "cpu_baseline": None,
+    }
+    del ms16_main
+    if not args.no_cpu:
+        log("cpu baseline (numpy oracle, 1 thread) ...")
+        cb, check = cpu_baseline(w, out, args.cpu_budget)
+        result["cpu_baseline"] = cb
+        result["config"]["gpu_vs_oracle_on_sample"] = {
+            "sequences": check["sequences"], "max_abs": round(check["max_abs"], 6),
+            "cos": round(check["cos"], 7)}
+        log(f"cpu baseline {cb['value']} GB/s; GPU vs oracle on sample: {check}")
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
