@@ -222,7 +222,7 @@ def main() -> int:
 
     # Decode kernel alone (no merge), same arguments as int8_call, workspace preallocated.
     chunk = 0
-    need = _lib.load().int8kv_decode_workspace_bytes(64, 28, 4, 128, w["bt"].shape[1], 16, chunk)
+    need = _lib.load().int8kv_decode_workspace_bytes(28, 4, 128, 16, chunk)
     ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
     out_main = torch.empty_like(w["q"])
 

@@ -4,7 +4,8 @@
  * Two hot operations of a static per-head symmetric INT8 KV cache:
  *   1. the paged cache write (slot_mapping scatter, RNE quantisation, clamp to [-127, 127]);
  *   2. PagedAttention decode over an INT8 cache (or a 16-bit cache, same kernel family),
- *      split over fixed-size token chunks with online-softmax partials and a merge pass.
+ *      split over equal ranges of the batch's token stream with online-softmax partials and a
+ *      merge pass.
  *
  * Conventions shared by every entry point:
  *   - All pointers are device pointers except the `*_strides` arrays, which are host arrays.
@@ -22,6 +23,8 @@
  *                           src/triton_ops/bf16_paged_attention.py:118-165 (bf16_paged_attention)
  *   int8kv_decode_workspace_bytes <- the partial-buffer allocation of
  *                           src/triton_ops/int8_paged_attention.py:594-603
+ *   int8kv_decode_auto_ranges <- the split-count heuristic _choose_num_splits,
+ *                           src/triton_ops/int8_paged_attention.py:39-49
  */
 #ifndef INT8KV_H
 #define INT8KV_H
@@ -52,7 +55,7 @@ enum int8kv_dtype {
 #define INT8KV_E_WORKSPACE (-5) /* workspace missing or smaller than required */
 
 /* Flags of int8kv_paged_decode. */
-#define INT8KV_DECODE_MAIN 1u   /* run the chunked decode kernel */
+#define INT8KV_DECODE_MAIN 1u   /* run the range decode kernel */
 #define INT8KV_DECODE_MERGE 2u  /* run the split merge kernel */
 #define INT8KV_DECODE_ALL 3u
 
@@ -82,20 +85,21 @@ int int8kv_cache_write(const void* key, const void* value, int src_dtype, int64_
                        int slot_dtype, const float* k_scale, const float* v_scale, void* stream);
 
 /*
- * Bytes of device workspace int8kv_paged_decode needs for these sizes (the split partials:
- * one running max, one running sum and one head_dim accumulator per chunk and query head).
- * chunk_tokens is the value that will be passed to int8kv_paged_decode (0 = automatic).
- * Returns 0 for sizes int8kv_paged_decode would reject.
+ * Automatic range count of int8kv_paged_decode (num_ranges = 0) on the current device: the
+ * token stream of a decode call is cut into this many equal ranges per kv head, a few
+ * workgroups per compute unit.
  */
-size_t int8kv_decode_workspace_bytes(int64_t batch, int32_t num_q_heads, int32_t num_kv_heads,
-                                     int32_t head_dim, int64_t table_width, int32_t block_size,
-                                     int32_t chunk_tokens);
+int32_t int8kv_decode_auto_ranges(int32_t num_kv_heads);
 
 /*
- * The chunk size in tokens int8kv_paged_decode uses for these sizes when chunk_tokens = 0.
+ * Bytes of device workspace int8kv_paged_decode needs (the split partials: one running max,
+ * one running sum and one head_dim accumulator per range, slot and query head); independent of
+ * the batch, the context lengths and the block-table width.  num_ranges is the value that will
+ * be passed to int8kv_paged_decode (0 = automatic, for the current device).  Returns 0 for
+ * sizes int8kv_paged_decode would reject.
  */
-int32_t int8kv_decode_auto_chunk_tokens(int64_t batch, int32_t num_kv_heads, int64_t table_width,
-                                        int32_t block_size);
+size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t block_size, int32_t num_ranges);
 
 /*
  * Paged decode attention, one query token per sequence, GQA group = num_q_heads / num_kv_heads
@@ -116,11 +120,16 @@ int32_t int8kv_decode_auto_chunk_tokens(int64_t batch, int32_t num_kv_heads, int
  *                 into range so that every access stays inside the caches).
  *   seq_lens:     [batch] of seq_lens_dtype (I32 or I64), contiguous.
  *   k_scale/v_scale: fp32 [num_kv_heads] for an I8 cache; ignored (may be NULL) otherwise.
- *   out:          [batch, num_q_heads, head_dim] of query_dtype, innermost stride 1.
+ *   out:          [batch, num_q_heads, head_dim] of query_dtype, innermost stride 1, rows
+ *                 16-byte aligned.
  *   workspace:    at least int8kv_decode_workspace_bytes(...) bytes, 16-byte aligned; it needs
- *                 no initialisation and may be NULL when that size is 0.
- *   chunk_tokens: tokens per work item (a multiple of 32, or 0 = automatic).  A sequence
- *                 longer than one chunk is merged by the split merge kernel.
+ *                 no initialisation.
+ *   num_ranges:   the 32-token tiles of all sequences form one stream per kv head, cut into
+ *                 P = min(num_ranges, ceil(tiles / min_tiles)) equal ranges, one workgroup
+ *                 each; a sequence cut by range bounds is combined by the merge kernel.
+ *                 0 = automatic (int8kv_decode_auto_ranges).  num_ranges = batch gives one
+ *                 range per sequence when all lengths are equal (a single pass).
+ *   min_tiles:    smallest range in tiles (0 = automatic, 2).
  *   flags:        INT8KV_DECODE_ALL normally; MAIN and MERGE separately let a caller time the
  *                 two kernels on their own (MERGE must follow MAIN with identical arguments).
  *
@@ -136,7 +145,7 @@ int int8kv_paged_decode(const void* query, int query_dtype, int64_t batch, int32
                         const int64_t table_strides[2], const void* seq_lens, int seq_lens_dtype,
                         const float* k_scale, const float* v_scale, float sm_scale, void* out,
                         const int64_t out_strides[3], void* workspace, size_t workspace_bytes,
-                        int32_t chunk_tokens, uint32_t flags, void* stream);
+                        int32_t num_ranges, int32_t min_tiles, uint32_t flags, void* stream);
 
 /* Library version string, e.g. "int8kv 0.1.0 gfx950". */
 const char* int8kv_version(void);

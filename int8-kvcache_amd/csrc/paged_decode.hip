@@ -7,33 +7,40 @@
 // weights times v_t * v_scale, with v_scale applied once at the end (:291-292).
 //
 // Work decomposition (MI355X-first, not the reference's grid):
-//   * A work item is (sequence b, kv head g, chunk c of chunk_tokens tokens); the grid is
-//     (max_chunks, num_kv_heads, batch) and items past the end of a sequence exit at once, so
-//     ragged batches are balanced without reading seq_lens on the host.
-//   * A workgroup is 4 waves; wave w takes the 32-token tiles w, w+4, ... of its chunk.  A tile
-//     is two 16-token cache blocks of one kv head.  All query heads of the GQA group are
-//     processed together on the matrix cores, so every K/V byte is read from HBM once.
-//   * Per tile and wave:  S^T = K * Q^T  (2 x 4 MFMA 16x16x32; rows = tokens, cols = heads),
-//     online softmax in the exp2 domain, then out^T += V^T * P^T (8 MFMA 16x16x32; rows =
-//     head_dim, cols = heads).  The MFMA accumulator layout puts one head per lane column,
-//     so the probabilities never leave registers.
+//   * Every sequence is cut into 32-token tiles; the tiles of all sequences, in batch order,
+//     form one stream of T tiles per kv head.  The stream is divided into P equal contiguous
+//     ranges (P = a few workgroups per CU), so a ragged batch costs every workgroup the same
+//     number of tiles (+-1) whatever the length distribution.  T and the range bounds are
+//     computed on the device from seq_lens; the host never reads them.
+//   * A workgroup owns one range for W kv heads, one wave per kv head.  The W waves read the
+//     same cache blocks (their head slices of the same 16-token rows) at the same time.  A wave
+//     handles all query heads of its GQA group on the matrix cores, so every K/V byte is read
+//     from HBM exactly once, and needs no LDS and no barrier.
+//   * A sequence wholly inside one range is finished by that wave (output written directly).
+//     A sequence cut by range bounds leaves (max, sum, accumulator) partials in the workspace,
+//     at most two per range and head; merge_kernel combines them.
+//   * Per 32-token tile and wave:  S^T = K * Q^T  (2 x 4 MFMA 16x16x32; rows = tokens, cols =
+//     heads), online softmax in the exp2 domain, then out^T += V^T * P^T (8 MFMA 16x16x32;
+//     rows = head_dim, cols = heads).  The MFMA accumulator layout puts one head per lane
+//     column, so the probabilities never leave registers.  The next tile's loads are in flight
+//     while a tile is computed; block-table entries are read 64 at a time into one register
+//     (one lane per block) ahead of use, so no table read sits on the tile critical path.
 //   * INT8 K/V are dequantised in registers to fp16 with the exact magic-number conversion
-//     (0x6400 | (x ^ 0x80)) - 1152 = x, two elements per v_pk_add_f16; the per-head k_scale and
-//     sm_scale * log2(e) are folded into Q once per work item, v_scale into the final output.
+//     (0x6400 | (x ^ 0x80)) - 1152 = x, two elements per v_pk_add_f16.  Q is scaled by a power
+//     of two into the upper fp16 range (exact for bf16 input); k_scale * sm_scale * log2(e) and
+//     that power of two are applied to the fp32 scores, v_scale to the final output.
 //   * A running max is only moved when a tile's max exceeds it by more than 8 (log2 units), so
 //     most tiles skip the accumulator rescale; probabilities are then <= 2^8 (fits fp16/bf16).
-//   * The 4 waves merge through LDS; a sequence that spans more than one chunk writes
-//     (max, sum, accumulator) partials which merge_kernel combines.
 
 #include "int8kv_common.h"
 
 namespace int8kv {
 
 constexpr int kHeadDim = 128;
-constexpr int kBlock = 16;     // tokens per cache block
-constexpr int kTile = 32;      // tokens per wave iteration
-constexpr int kWaves = 4;      // waves per workgroup
-constexpr int kMaxGroup = 16;  // query heads per kv head (MFMA column count)
+constexpr int kBlock = 16;          // tokens per cache block
+constexpr int kTile = 32;           // tokens per wave iteration
+constexpr int kMaxGroup = 16;       // query heads per kv head (MFMA column count)
+constexpr int kWindowTiles = 32;    // tiles covered by one 64-entry block-table window
 constexpr float kLazyRescale = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -51,20 +58,78 @@ struct DecodeArgs {
   const float* v_scale;
   char* out;
   int64_t o_sb, o_sh;  // element strides
-  float* ws_acc;
-  float* ws_m;
-  float* ws_l;
+  float* ws_acc;       // [max_ranges * 2][num_q_heads][kHeadDim]
+  float* ws_m;         // [max_ranges * 2][num_q_heads]
+  float* ws_l;         // [max_ranges * 2][num_q_heads]
   int64_t num_blocks;
+  int64_t batch;
   int32_t num_kv_heads;
+  int32_t num_q_heads;
   int32_t group;
-  int32_t width;        // block-table width in blocks
-  int32_t chunk_tiles;  // 32-token tiles per work item
-  int32_t max_chunks;
+  int32_t width;       // block-table width in blocks
+  int32_t max_ranges;  // P upper bound (= grid.x of decode_kernel)
+  int32_t min_tiles;   // P <= ceil(T / min_tiles)
   int32_t bt_is64;
   int32_t sl_is64;
   float sm_scale_log2e;
 };
 
+// ------------------------------------------------------------------------ wave utilities
+__device__ __forceinline__ int64_t wave_sum(int64_t x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+__device__ __forceinline__ int64_t wave_inclusive_scan(int64_t x, int lane) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int64_t y = __shfl_up(x, (unsigned)o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+__device__ __forceinline__ int64_t readlane64(int64_t x, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)x >> 32), lane);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// ------------------------------------------------------------------------ work plan
+// Sequence b's token count L_b = clamp(seq_lens[b], 0, width * 16) and tile count
+// n_b = ceil(L_b / 32); T = sum_b n_b; P = clamp(ceil(T / min_tiles), 1, max_ranges);
+// range r covers stream tiles [r * T / P, (r + 1) * T / P).
+__device__ __forceinline__ int64_t seq_len_of(const DecodeArgs& a, int64_t b) {
+  if (b >= a.batch) return 0;
+  int64_t L = load_index(a.sl, b, a.sl_is64);
+  const int64_t cap = (int64_t)a.width * kBlock;
+  return L < 0 ? 0 : (L > cap ? cap : L);
+}
+
+__device__ __forceinline__ int64_t tiles_of(int64_t L) { return (L + kTile - 1) / kTile; }
+
+struct Plan {
+  int64_t T;
+  int64_t P;
+};
+
+__device__ __forceinline__ Plan make_plan(const DecodeArgs& a, int lane) {
+  int64_t T = 0;
+  for (int64_t base = 0; base < a.batch; base += kWave) T += wave_sum(tiles_of(seq_len_of(a, base + lane)));
+  int64_t P = (T + a.min_tiles - 1) / a.min_tiles;
+  P = P < 1 ? 1 : (P > a.max_ranges ? a.max_ranges : P);
+  return {T, P};
+}
+
+__device__ __forceinline__ int64_t range_start(const Plan& p, int64_t r) { return r * p.T / p.P; }
+
+// The range holding stream tile x (0 <= x < T): the largest r with range_start(r) <= x.
+__device__ __forceinline__ int64_t range_of(const Plan& p, int64_t x) {
+  return ((x + 1) * p.P - 1) / p.T;
+}
+
+// ------------------------------------------------------------------------ tile registers
 // Registers holding one 32-token tile of K and V for one lane.
 //   K: lane (i = lane % 16, g = lane / 16) holds token i of block s, head_dim elements
 //      [32g, 32g + 32).
@@ -130,19 +195,28 @@ __device__ __forceinline__ f16x8 i8x8_to_f16(uint32_t d0, uint32_t d1) {
 }
 
 template <int DT>
-__device__ __forceinline__ void store_out(char* p, float x) {
-  if constexpr (DT == kF32) {
-    *reinterpret_cast<float*>(p) = x;
-  } else if constexpr (DT == kF16) {
-    *reinterpret_cast<_Float16*>(p) = (_Float16)x;
-  } else {
-    *reinterpret_cast<__bf16*>(p) = (__bf16)x;
-  }
-}
-
-template <int DT>
 constexpr int esize() {
   return DT == kF32 ? 4 : (DT == kI8 ? 1 : 2);
+}
+
+// Stores 8 consecutive fp32 values as DT (16-byte aligned destination).
+template <int DT>
+__device__ __forceinline__ void store8(char* p, const float (&x)[8]) {
+  if constexpr (DT == kF32) {
+    f32x4* q = reinterpret_cast<f32x4*>(p);
+    q[0] = f32x4{x[0], x[1], x[2], x[3]};
+    q[1] = f32x4{x[4], x[5], x[6], x[7]};
+  } else if constexpr (DT == kF16) {
+    f16x8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = (_Float16)x[i];
+    *reinterpret_cast<f16x8*>(p) = h;
+  } else {
+    bf16x8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = (__bf16)x[i];
+    *reinterpret_cast<bf16x8*>(p) = h;
+  }
 }
 
 template <int CACHE>
@@ -291,60 +365,79 @@ __device__ __forceinline__ void compute_tile(RawTile<CACHE>& r,
   }
 }
 
+// Q^T operand of one wave: lane (head li, group lg) holds q[li][32lg + 8ks + e].  Returns the
+// fp32 factor that turns the MFMA scores into log2-domain logits.
 template <int CACHE, int QT>
-__global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
-  typedef typename MfmaOp<CACHE>::T OpT;
-  __shared__ float s_acc[kWaves][kMaxGroup][kHeadDim];
-  __shared__ float s_m[kWaves][kMaxGroup];
-  __shared__ float s_l[kWaves][kMaxGroup];
-
-  const int c = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
-  const int G = a.group;
-
-  int64_t L = load_index(a.sl, b, a.sl_is64);
-  const int64_t cap = (int64_t)a.width * kBlock;
-  L = L < 0 ? 0 : (L > cap ? cap : L);
-  const int64_t CT = (int64_t)a.chunk_tiles * kTile;
-  const int64_t nchunks = L > CT ? (L + CT - 1) / CT : 1;
-  if (c >= nchunks) return;
-
-  const int64_t tok0 = (int64_t)c * CT;
-  const int64_t tok1 = (tok0 + CT < L) ? tok0 + CT : L;
-  const int ntiles = tok1 > tok0 ? (int)((tok1 - tok0 + kTile - 1) / kTile) : 0;
-  const int64_t nblk = (L + kBlock - 1) / kBlock;
-
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int lane = threadIdx.x % kWave;
-  const int li = lane & 15;
-  const int lg = lane >> 4;
-
-  // ---- Q^T operand: lane (head li, group lg) holds q[li][32lg + 8ks + e] ----
-  float qscale = 1.0f;
-  float s_scale = a.sm_scale_log2e;
-  if constexpr (CACHE == kI8) {
-    qscale = fmaxf(a.k_scale[kvh], 1e-6f) * a.sm_scale_log2e;
-    s_scale = 1.0f;
-  }
-  OpT qop[4];
-  if (li < G) {
-    constexpr int QE = esize<QT>();
-    const char* qp = a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * G + li) * a.q_sh + 32 * lg) * QE;
+__device__ __forceinline__ float load_query(const DecodeArgs& a, int64_t b, int kvh, int li,
+                                            int lg, typename MfmaOp<CACHE>::T (&qop)[4]) {
+  constexpr int QE = esize<QT>();
+  float x[4][8];
+  float amax = 0.0f;
+  if (li < a.group) {
+    const char* qp =
+        a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh + 32 * lg) * QE;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      float x[8];
-      load8_f32<QT>(qp + 8 * ks * QE, x);
+      load8_f32<QT>(qp + 8 * ks * QE, x[ks]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        qop[ks][e] = (typename MfmaOp<CACHE>::E)(x[e] * qscale);
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[ks][e]));
     }
   } else {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qop[ks][e] = 0;
+      for (int e = 0; e < 8; ++e) x[ks][e] = 0.0f;
   }
+  float s_scale = a.sm_scale_log2e;
+  if constexpr (CACHE == kI8) s_scale *= fmaxf(a.k_scale[kvh], 1e-6f);
+  float qmul = 1.0f;
+  if constexpr (CACHE != kBF16) {
+    // fp16 operands: scale q by 2^e so that the largest |q| of the wave lands in [2^14, 2^15).
+    // A power of two is exact, and the range of fp16 is never exceeded.
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    amax = fmaxf(amax, __shfl_xor(amax, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    if (amax > 0.0f && amax < INFINITY) {
+      const int e = 14 - ilogbf(amax);
+      qmul = ldexpf(1.0f, e);
+      s_scale = ldexpf(s_scale, -e);
+    }
+  }
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qop[ks][e] = (typename MfmaOp<CACHE>::E)(x[ks][e] * qmul);
+  return s_scale;
+}
+
+// Physical block ids of blocks [first, first + 64) of row b, one per lane (0 past the
+// sequence's last block, clamped into [0, num_blocks) so every access stays in the caches).
+__device__ __forceinline__ int32_t load_window(const DecodeArgs& a, int64_t b, int64_t first,
+                                               int64_t nblk, int lane) {
+  const int64_t blk = first + lane;
+  if (blk >= nblk) return 0;
+  int64_t p = load_index(a.bt, b * a.bt_sb + blk * a.bt_sl, a.bt_is64);
+  const int64_t hi = a.num_blocks - 1;
+  p = p < 0 ? 0 : (p > hi ? hi : p);
+  return (int32_t)p;
+}
+
+// Processes tiles [ta, tb) of sequence b (length L) for kv head kvh with one wave, then writes
+// either the final output (full == true) or a partial record.
+template <int CACHE, int QT>
+__device__ __forceinline__ void run_segment(const DecodeArgs& a, int64_t b, int64_t L, int kvh,
+                                            int64_t ta, int64_t tb, bool full, int64_t rec,
+                                            int lane) {
+  typedef typename MfmaOp<CACHE>::T OpT;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int G = a.group;
+
+  OpT qop[4];
+  const float s_scale = load_query<CACHE, QT>(a, b, kvh, li, lg, qop);
 
   f32x4 acc[8];
 #pragma unroll
@@ -354,117 +447,174 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
 
   const char* kb = a.kc + (int64_t)kvh * a.kc_sh;
   const char* vb = a.vc + (int64_t)kvh * a.vc_sh;
-  const int64_t bt_row = (int64_t)b * a.bt_sb;
-  const int64_t nb_max = a.num_blocks - 1;
+  const int64_t nblk = (L + kBlock - 1) / kBlock;
 
-  auto phys = [&](int64_t lb) -> int64_t {
-    int64_t p = load_index(a.bt, bt_row + lb * a.bt_sl, a.bt_is64);
-    return p < 0 ? 0 : (p > nb_max ? nb_max : p);
-  };
-  auto load = [&](RawTile<CACHE>& r, int t) {
-    const int64_t lb0 = (tok0 + (int64_t)t * kTile) / kBlock;
-    const int64_t p0 = phys(lb0);
-    const int64_t p1 = (lb0 + 1 < nblk) ? phys(lb0 + 1) : p0;
+  int64_t wbase = ta;  // first tile of the current table window
+  int32_t tbl = load_window(a, b, 2 * wbase, nblk, lane);
+  int32_t tbl_next = load_window(a, b, 2 * (wbase + kWindowTiles), nblk, lane);
+
+  auto issue = [&](RawTile<CACHE>& r, int64_t t) {
+    int rel = (int)(t - wbase);
+    if (rel >= kWindowTiles) {
+      wbase += kWindowTiles;
+      rel -= kWindowTiles;
+      tbl = tbl_next;
+      tbl_next = load_window(a, b, 2 * (wbase + kWindowTiles), nblk, lane);
+    }
+    const int64_t p0 = __builtin_amdgcn_readlane(tbl, 2 * rel);
+    const int64_t p1 = __builtin_amdgcn_readlane(tbl, 2 * rel + 1);
     issue_tile_loads<CACHE>(r, kb, vb, p0, p1, a, li, lg);
   };
-  auto valid_of = [&](int t) -> int {
-    const int64_t v = tok1 - (tok0 + (int64_t)t * kTile);
+  auto valid_of = [&](int64_t t) -> int {
+    const int64_t v = L - t * kTile;
     return v >= kTile ? kTile : (int)v;
   };
 
   // Two register buffers: the next tile's loads are in flight while this one is computed.
   RawTile<CACHE> r0, r1;
-  int t = wave;
-  if (t < ntiles) load(r0, t);
-  while (t < ntiles) {
-    int tn = t + kWaves;
-    if (tn < ntiles) load(r1, tn);
+  int64_t t = ta;
+  issue(r0, t);
+  while (true) {
+    if (t + 1 < tb) issue(r1, t + 1);
     compute_tile<CACHE>(r0, qop, acc, m_run, l_part, valid_of(t), lg, s_scale);
-    t = tn;
-    if (t >= ntiles) break;
-    tn = t + kWaves;
-    if (tn < ntiles) load(r0, tn);
+    if (++t >= tb) break;
+    if (t + 1 < tb) issue(r0, t + 1);
     compute_tile<CACHE>(r1, qop, acc, m_run, l_part, valid_of(t), lg, s_scale);
-    t = tn;
+    if (++t >= tb) break;
   }
 
-  // ---- merge the 4 waves through LDS ----
   l_part += __shfl_xor(l_part, 16);
   l_part += __shfl_xor(l_part, 32);
-  if (li < G) {
+  if (li >= G) return;
+  const int h = kvh * G + li;
+  if (full) {
+    const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
+    const float inv = l_part > 0.0f ? vscale / l_part : 0.0f;
+    char* op = a.out + (b * a.o_sb + (int64_t)h * a.o_sh) * esize<QT>();
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
+    for (int rr = 0; rr < 4; ++rr) {
+      float o[8];
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) s_acc[wave][li][32 * lg + 8 * rr + dt] = acc[dt][rr];
+      for (int dt = 0; dt < 8; ++dt) o[dt] = acc[dt][rr] * inv;
+      store8<QT>(op + (32 * lg + 8 * rr) * esize<QT>(), o);
+    }
+  } else {
+    const int64_t row = rec * a.num_q_heads + h;
+    char* pp = reinterpret_cast<char*>(a.ws_acc + row * kHeadDim);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      float o[8];
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[dt] = acc[dt][rr];
+      store8<kF32>(pp + (32 * lg + 8 * rr) * 4, o);
+    }
     if (lg == 0) {
-      s_m[wave][li] = m_run;
-      s_l[wave][li] = l_part;
-    }
-  }
-  __syncthreads();
-
-  const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
-  const bool single = nchunks == 1;
-  const int64_t item = ((int64_t)b * a.num_kv_heads + kvh) * a.max_chunks + c;
-  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += kWaves * kWave) {
-    const int j = idx / kHeadDim;
-    const int d = idx % kHeadDim;
-    float M = s_m[0][j];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w][j]);
-    float Ls = 0.0f, O = 0.0f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float wt = exp2_fast(s_m[w][j] - M);
-        Ls += wt * s_l[w][j];
-        O += wt * s_acc[w][j][d];
-      }
-    }
-    if (single) {
-      const float o = Ls > 0.0f ? O * vscale / Ls : 0.0f;
-      store_out<QT>(a.out + ((int64_t)b * a.o_sb + (int64_t)(kvh * G + j) * a.o_sh + d) *
-                                esize<QT>(),
-                    o);
-    } else {
-      a.ws_acc[(item * G + j) * kHeadDim + d] = O;
-      if (d == 0) {
-        a.ws_m[item * G + j] = M;
-        a.ws_l[item * G + j] = Ls;
-      }
+      a.ws_m[row] = m_run;
+      a.ws_l[row] = l_part;
     }
   }
 }
 
-// Merges the chunk partials of every sequence that spans more than one chunk.
-// grid (num_q_heads, batch), 128 threads (one per head_dim element).
+// grid (max_ranges, num_kv_heads / W), block W waves; wave w of workgroup (r, y) handles
+// kv head y * W + w over stream range r.
+template <int CACHE, int QT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(DecodeArgs a) {
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int kvh = blockIdx.y * (blockDim.x / kWave) + wave;
+  const int64_t r = blockIdx.x;
+
+  const Plan plan = make_plan(a, lane);
+  if (r >= plan.P) return;
+  const int64_t t0 = range_start(plan, r);
+  const int64_t t1 = range_start(plan, r + 1);
+
+  int64_t cum = 0;  // tiles of the sequences before this 64-sequence chunk
+  for (int64_t base = 0; base < a.batch; base += kWave) {
+    const int64_t L = seq_len_of(a, base + lane);
+    const int64_t n = tiles_of(L);
+    const int64_t incl = wave_inclusive_scan(n, lane) + cum;
+    const int64_t excl = incl - n;
+    const int64_t chunk_end = readlane64(incl, kWave - 1);
+    if (chunk_end > t0) {
+      uint64_t mask = __ballot(n > 0 && incl > t0 && excl < t1);
+      while (mask) {
+        const int j = __builtin_ctzll(mask);
+        mask &= mask - 1;
+        const int64_t S = readlane64(excl, j);
+        const int64_t nb = readlane64(n, j);
+        const int64_t Lb = readlane64(L, j);
+        const int64_t ta = (t0 > S ? t0 : S) - S;
+        const int64_t te = (t1 < S + nb ? t1 : S + nb) - S;
+        const bool full = ta == 0 && te == nb;
+        const int64_t slot = (S + ta == t0) ? 0 : 1;
+        run_segment<CACHE, QT>(a, base + j, Lb, kvh, ta, te, full, 2 * r + slot, lane);
+      }
+    }
+    if (chunk_end >= t1) break;
+    cum = chunk_end;
+  }
+}
+
+// Combines the partials of every sequence cut by range bounds and writes zeros for empty
+// sequences.  grid (batch, num_kv_heads), 128 threads (one per head_dim element).
 template <int CACHE, int QT>
 __global__ __launch_bounds__(128) void merge_kernel(DecodeArgs a) {
-  const int h = blockIdx.x;
-  const int b = blockIdx.y;
-  const int G = a.group;
-  const int kvh = h / G;
-  const int j = h % G;
-  int64_t L = load_index(a.sl, b, a.sl_is64);
-  const int64_t cap = (int64_t)a.width * kBlock;
-  L = L < 0 ? 0 : (L > cap ? cap : L);
-  const int64_t CT = (int64_t)a.chunk_tiles * kTile;
-  const int64_t nchunks = L > CT ? (L + CT - 1) / CT : 1;
-  if (nchunks <= 1) return;
+  const int64_t b = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int lane = threadIdx.x % kWave;
   const int d = threadIdx.x;
-  const int64_t item0 = ((int64_t)b * a.num_kv_heads + kvh) * a.max_chunks;
-  float M = -INFINITY;
-  for (int64_t c = 0; c < nchunks; ++c) M = fmaxf(M, a.ws_m[(item0 + c) * G + j]);
-  float Ls = 0.0f, O = 0.0f;
-  for (int64_t c = 0; c < nchunks; ++c) {
-    const int64_t row = (item0 + c) * G + j;
-    const float wt = exp2_fast(a.ws_m[row] - M);
-    Ls += wt * a.ws_l[row];
-    O += wt * a.ws_acc[row * kHeadDim + d];
+  const int G = a.group;
+
+  const Plan plan = make_plan(a, lane);
+  int64_t S = 0;  // stream tiles before sequence b
+  for (int64_t base = 0; base < b; base += kWave) {
+    const int64_t bb = base + lane;
+    S += wave_sum(bb < b ? tiles_of(seq_len_of(a, bb)) : 0);
   }
+  const int64_t n = tiles_of(seq_len_of(a, b));
+  char* ob = a.out + (b * a.o_sb + (int64_t)(kvh * G) * a.o_sh + d) * esize<QT>();
+  if (n == 0) {
+    for (int j = 0; j < G; ++j) {
+      const float z[1] = {0.0f};
+      if constexpr (QT == kF32) {
+        *reinterpret_cast<float*>(ob + j * a.o_sh * 4) = z[0];
+      } else if constexpr (QT == kF16) {
+        *reinterpret_cast<_Float16*>(ob + j * a.o_sh * 2) = (_Float16)z[0];
+      } else {
+        *reinterpret_cast<__bf16*>(ob + j * a.o_sh * 2) = (__bf16)z[0];
+      }
+    }
+    return;
+  }
+  const int64_t r0 = range_of(plan, S);
+  const int64_t r1 = range_of(plan, S + n - 1);
+  if (r0 == r1) return;  // finished inside one range by decode_kernel
+  const int64_t slot0 = range_start(plan, r0) == S ? 0 : 1;
   const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
-  const float o = Ls > 0.0f ? O * vscale / Ls : 0.0f;
-  store_out<QT>(a.out + ((int64_t)b * a.o_sb + (int64_t)h * a.o_sh + d) * esize<QT>(), o);
+  for (int j = 0; j < G; ++j) {
+    const int h = kvh * G + j;
+    float M = -INFINITY;
+    for (int64_t r = r0; r <= r1; ++r) {
+      const int64_t rec = 2 * r + (r == r0 ? slot0 : 0);
+      M = fmaxf(M, a.ws_m[rec * a.num_q_heads + h]);
+    }
+    float Ls = 0.0f, O = 0.0f;
+    for (int64_t r = r0; r <= r1; ++r) {
+      const int64_t row = (2 * r + (r == r0 ? slot0 : 0)) * a.num_q_heads + h;
+      const float wt = exp2_fast(a.ws_m[row] - M);
+      Ls += wt * a.ws_l[row];
+      O += wt * a.ws_acc[row * kHeadDim + d];
+    }
+    const float o = Ls > 0.0f ? O * vscale / Ls : 0.0f;
+    if constexpr (QT == kF32) {
+      *reinterpret_cast<float*>(ob + j * a.o_sh * 4) = o;
+    } else if constexpr (QT == kF16) {
+      *reinterpret_cast<_Float16*>(ob + j * a.o_sh * 2) = (_Float16)o;
+    } else {
+      *reinterpret_cast<__bf16*>(ob + j * a.o_sh * 2) = (__bf16)o;
+    }
+  }
 }
 
 }  // namespace int8kv
@@ -473,41 +623,57 @@ using namespace int8kv;
 
 namespace {
 
-int64_t ceil_div(int64_t x, int64_t y) { return (x + y - 1) / y; }
+constexpr int kMaxRangesLimit = 1 << 20;
+constexpr int kWavesPerCU = 8;  // resident decode waves per CU the automatic range count targets
 
-int32_t auto_chunk_tokens(int64_t batch, int32_t num_kv_heads, int64_t table_width,
-                          int32_t block_size) {
-  const int64_t tokens = table_width * block_size;
-  const int32_t cands[3] = {512, 256, 128};
-  for (int i = 0; i < 3; ++i) {
-    if (batch * num_kv_heads * ceil_div(tokens, cands[i]) >= 2048) return cands[i];
-  }
-  return 128;
+// Waves per workgroup: the largest of 4, 3, 2, 1 dividing num_kv_heads.
+int waves_per_wg(int32_t num_kv_heads) {
+  for (int w = 4; w > 1; --w)
+    if (num_kv_heads % w == 0) return w;
+  return 1;
 }
 
-size_t workspace_bytes(int64_t batch, int32_t num_q_heads, int32_t num_kv_heads,
-                       int64_t table_width, int32_t block_size, int32_t chunk_tokens) {
-  const int64_t max_chunks = ceil_div(table_width * block_size, chunk_tokens);
-  if (max_chunks <= 1) return 0;
-  const int64_t rows = batch * (int64_t)num_q_heads * max_chunks;  // (item, head) rows
-  return (size_t)(rows * (kHeadDim + 2) * (int64_t)sizeof(float));
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev >= 0 && dev < 64 && cached[dev] > 0) return cached[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  if (dev >= 0 && dev < 64) cached[dev] = n;
+  return n;
+}
+
+int32_t auto_ranges(int32_t num_kv_heads) {
+  const int64_t p = (int64_t)cu_count() * kWavesPerCU / num_kv_heads;
+  return (int32_t)(p < 1 ? 1 : (p > kMaxRangesLimit ? kMaxRangesLimit : p));
+}
+
+size_t workspace_bytes(int32_t num_q_heads, int32_t ranges) {
+  return (size_t)ranges * 2 * num_q_heads * (kHeadDim + 2) * sizeof(float);
 }
 
 bool aligned16(const void* p, int64_t stride_bytes) {
   return ((uintptr_t)p % 16) == 0 && (stride_bytes % 16) == 0;
 }
 
+bool shape_ok(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size) {
+  return num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0 &&
+         num_q_heads / num_kv_heads <= kMaxGroup && head_dim == kHeadDim && block_size == kBlock;
+}
+
 template <int CACHE, int QT>
-int launch(const DecodeArgs& a, int64_t batch, int32_t num_q_heads, uint32_t flags,
-           hipStream_t s) {
+int launch(const DecodeArgs& a, uint32_t flags, hipStream_t s) {
+  const int W = waves_per_wg(a.num_kv_heads);
   if (flags & INT8KV_DECODE_MAIN) {
-    dim3 grid((unsigned)a.max_chunks, (unsigned)a.num_kv_heads, (unsigned)batch);
-    hipLaunchKernelGGL((decode_kernel<CACHE, QT>), grid, dim3(kWaves * kWave), 0, s, a);
+    dim3 grid((unsigned)a.max_ranges, (unsigned)(a.num_kv_heads / W));
+    hipLaunchKernelGGL((decode_kernel<CACHE, QT>), grid, dim3(W * kWave), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }
-  if ((flags & INT8KV_DECODE_MERGE) && a.max_chunks > 1) {
-    dim3 grid((unsigned)num_q_heads, (unsigned)batch);
+  if (flags & INT8KV_DECODE_MERGE) {
+    dim3 grid((unsigned)a.batch, (unsigned)a.num_kv_heads);
     hipLaunchKernelGGL((merge_kernel<CACHE, QT>), grid, dim3(kHeadDim), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
@@ -516,37 +682,32 @@ int launch(const DecodeArgs& a, int64_t batch, int32_t num_q_heads, uint32_t fla
 }
 
 template <int CACHE>
-int launch_q(const DecodeArgs& a, int query_dtype, int64_t batch, int32_t num_q_heads,
-             uint32_t flags, hipStream_t s) {
+int launch_q(const DecodeArgs& a, int query_dtype, uint32_t flags, hipStream_t s) {
   switch (query_dtype) {
     case INT8KV_F32:
-      return launch<CACHE, kF32>(a, batch, num_q_heads, flags, s);
+      return launch<CACHE, kF32>(a, flags, s);
     case INT8KV_F16:
-      return launch<CACHE, kF16>(a, batch, num_q_heads, flags, s);
+      return launch<CACHE, kF16>(a, flags, s);
     default:
-      return launch<CACHE, kBF16>(a, batch, num_q_heads, flags, s);
+      return launch<CACHE, kBF16>(a, flags, s);
   }
 }
 
 }  // namespace
 
-extern "C" int32_t int8kv_decode_auto_chunk_tokens(int64_t batch, int32_t num_kv_heads,
-                                                   int64_t table_width, int32_t block_size) {
-  if (batch <= 0 || num_kv_heads <= 0 || table_width <= 0 || block_size <= 0) return 128;
-  return auto_chunk_tokens(batch, num_kv_heads, table_width, block_size);
+extern "C" int32_t int8kv_decode_auto_ranges(int32_t num_kv_heads) {
+  if (num_kv_heads <= 0) return 1;
+  return auto_ranges(num_kv_heads);
 }
 
-extern "C" size_t int8kv_decode_workspace_bytes(int64_t batch, int32_t num_q_heads,
-                                                int32_t num_kv_heads, int32_t head_dim,
-                                                int64_t table_width, int32_t block_size,
-                                                int32_t chunk_tokens) {
-  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim != kHeadDim ||
-      block_size != kBlock || table_width <= 0 || num_q_heads % num_kv_heads != 0 ||
-      num_q_heads / num_kv_heads > kMaxGroup || chunk_tokens < 0 || chunk_tokens % kTile != 0)
+extern "C" size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads,
+                                                int32_t head_dim, int32_t block_size,
+                                                int32_t num_ranges) {
+  if (!shape_ok(num_q_heads, num_kv_heads, head_dim, block_size) || num_ranges < 0 ||
+      num_ranges > kMaxRangesLimit)
     return 0;
-  if (chunk_tokens == 0)
-    chunk_tokens = auto_chunk_tokens(batch, num_kv_heads, table_width, block_size);
-  return workspace_bytes(batch, num_q_heads, num_kv_heads, table_width, block_size, chunk_tokens);
+  if (num_ranges == 0) num_ranges = auto_ranges(num_kv_heads);
+  return workspace_bytes(num_q_heads, num_ranges);
 }
 
 extern "C" int int8kv_paged_decode(
@@ -557,7 +718,8 @@ extern "C" int int8kv_paged_decode(
     const void* block_tables, int table_dtype, int64_t table_width, const int64_t table_strides[2],
     const void* seq_lens, int seq_lens_dtype, const float* k_scale, const float* v_scale,
     float sm_scale, void* out, const int64_t out_strides[3], void* workspace,
-    size_t workspace_bytes_given, int32_t chunk_tokens, uint32_t flags, void* stream) {
+    size_t workspace_bytes_given, int32_t num_ranges, int32_t min_tiles, uint32_t flags,
+    void* stream) {
   if (!query_strides || !key_cache_strides || !value_cache_strides || !table_strides ||
       !out_strides)
     return INT8KV_E_NULL;
@@ -567,10 +729,10 @@ extern "C" int int8kv_paged_decode(
     return INT8KV_E_DTYPE;
   if (table_dtype != INT8KV_I32 && table_dtype != INT8KV_I64) return INT8KV_E_DTYPE;
   if (seq_lens_dtype != INT8KV_I32 && seq_lens_dtype != INT8KV_I64) return INT8KV_E_DTYPE;
-  if (batch < 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
-      num_q_heads / num_kv_heads > kMaxGroup || head_dim != kHeadDim || block_size != kBlock ||
-      num_blocks <= 0 || table_width <= 0 || chunk_tokens < 0 || chunk_tokens % kTile != 0 ||
-      batch > 65535 || num_kv_heads > 65535)
+  if (batch < 0 || !shape_ok(num_q_heads, num_kv_heads, head_dim, block_size) ||
+      num_blocks <= 0 || table_width <= 0 || table_width > 0x7fffffffLL || num_ranges < 0 ||
+      num_ranges > kMaxRangesLimit || min_tiles < 0 || batch > 0x7fffffffLL ||
+      num_kv_heads > 65535)
     return INT8KV_E_SHAPE;
   if (batch == 0) return INT8KV_OK;
   if (!query || !key_cache || !value_cache || !block_tables || !seq_lens || !out)
@@ -582,7 +744,8 @@ extern "C" int int8kv_paged_decode(
   if (query_strides[2] != 1 || out_strides[2] != 1 || key_cache_strides[3] != 1 ||
       value_cache_strides[3] != 1)
     return INT8KV_E_STRIDE;
-  if (!aligned16(query, query_strides[0] * qe) || !aligned16(query, query_strides[1] * qe))
+  if (!aligned16(query, query_strides[0] * qe) || !aligned16(query, query_strides[1] * qe) ||
+      !aligned16(out, out_strides[0] * qe) || !aligned16(out, out_strides[1] * qe))
     return INT8KV_E_STRIDE;
   for (int i = 0; i < 3; ++i) {
     if (!aligned16(key_cache, key_cache_strides[i] * ce) ||
@@ -590,14 +753,10 @@ extern "C" int int8kv_paged_decode(
       return INT8KV_E_STRIDE;
   }
 
-  if (chunk_tokens == 0)
-    chunk_tokens = auto_chunk_tokens(batch, num_kv_heads, table_width, block_size);
-  const int64_t max_chunks = ceil_div(table_width * block_size, chunk_tokens);
-  if (max_chunks > 0x7fffffffLL) return INT8KV_E_SHAPE;
-  const size_t need =
-      workspace_bytes(batch, num_q_heads, num_kv_heads, table_width, block_size, chunk_tokens);
-  if (need > 0 && (workspace == nullptr || workspace_bytes_given < need ||
-                   ((uintptr_t)workspace % 16) != 0))
+  if (num_ranges == 0) num_ranges = auto_ranges(num_kv_heads);
+  if (min_tiles == 0) min_tiles = 2;
+  const size_t need = workspace_bytes(num_q_heads, num_ranges);
+  if (workspace == nullptr || workspace_bytes_given < need || ((uintptr_t)workspace % 16) != 0)
     return INT8KV_E_WORKSPACE;
 
   DecodeArgs a;
@@ -621,17 +780,19 @@ extern "C" int int8kv_paged_decode(
   a.out = static_cast<char*>(out);
   a.o_sb = out_strides[0];
   a.o_sh = out_strides[1];
-  const int64_t rows = batch * (int64_t)num_q_heads * max_chunks;
+  const int64_t recs = (int64_t)num_ranges * 2 * num_q_heads;
   float* ws = static_cast<float*>(workspace);
-  a.ws_acc = need ? ws : nullptr;
-  a.ws_m = need ? ws + rows * kHeadDim : nullptr;
-  a.ws_l = need ? ws + rows * (kHeadDim + 1) : nullptr;
+  a.ws_acc = ws;
+  a.ws_m = ws + recs * kHeadDim;
+  a.ws_l = ws + recs * (kHeadDim + 1);
   a.num_blocks = num_blocks;
+  a.batch = batch;
   a.num_kv_heads = num_kv_heads;
+  a.num_q_heads = num_q_heads;
   a.group = num_q_heads / num_kv_heads;
-  a.width = (int32_t)(table_width > 0x7fffffffLL ? 0x7fffffff : table_width);
-  a.chunk_tiles = chunk_tokens / kTile;
-  a.max_chunks = (int32_t)max_chunks;
+  a.width = (int32_t)table_width;
+  a.max_ranges = num_ranges;
+  a.min_tiles = min_tiles;
   a.bt_is64 = table_dtype == INT8KV_I64;
   a.sl_is64 = seq_lens_dtype == INT8KV_I64;
   a.sm_scale_log2e = sm_scale * kLog2e;
@@ -639,10 +800,10 @@ extern "C" int int8kv_paged_decode(
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (cache_dtype) {
     case INT8KV_I8:
-      return launch_q<kI8>(a, query_dtype, batch, num_q_heads, flags, s);
+      return launch_q<kI8>(a, query_dtype, flags, s);
     case INT8KV_BF16:
-      return launch_q<kBF16>(a, query_dtype, batch, num_q_heads, flags, s);
+      return launch_q<kBF16>(a, query_dtype, flags, s);
     default:
-      return launch_q<kF16>(a, query_dtype, batch, num_q_heads, flags, s);
+      return launch_q<kF16>(a, query_dtype, flags, s);
   }
 }

@@ -24,14 +24,18 @@ def _aligned16(t: torch.Tensor, dims) -> bool:
     return all((t.stride(d) * e) % 16 == 0 for d in dims)
 
 
-def chunk_tokens_for(table_width: int, block_size: int, num_splits) -> int:
-    """Chunk size for a forced split count (0 = let the library choose)."""
+MAX_RANGES = 1 << 20
+
+
+def ranges_for(batch: int, num_splits) -> int:
+    """Range count for a forced split count (0 = let the library choose).
+
+    The kernel cuts the batch's token stream into equal ranges; ``num_splits`` splits per
+    sequence correspond to ``num_splits * batch`` ranges (exactly so for equal lengths).
+    """
     if num_splits is None:
         return 0
-    splits = max(1, int(num_splits))
-    tokens = table_width * block_size
-    per = -(-tokens // splits)
-    return max(32, -(-per // 32) * 32)
+    return max(1, min(MAX_RANGES, int(num_splits) * max(1, int(batch))))
 
 
 def debug_check(block_tables, seq_lens, num_blocks, block_size, require_positive) -> None:
@@ -55,9 +59,10 @@ def paged_decode(
     k_scale,
     v_scale,
     out: torch.Tensor,
-    chunk_tokens: int = 0,
+    num_ranges: int = 0,
     flags: int = _lib.DECODE_ALL,
     workspace: torch.Tensor | None = None,
+    min_tiles: int = 0,
 ) -> torch.Tensor:
     """Launches int8kv_paged_decode on torch's current stream; returns ``out``."""
     B, Hq, D = query.shape
@@ -70,9 +75,9 @@ def paged_decode(
         query = query.contiguous()
     seq_lens = seq_lens.contiguous()
     lib = _lib.load()
-    need = lib.int8kv_decode_workspace_bytes(B, Hq, Hkv, D, width, block_size, chunk_tokens)
-    if need and (workspace is None or workspace.numel() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    need = lib.int8kv_decode_workspace_bytes(Hq, Hkv, D, block_size, num_ranges)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
     status = lib.int8kv_paged_decode(
         query.data_ptr(),
         _lib.DTYPE_CODE[query.dtype],
@@ -99,9 +104,10 @@ def paged_decode(
         1.0 / math.sqrt(D),
         out.data_ptr(),
         _lib.strides(out),
-        workspace.data_ptr() if need else None,
-        need,
-        chunk_tokens,
+        workspace.data_ptr(),
+        workspace.numel(),
+        num_ranges,
+        min_tiles,
         flags,
         _lib.stream_handle(dev),
     )

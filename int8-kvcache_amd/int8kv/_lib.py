@@ -60,14 +60,14 @@ def load() -> ctypes.CDLL:
         _c_i64p, _c_i64p, _vp, ctypes.c_int, _vp, _vp, _vp,
     ]
     lib.int8kv_decode_workspace_bytes.restype = sz
-    lib.int8kv_decode_workspace_bytes.argtypes = [i64, i32, i32, i32, i64, i32, i32]
-    lib.int8kv_decode_auto_chunk_tokens.restype = i32
-    lib.int8kv_decode_auto_chunk_tokens.argtypes = [i64, i32, i64, i32]
+    lib.int8kv_decode_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
+    lib.int8kv_decode_auto_ranges.restype = i32
+    lib.int8kv_decode_auto_ranges.argtypes = [i32]
     lib.int8kv_paged_decode.restype = ctypes.c_int
     lib.int8kv_paged_decode.argtypes = [
         _vp, ctypes.c_int, i64, i32, i32, _c_i64p, _vp, _vp, ctypes.c_int, i64, i32, i32,
         _c_i64p, _c_i64p, _vp, ctypes.c_int, i64, _c_i64p, _vp, ctypes.c_int, _vp, _vp, f32,
-        _vp, _c_i64p, _vp, sz, i32, u32, _vp,
+        _vp, _c_i64p, _vp, sz, i32, i32, u32, _vp,
     ]
     lib.int8kv_version.restype = ctypes.c_char_p
     lib.int8kv_version.argtypes = []

@@ -40,8 +40,8 @@ def bf16_paged_attention(
     assert all(t.device == query.device for t in tensors), "all tensors must be on one device"
     if _decode.DEBUG_CHECKS:
         _decode.debug_check(block_tables, seq_lens, num_blocks, block_size, False)
-    chunk = _decode.chunk_tokens_for(block_tables.shape[1], block_size, num_splits)
+    ranges = _decode.ranges_for(B, num_splits)
     output = torch.empty((B, Hq, D), device=query.device, dtype=query.dtype)
     return _decode.paged_decode(
-        query, key_cache, value_cache, block_tables, seq_lens, None, None, output, chunk
+        query, key_cache, value_cache, block_tables, seq_lens, None, None, output, ranges
     )

@@ -7,11 +7,15 @@ libint8kv.so.  Differences that a caller can observe:
 * No host synchronisation: the reference's ``seq_lens.min()/max().item()`` checks (:720-723)
   only run when the environment variable INT8KV_DEBUG=1 is set.  The kernel bounds every
   sequence by ``block_tables.shape[1] * block_size`` instead and writes 0 for empty sequences.
-* ``impl``: "v4" and "auto" run the group-shared kernel with automatic chunking; "v3" (one
-  pass per sequence in the reference, :393-504) runs the same kernel with one chunk per
-  sequence.  Any other value raises ValueError, as in the reference (:767-768).
-* ``num_splits``: an integer forces that many chunks over the block-table width (the
-  reference splits the logical blocks of the longest sequence into that many ranges, :156-162).
+* Work split: the kernel cuts the batch's token stream (all sequences' 32-token tiles in batch
+  order) into equal ranges, one workgroup each, so ragged batches are balanced; sequences cut
+  by a range bound are combined by a merge pass.
+* ``impl``: "v4" and "auto" run the group-shared kernel with the automatic range count; "v3"
+  (one pass per query head and sequence in the reference, :393-504) runs the same kernel with
+  one range per sequence on average.  Any other value raises ValueError, as in the reference
+  (:767-768).
+* ``num_splits``: an integer S asks for S splits per sequence, i.e. S * B ranges (the reference
+  splits the logical blocks of the longest sequence into S ranges, :156-162).
 * ``num_warps`` is accepted and ignored; ``quantize_q=True`` raises NotImplementedError.
 """
 
@@ -64,11 +68,10 @@ def int8_paged_attention(
 
     k_scale = k_scale.to(torch.float32).contiguous()
     v_scale = v_scale.to(torch.float32).contiguous()
-    width = block_tables.shape[1]
     if impl == "v3" and num_splits is None:
         num_splits = 1
-    chunk = _decode.chunk_tokens_for(width, block_size, num_splits)
+    ranges = _decode.ranges_for(B, num_splits)
     output = torch.empty((B, Hq, D), device=query.device, dtype=query.dtype)
     return _decode.paged_decode(
-        query, key_cache, value_cache, block_tables, seq_lens, k_scale, v_scale, output, chunk
+        query, key_cache, value_cache, block_tables, seq_lens, k_scale, v_scale, output, ranges
     )

@@ -31,7 +31,7 @@ def lib():
 def test_header_declares_expected_entry_points():
     assert _declared_functions() == [
         "int8kv_cache_write",
-        "int8kv_decode_auto_chunk_tokens",
+        "int8kv_decode_auto_ranges",
         "int8kv_decode_workspace_bytes",
         "int8kv_paged_decode",
         "int8kv_version",
@@ -45,20 +45,21 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_workspace_bytes(lib):
-    # B=64, Hq=28, Hkv=4, D=128, width 2048 blocks, chunk 512 -> 64 chunks of partials
-    n = lib.int8kv_decode_workspace_bytes(64, 28, 4, 128, 2048, 16, 512)
-    assert n == 64 * 28 * 64 * (128 + 2) * 4
-    # a single chunk per sequence needs no workspace
-    assert lib.int8kv_decode_workspace_bytes(8, 28, 4, 128, 32, 16, 512) == 0
+    # 512 ranges x 2 slots x 28 query heads x (128 accumulators + max + sum) fp32
+    assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 512) == 512 * 2 * 28 * 130 * 4
+    assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 1) == 2 * 28 * 130 * 4
     # unsupported sizes -> 0
-    assert lib.int8kv_decode_workspace_bytes(8, 28, 4, 64, 32, 16, 0) == 0
-    assert lib.int8kv_decode_workspace_bytes(8, 28, 4, 128, 32, 32, 0) == 0
-    assert lib.int8kv_decode_workspace_bytes(8, 34, 2, 128, 32, 16, 0) == 0  # group 17
-    assert lib.int8kv_decode_workspace_bytes(8, 28, 4, 128, 32, 16, 48) == 0  # not /32
-    auto = lib.int8kv_decode_auto_chunk_tokens(64, 4, 2048, 16)
-    assert auto % 32 == 0 and 128 <= auto <= 4096
-    assert lib.int8kv_decode_workspace_bytes(64, 28, 4, 128, 2048, 16, 0) == \
-        lib.int8kv_decode_workspace_bytes(64, 28, 4, 128, 2048, 16, auto)
+    assert lib.int8kv_decode_workspace_bytes(28, 4, 64, 16, 0) == 0  # head_dim
+    assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 32, 0) == 0  # block size
+    assert lib.int8kv_decode_workspace_bytes(34, 2, 128, 16, 0) == 0  # group 17
+    assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, -1) == 0
+    assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, (1 << 20) + 1) == 0
+    # automatic: a few workgroups per compute unit (no GPU here: the library assumes 256 CUs)
+    auto = lib.int8kv_decode_auto_ranges(4)
+    assert auto >= 1
+    assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 0) == \
+        lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, auto)
+    assert lib.int8kv_decode_auto_ranges(8) * 2 == auto
 
 
 def _decode_call(lib, **over):
@@ -68,8 +69,8 @@ def _decode_call(lib, **over):
     args = dict(query=16, query_dtype=2, batch=1, num_q_heads=28, head_dim=128, qs=st3,
                 kc=16, vc=16, cache_dtype=3, num_blocks=8, block_size=16, num_kv_heads=4,
                 kcs=st4, vcs=st4, bt=16, table_dtype=4, width=8, bts=st2, sl=16, sl_dtype=4,
-                ks=16, vs=16, sm=0.088, out=16, os=st3, ws=None, wsb=0, chunk=0, flags=3,
-                stream=None)
+                ks=16, vs=16, sm=0.088, out=16, os=st3, ws=16, wsb=1 << 30, ranges=0,
+                min_tiles=0, flags=3, stream=None)
     args.update(over)
     return lib.int8kv_paged_decode(*args.values())
 
@@ -82,15 +83,18 @@ def test_decode_rejects_bad_arguments_without_launching(lib):
     assert _decode_call(lib, head_dim=64) == -3
     assert _decode_call(lib, block_size=32) == -3
     assert _decode_call(lib, num_q_heads=30) == -3
-    assert _decode_call(lib, chunk=40) == -3
+    assert _decode_call(lib, ranges=-1) == -3
+    assert _decode_call(lib, min_tiles=-1) == -3
     assert _decode_call(lib, query=None) == -1
     assert _decode_call(lib, ks=None) == -1
     st3 = (ctypes.c_int64 * 3)(28 * 128, 128, 2)
     assert _decode_call(lib, qs=st3) == -4
     assert _decode_call(lib, query=24) == -4  # misaligned
-    # needs partials (width 64 blocks = 1024 tokens > chunk 128) but no workspace
-    st2 = (ctypes.c_int64 * 2)(64, 1)
-    assert _decode_call(lib, width=64, bts=st2, chunk=128) == -5
+    assert _decode_call(lib, out=40) == -4  # misaligned output
+    # the partial workspace is always required
+    assert _decode_call(lib, ws=None) == -5
+    assert _decode_call(lib, wsb=1000) == -5
+    assert _decode_call(lib, ws=24) == -5
     assert _decode_call(lib, batch=0) == 0  # nothing to do
 
 

@@ -76,12 +76,13 @@ def test_dequantize_debug_helper():
     assert out.tolist() == [[[[0.5, -1.0], [6.0, 8.0]]]]
 
 
-def test_chunk_tokens_for_forced_splits():
-    assert _decode.chunk_tokens_for(2048, 16, None) == 0
-    assert _decode.chunk_tokens_for(2048, 16, 1) == 32768
-    assert _decode.chunk_tokens_for(2048, 16, 4) == 8192
-    assert _decode.chunk_tokens_for(3, 16, 4) == 32  # at least one 32-token tile
-    assert _decode.chunk_tokens_for(19, 16, 4) == 96  # 304 tokens / 4 -> 76 -> 96
+def test_ranges_for_forced_splits():
+    assert _decode.ranges_for(64, None) == 0
+    assert _decode.ranges_for(64, 1) == 64
+    assert _decode.ranges_for(3, 4) == 12
+    assert _decode.ranges_for(0, 4) == 4
+    assert _decode.ranges_for(5, 0) == 1
+    assert _decode.ranges_for(1 << 20, 8) == 1 << 20
 
 
 def test_synthetic_generators():
