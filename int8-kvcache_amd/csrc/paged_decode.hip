@@ -38,9 +38,15 @@ namespace int8kv {
 
 constexpr int kHeadDim = 128;
 constexpr int kBlock = 16;          // tokens per cache block
-constexpr int kTile = 32;           // tokens per wave iteration
 constexpr int kMaxGroup = 16;       // query heads per kv head (MFMA column count)
-constexpr int kWindowTiles = 32;    // tiles covered by one 64-entry block-table window
+constexpr int kChunkTiles = 256;    // tiles whose block ids a wave stages in LDS at a time
+constexpr int kMaxWavesPerWG = 4;
+
+// Cache blocks per wave iteration ("tile"): 32 tokens, one MFMA k-step of P*V.
+template <int CACHE>
+constexpr int tile_blocks() {
+  return 2;
+}
 constexpr float kLazyRescale = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -69,6 +75,7 @@ struct DecodeArgs {
   int32_t width;       // block-table width in blocks
   int32_t max_ranges;  // P upper bound (= grid.x of decode_kernel)
   int32_t min_tiles;   // P <= ceil(T / min_tiles)
+  int32_t tile_tokens;  // 16 * tile_blocks<CACHE>()
   int32_t bt_is64;
   int32_t sl_is64;
   float sm_scale_log2e;
@@ -98,7 +105,7 @@ __device__ __forceinline__ int64_t readlane64(int64_t x, int lane) {
 
 // ------------------------------------------------------------------------ work plan
 // Sequence b's token count L_b = clamp(seq_lens[b], 0, width * 16) and tile count
-// n_b = ceil(L_b / 32); T = sum_b n_b; P = clamp(ceil(T / min_tiles), 1, max_ranges);
+// n_b = ceil(L_b / tile_tokens); T = sum_b n_b; P = clamp(ceil(T / min_tiles), 1, max_ranges);
 // range r covers stream tiles [r * T / P, (r + 1) * T / P).
 __device__ __forceinline__ int64_t seq_len_of(const DecodeArgs& a, int64_t b) {
   if (b >= a.batch) return 0;
@@ -107,7 +114,9 @@ __device__ __forceinline__ int64_t seq_len_of(const DecodeArgs& a, int64_t b) {
   return L < 0 ? 0 : (L > cap ? cap : L);
 }
 
-__device__ __forceinline__ int64_t tiles_of(int64_t L) { return (L + kTile - 1) / kTile; }
+__device__ __forceinline__ int64_t tiles_of(const DecodeArgs& a, int64_t L) {
+  return (L + a.tile_tokens - 1) / a.tile_tokens;
+}
 
 struct Plan {
   int64_t T;
@@ -116,7 +125,7 @@ struct Plan {
 
 __device__ __forceinline__ Plan make_plan(const DecodeArgs& a, int lane) {
   int64_t T = 0;
-  for (int64_t base = 0; base < a.batch; base += kWave) T += wave_sum(tiles_of(seq_len_of(a, base + lane)));
+  for (int64_t base = 0; base < a.batch; base += kWave) T += wave_sum(tiles_of(a, seq_len_of(a, base + lane)));
   int64_t P = (T + a.min_tiles - 1) / a.min_tiles;
   P = P < 1 ? 1 : (P > a.max_ranges ? a.max_ranges : P);
   return {T, P};
@@ -130,21 +139,25 @@ __device__ __forceinline__ int64_t range_of(const Plan& p, int64_t x) {
 }
 
 // ------------------------------------------------------------------------ tile registers
-// Registers holding one 32-token tile of K and V for one lane.
+// Registers holding the K or the V half of one tile (NB cache blocks) for one lane.
 //   K: lane (i = lane % 16, g = lane / 16) holds token i of block s, head_dim elements
 //      [32g, 32g + 32).
 //   V: lane (i, g) holds tokens 4g + r (r = 0..3) of block s, head_dim elements [8i, 8i + 8).
 template <int CACHE>
-struct RawTile;
-template <>
-struct RawTile<kI8> {
-  u32x4 k[2][2];
-  u32x2 v[2][4];
+struct VRow {
+  typedef u32x4 T;  // 8 16-bit elements
 };
-template <int CACHE>
-struct RawTile {
-  u32x4 k[2][4];
-  u32x4 v[2][4];
+template <>
+struct VRow<kI8> {
+  typedef u32x2 T;  // 8 int8 elements
+};
+template <int CACHE, int NB>
+struct KTile {
+  u32x4 k[NB][CACHE == kI8 ? 2 : 4];
+};
+template <int CACHE, int NB>
+struct VTile {
+  typename VRow<CACHE>::T v[NB][4];
 };
 
 template <int CACHE>
@@ -219,49 +232,49 @@ __device__ __forceinline__ void store8(char* p, const float (&x)[8]) {
   }
 }
 
-template <int CACHE>
-__device__ __forceinline__ void issue_tile_loads(RawTile<CACHE>& r, const char* kb,
-                                                 const char* vb, int64_t p0, int64_t p1,
-                                                 const DecodeArgs& a, int li, int lg) {
+template <int CACHE, int NB>
+__device__ __forceinline__ void issue_k(KTile<CACHE, NB>& r, const char* kb,
+                                        const int64_t (&ph)[NB], const DecodeArgs& a, int li,
+                                        int lg) {
   constexpr int E = esize<CACHE>();
-  const int64_t ph[2] = {p0, p1};
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const char* kp = kb + ph[s] * a.kc_sb + li * a.kc_ss + lg * (32 * E);
-    const u32x4* k4 = reinterpret_cast<const u32x4*>(kp);
-    if constexpr (CACHE == kI8) {
-      r.k[s][0] = k4[0];
-      r.k[s][1] = k4[1];
-    } else {
-      r.k[s][0] = k4[0];
-      r.k[s][1] = k4[1];
-      r.k[s][2] = k4[2];
-      r.k[s][3] = k4[3];
-    }
-    const char* vp = vb + ph[s] * a.vc_sb + (4 * lg) * a.vc_ss + li * (8 * E);
+  for (int s = 0; s < NB; ++s) {
+    const u32x4* k4 =
+        reinterpret_cast<const u32x4*>(kb + ph[s] * a.kc_sb + li * a.kc_ss + lg * (32 * E));
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      if constexpr (CACHE == kI8) {
-        r.v[s][rr] = *reinterpret_cast<const u32x2*>(vp + rr * a.vc_ss);
-      } else {
-        r.v[s][rr] = *reinterpret_cast<const u32x4*>(vp + rr * a.vc_ss);
-      }
-    }
+    for (int i = 0; i < 2 * E; ++i) r.k[s][i] = k4[i];
   }
 }
 
-// One 32-token tile: scores, online softmax update, P*V accumulation.
-//   valid: number of tokens of this tile inside the sequence (1..32).
-template <int CACHE>
-__device__ __forceinline__ void compute_tile(RawTile<CACHE>& r,
-                                             const typename MfmaOp<CACHE>::T (&qop)[4],
-                                             f32x4 (&acc)[8], float& m_run, float& l_part,
-                                             int valid, int lg, float s_scale) {
-  typedef typename MfmaOp<CACHE>::T OpT;
-  // ---- scores S^T[token][head] for the two blocks of the tile ----
-  f32x4 S[2];
+template <int CACHE, int NB>
+__device__ __forceinline__ void issue_v(VTile<CACHE, NB>& r, const char* vb,
+                                        const int64_t (&ph)[NB], const DecodeArgs& a, int li,
+                                        int lg) {
+  constexpr int E = esize<CACHE>();
+  typedef typename VRow<CACHE>::T Row;
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
+  for (int s = 0; s < NB; ++s) {
+    const char* vp = vb + ph[s] * a.vc_sb + (4 * lg) * a.vc_ss + li * (8 * E);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) r.v[s][rr] = *reinterpret_cast<const Row*>(vp + rr * a.vc_ss);
+  }
+}
+
+// Scores of one tile (NB cache blocks) and the online-softmax update: rescales acc/l_part when
+// the running max moves and returns the P^T operands (one per MFMA k-step of 32 tokens).
+//   valid: number of tokens of this tile inside the sequence (1..16 NB).
+template <int CACHE, int NB>
+__device__ __forceinline__ void tile_scores(const KTile<CACHE, NB>& r,
+                                            const typename MfmaOp<CACHE>::T (&qop)[4],
+                                            f32x4 (&acc)[8], float& m_run, float& l_part,
+                                            int valid, int lg, float s_scale,
+                                            typename MfmaOp<CACHE>::T (&pop)[NB / 2]) {
+  typedef typename MfmaOp<CACHE>::T OpT;
+  constexpr int kTileTokens = NB * kBlock;
+  // ---- scores S^T[token][head] for each block of the tile ----
+  f32x4 S[NB];
+#pragma unroll
+  for (int s = 0; s < NB; ++s) {
     S[s] = (f32x4)(0.0f);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -278,29 +291,21 @@ __device__ __forceinline__ void compute_tile(RawTile<CACHE>& r,
   }
 
   // ---- online softmax (exp2 domain); lane column = head, rows = tokens 16s + 4lg + r ----
-  float sv[8];
+  float sv[4 * NB];
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
+  for (int s = 0; s < NB; ++s)
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) sv[4 * s + rr] = S[s][rr] * s_scale;
-  if (valid < kTile) {
+  if (valid < kTileTokens) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < NB; ++s)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
         if (16 * s + 4 * lg + rr >= valid) sv[4 * s + rr] = -INFINITY;
-    if constexpr (CACHE != kI8) {
-      // 16-bit rows past the sequence end may hold non-finite garbage; 0 * NaN would leak.
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          if (16 * s + 4 * lg + rr >= valid) r.v[s][rr] = (u32x4)(0u);
-    }
   }
   float mx = sv[0];
 #pragma unroll
-  for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
+  for (int e = 1; e < 4 * NB; ++e) mx = fmaxf(mx, sv[e]);
   mx = fmaxf(mx, __shfl_xor(mx, 16));
   mx = fmaxf(mx, __shfl_xor(mx, 32));
   const bool need = mx > m_run + kLazyRescale;
@@ -312,55 +317,72 @@ __device__ __forceinline__ void compute_tile(RawTile<CACHE>& r,
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
   }
-  float p[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    p[e] = exp2_fast(sv[e] - m_run);
-    l_part += p[e];
+  for (int e = 0; e < 4 * NB; ++e) {
+    const float pe = exp2_fast(sv[e] - m_run);
+    l_part += pe;
+    pop[e / 8][e % 8] = (typename MfmaOp<CACHE>::E)pe;
   }
-  OpT pop;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) pop[e] = (typename MfmaOp<CACHE>::E)p[e];
+}
 
-  // ---- out^T[dim][head] += V^T[dim][token] * P^T[token][head] ----
-  // MFMA row i of dim tile dt is head_dim element 8i + dt; k-slot e of lane group g is token
-  // (block e / 4, row 4g + e % 4), matching the P^T operand built above.
-  if constexpr (CACHE == kI8) {
-    uint32_t pk[2][2][2][2];  // [block][token pair][lo/hi dword][byte pair 01/23]
+// out^T[dim][head] += V^T[dim][token] * P^T[token][head] for one tile.
+// MFMA row i of dim tile dt is head_dim element 8i + dt; k-slot e of lane group g in k-step
+// kst is token (block 2 kst + e / 4, row 4g + e % 4), matching the P^T operands.
+template <int CACHE, int NB>
+__device__ __forceinline__ void tile_pv(VTile<CACHE, NB>& r,
+                                        const typename MfmaOp<CACHE>::T (&pop)[NB / 2],
+                                        f32x4 (&acc)[8], int valid, int lg) {
+  typedef typename MfmaOp<CACHE>::T OpT;
+  if constexpr (CACHE != kI8) {
+    // 16-bit rows past the sequence end may hold non-finite garbage; 0 * NaN would leak.
+    if (valid < NB * kBlock) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+      for (int s = 0; s < NB; ++s)
 #pragma unroll
-      for (int rp = 0; rp < 2; ++rp)
-#pragma unroll
-        for (int hsel = 0; hsel < 2; ++hsel) {
-          const uint32_t a0 = r.v[s][2 * rp][hsel] ^ kSignFlip;
-          const uint32_t b0 = r.v[s][2 * rp + 1][hsel] ^ kSignFlip;
-          pk[s][rp][hsel][0] = perm(a0, b0, 0x01050004u);  // [a.b0, b.b0, a.b1, b.b1]
-          pk[s][rp][hsel][1] = perm(a0, b0, 0x03070206u);  // [a.b2, b.b2, a.b3, b.b3]
-        }
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const int hsel = dt >> 2, bp = (dt >> 1) & 1;
-      const uint32_t sel = (dt & 1) ? kSelHi : kSelLo;
-      u32x4 w;
-      w[0] = perm(kMagic, pk[0][0][hsel][bp], sel);
-      w[1] = perm(kMagic, pk[0][1][hsel][bp], sel);
-      w[2] = perm(kMagic, pk[1][0][hsel][bp], sel);
-      w[3] = perm(kMagic, pk[1][1][hsel][bp], sel);
-      const f16x8 vop = __builtin_bit_cast(f16x8, w) - (f16x8)(_Float16)1152.0f;
-      acc[dt] = mfma(vop, pop, acc[dt]);
+        for (int rr = 0; rr < 4; ++rr)
+          if (16 * s + 4 * lg + rr >= valid) r.v[s][rr] = (u32x4)(0u);
     }
-  } else {
+  }
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const int wd = dt >> 1;
-      const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
-      u32x4 w;
-      w[0] = perm(r.v[0][1][wd], r.v[0][0][wd], sel);
-      w[1] = perm(r.v[0][3][wd], r.v[0][2][wd], sel);
-      w[2] = perm(r.v[1][1][wd], r.v[1][0][wd], sel);
-      w[3] = perm(r.v[1][3][wd], r.v[1][2][wd], sel);
-      acc[dt] = mfma(__builtin_bit_cast(OpT, w), pop, acc[dt]);
+  for (int kst = 0; kst < NB / 2; ++kst) {
+    const int s0 = 2 * kst;
+    if constexpr (CACHE == kI8) {
+      uint32_t pk[2][2][2][2];  // [block][token pair][lo/hi dword][byte pair 01/23]
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int rp = 0; rp < 2; ++rp)
+#pragma unroll
+          for (int hsel = 0; hsel < 2; ++hsel) {
+            const uint32_t a0 = r.v[s0 + s][2 * rp][hsel] ^ kSignFlip;
+            const uint32_t b0 = r.v[s0 + s][2 * rp + 1][hsel] ^ kSignFlip;
+            pk[s][rp][hsel][0] = perm(a0, b0, 0x01050004u);  // [a.b0, b.b0, a.b1, b.b1]
+            pk[s][rp][hsel][1] = perm(a0, b0, 0x03070206u);  // [a.b2, b.b2, a.b3, b.b3]
+          }
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const int hsel = dt >> 2, bp = (dt >> 1) & 1;
+        const uint32_t sel = (dt & 1) ? kSelHi : kSelLo;
+        u32x4 w;
+        w[0] = perm(kMagic, pk[0][0][hsel][bp], sel);
+        w[1] = perm(kMagic, pk[0][1][hsel][bp], sel);
+        w[2] = perm(kMagic, pk[1][0][hsel][bp], sel);
+        w[3] = perm(kMagic, pk[1][1][hsel][bp], sel);
+        const f16x8 vop = __builtin_bit_cast(f16x8, w) - (f16x8)(_Float16)1152.0f;
+        acc[dt] = mfma(vop, pop[kst], acc[dt]);
+      }
+    } else {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const int wd = dt >> 1;
+        const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
+        u32x4 w;
+        w[0] = perm(r.v[s0][1][wd], r.v[s0][0][wd], sel);
+        w[1] = perm(r.v[s0][3][wd], r.v[s0][2][wd], sel);
+        w[2] = perm(r.v[s0 + 1][1][wd], r.v[s0 + 1][0][wd], sel);
+        w[3] = perm(r.v[s0 + 1][3][wd], r.v[s0 + 1][2][wd], sel);
+        acc[dt] = mfma(__builtin_bit_cast(OpT, w), pop[kst], acc[dt]);
+      }
     }
   }
 }
@@ -413,24 +435,28 @@ __device__ __forceinline__ float load_query(const DecodeArgs& a, int64_t b, int 
   return s_scale;
 }
 
-// Physical block ids of blocks [first, first + 64) of row b, one per lane (0 past the
-// sequence's last block, clamped into [0, num_blocks) so every access stays in the caches).
-__device__ __forceinline__ int32_t load_window(const DecodeArgs& a, int64_t b, int64_t first,
-                                               int64_t nblk, int lane) {
-  const int64_t blk = first + lane;
-  if (blk >= nblk) return 0;
-  int64_t p = load_index(a.bt, b * a.bt_sb + blk * a.bt_sl, a.bt_is64);
+// Stages the physical block ids of tiles [c0, c1) of sequence b (nblk blocks) in this wave's
+// LDS slots: ids[NB * (t - c0) + s] = block s of tile t, 0 past the sequence's last block and
+// clamped into [0, num_blocks) so every access stays inside the caches.
+template <int NB>
+__device__ __forceinline__ void stage_block_ids(const DecodeArgs& a, int32_t* ids, int64_t b,
+                                                int64_t c0, int64_t c1, int64_t nblk, int lane) {
+  const int n = (int)(NB * (c1 - c0));
   const int64_t hi = a.num_blocks - 1;
-  p = p < 0 ? 0 : (p > hi ? hi : p);
-  return (int32_t)p;
+  for (int j = lane; j < n; j += kWave) {
+    const int64_t blk = NB * c0 + j;
+    int64_t p = 0;
+    if (blk < nblk) p = load_index(a.bt, b * a.bt_sb + blk * a.bt_sl, a.bt_is64);
+    ids[j] = (int32_t)(p < 0 ? 0 : (p > hi ? hi : p));
+  }
 }
 
 // Processes tiles [ta, tb) of sequence b (length L) for kv head kvh with one wave, then writes
-// either the final output (full == true) or a partial record.
+// either the final output (full == true) or a partial record.  ids: this wave's LDS slots.
 template <int CACHE, int QT>
-__device__ __forceinline__ void run_segment(const DecodeArgs& a, int64_t b, int64_t L, int kvh,
-                                            int64_t ta, int64_t tb, bool full, int64_t rec,
-                                            int lane) {
+__device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, int64_t b,
+                                            int64_t L, int kvh, int64_t ta, int64_t tb,
+                                            bool full, int64_t rec, int lane) {
   typedef typename MfmaOp<CACHE>::T OpT;
   const int li = lane & 15;
   const int lg = lane >> 4;
@@ -448,39 +474,69 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int64_t b, int6
   const char* kb = a.kc + (int64_t)kvh * a.kc_sh;
   const char* vb = a.vc + (int64_t)kvh * a.vc_sh;
   const int64_t nblk = (L + kBlock - 1) / kBlock;
+  constexpr int NB = tile_blocks<CACHE>();
+  constexpr int kTileTokens = NB * kBlock;
 
-  int64_t wbase = ta;  // first tile of the current table window
-  int32_t tbl = load_window(a, b, 2 * wbase, nblk, lane);
-  int32_t tbl_next = load_window(a, b, 2 * (wbase + kWindowTiles), nblk, lane);
-
-  auto issue = [&](RawTile<CACHE>& r, int64_t t) {
-    int rel = (int)(t - wbase);
-    if (rel >= kWindowTiles) {
-      wbase += kWindowTiles;
-      rel -= kWindowTiles;
-      tbl = tbl_next;
-      tbl_next = load_window(a, b, 2 * (wbase + kWindowTiles), nblk, lane);
-    }
-    const int64_t p0 = __builtin_amdgcn_readlane(tbl, 2 * rel);
-    const int64_t p1 = __builtin_amdgcn_readlane(tbl, 2 * rel + 1);
-    issue_tile_loads<CACHE>(r, kb, vb, p0, p1, a, li, lg);
-  };
   auto valid_of = [&](int64_t t) -> int {
-    const int64_t v = L - t * kTile;
-    return v >= kTile ? kTile : (int)v;
+    const int64_t v = L - t * kTileTokens;
+    return v >= kTileTokens ? kTileTokens : (int)v;
   };
 
-  // Two register buffers: the next tile's loads are in flight while this one is computed.
-  RawTile<CACHE> r0, r1;
-  int64_t t = ta;
-  issue(r0, t);
-  while (true) {
-    if (t + 1 < tb) issue(r1, t + 1);
-    compute_tile<CACHE>(r0, qop, acc, m_run, l_part, valid_of(t), lg, s_scale);
-    if (++t >= tb) break;
-    if (t + 1 < tb) issue(r0, t + 1);
-    compute_tile<CACHE>(r1, qop, acc, m_run, l_part, valid_of(t), lg, s_scale);
-    if (++t >= tb) break;
+  for (int64_t c0 = ta; c0 < tb; c0 += kChunkTiles) {
+    const int64_t c1 = (tb - c0 > kChunkTiles) ? c0 + kChunkTiles : tb;
+    stage_block_ids<NB>(a, ids, b, c0, c1, nblk, lane);
+      // Block ids come from LDS (the LDS counter), so the waits on tile loads below only ever
+    // count tile loads.
+    auto blocks_of = [&](int64_t t, int64_t (&ph)[NB]) {
+      const int j = NB * (int)(t - c0);
+#pragma unroll
+      for (int s = 0; s < NB; ++s) ph[s] = __builtin_amdgcn_readfirstlane(ids[j + s]);
+    };
+
+    // Two K and two V register buffers, refilled as soon as they are consumed: K(t + 2) is
+    // requested right after the scores of tile t, V(t + 2) right after its P*V, so up to two
+    // tiles of loads are in flight while a tile is computed.  The loop body handles a pair of
+    // tiles as one straight-line block and every load in it is unconditional (a request past
+    // the chunk repeats its last tile, which the caches still hold), so the compiler's wait
+    // counts are exact and no wait drains the pipeline.
+    KTile<CACHE, NB> ka, kb2;
+    VTile<CACHE, NB> va, vb2;
+    int64_t pha[NB], phb[NB];
+    OpT pop[NB / 2];
+    const int64_t last = c1 - 1;
+    int64_t t = c0;
+    blocks_of(t, pha);
+    issue_k<CACHE, NB>(ka, kb, pha, a, li, lg);
+    issue_v<CACHE, NB>(va, vb, pha, a, li, lg);
+    blocks_of(t + 1 < c1 ? t + 1 : last, phb);
+    issue_k<CACHE, NB>(kb2, kb, phb, a, li, lg);
+    issue_v<CACHE, NB>(vb2, vb, phb, a, li, lg);
+    // sched_barrier(0) keeps the compiler's scheduler from sinking the refills past the
+    // compute that follows them (which would shorten the prefetch distance).
+    for (; t + 1 < c1; t += 2) {
+      int valid = valid_of(t);
+      tile_scores<CACHE, NB>(ka, qop, acc, m_run, l_part, valid, lg, s_scale, pop);
+      blocks_of(t + 2 < c1 ? t + 2 : last, pha);
+      issue_k<CACHE, NB>(ka, kb, pha, a, li, lg);
+      __builtin_amdgcn_sched_barrier(0);
+      tile_pv<CACHE, NB>(va, pop, acc, valid, lg);
+      issue_v<CACHE, NB>(va, vb, pha, a, li, lg);
+      __builtin_amdgcn_sched_barrier(0);
+
+      valid = valid_of(t + 1);
+      tile_scores<CACHE, NB>(kb2, qop, acc, m_run, l_part, valid, lg, s_scale, pop);
+      blocks_of(t + 3 < c1 ? t + 3 : last, phb);
+      issue_k<CACHE, NB>(kb2, kb, phb, a, li, lg);
+      __builtin_amdgcn_sched_barrier(0);
+      tile_pv<CACHE, NB>(vb2, pop, acc, valid, lg);
+      issue_v<CACHE, NB>(vb2, vb, phb, a, li, lg);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (t < c1) {  // odd tile count: the last tile is in the A buffers
+      const int valid = valid_of(t);
+      tile_scores<CACHE, NB>(ka, qop, acc, m_run, l_part, valid, lg, s_scale, pop);
+      tile_pv<CACHE, NB>(va, pop, acc, valid, lg);
+    }
   }
 
   l_part += __shfl_xor(l_part, 16);
@@ -519,6 +575,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int64_t b, int6
 // kv head y * W + w over stream range r.
 template <int CACHE, int QT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(DecodeArgs a) {
+  __shared__ int32_t s_ids[kMaxWavesPerWG][kChunkTiles * tile_blocks<CACHE>()];
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int kvh = blockIdx.y * (blockDim.x / kWave) + wave;
@@ -532,7 +589,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   int64_t cum = 0;  // tiles of the sequences before this 64-sequence chunk
   for (int64_t base = 0; base < a.batch; base += kWave) {
     const int64_t L = seq_len_of(a, base + lane);
-    const int64_t n = tiles_of(L);
+    const int64_t n = tiles_of(a, L);
     const int64_t incl = wave_inclusive_scan(n, lane) + cum;
     const int64_t excl = incl - n;
     const int64_t chunk_end = readlane64(incl, kWave - 1);
@@ -548,7 +605,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
         const int64_t te = (t1 < S + nb ? t1 : S + nb) - S;
         const bool full = ta == 0 && te == nb;
         const int64_t slot = (S + ta == t0) ? 0 : 1;
-        run_segment<CACHE, QT>(a, base + j, Lb, kvh, ta, te, full, 2 * r + slot, lane);
+        run_segment<CACHE, QT>(a, s_ids[wave], base + j, Lb, kvh, ta, te, full, 2 * r + slot,
+                               lane);
       }
     }
     if (chunk_end >= t1) break;
@@ -556,64 +614,120 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   }
 }
 
+// Stores 4 consecutive fp32 values as DT (aligned to 4 elements).
+template <int DT>
+__device__ __forceinline__ void store4(char* p, f32x4 x) {
+  if constexpr (DT == kF32) {
+    *reinterpret_cast<f32x4*>(p) = x;
+  } else if constexpr (DT == kF16) {
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    f16x4 h = {(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
+    *reinterpret_cast<f16x4*>(p) = h;
+  } else {
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    bf16x4 h = {(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]};
+    *reinterpret_cast<bf16x4*>(p) = h;
+  }
+}
+
+__device__ __forceinline__ float wave_max_f(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum_f(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
 // Combines the partials of every sequence cut by range bounds and writes zeros for empty
-// sequences.  grid (batch, num_kv_heads), 128 threads (one per head_dim element).
+// sequences.  grid (batch, num_kv_heads), 4 waves; wave w merges query heads w, w + 4, ... of
+// the kv head's group.  A wave first reduces (max, sum) over the sequence's ranges with one
+// range per lane, then accumulates the weighted partial rows with lane = (range parity,
+// 4-element column), four rows in flight per lane.
 template <int CACHE, int QT>
-__global__ __launch_bounds__(128) void merge_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
   const int64_t b = blockIdx.x;
   const int kvh = blockIdx.y;
   const int lane = threadIdx.x % kWave;
-  const int d = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int nwaves = blockDim.x / kWave;
   const int G = a.group;
+  const int rs = lane >> 5;  // range parity handled by this lane
+  const int c4 = lane & 31;  // head_dim elements [4 c4, 4 c4 + 4)
 
   const Plan plan = make_plan(a, lane);
   int64_t S = 0;  // stream tiles before sequence b
   for (int64_t base = 0; base < b; base += kWave) {
     const int64_t bb = base + lane;
-    S += wave_sum(bb < b ? tiles_of(seq_len_of(a, bb)) : 0);
+    S += wave_sum(bb < b ? tiles_of(a, seq_len_of(a, bb)) : 0);
   }
-  const int64_t n = tiles_of(seq_len_of(a, b));
-  char* ob = a.out + (b * a.o_sb + (int64_t)(kvh * G) * a.o_sh + d) * esize<QT>();
+  const int64_t n = tiles_of(a, seq_len_of(a, b));
+  constexpr int QE = esize<QT>();
   if (n == 0) {
-    for (int j = 0; j < G; ++j) {
-      const float z[1] = {0.0f};
-      if constexpr (QT == kF32) {
-        *reinterpret_cast<float*>(ob + j * a.o_sh * 4) = z[0];
-      } else if constexpr (QT == kF16) {
-        *reinterpret_cast<_Float16*>(ob + j * a.o_sh * 2) = (_Float16)z[0];
-      } else {
-        *reinterpret_cast<__bf16*>(ob + j * a.o_sh * 2) = (__bf16)z[0];
-      }
+    for (int j = wave; j < G; j += nwaves) {
+      if (rs == 0)
+        store4<QT>(a.out + (b * a.o_sb + (int64_t)(kvh * G + j) * a.o_sh + 4 * c4) * QE,
+                   (f32x4)(0.0f));
     }
     return;
   }
   const int64_t r0 = range_of(plan, S);
   const int64_t r1 = range_of(plan, S + n - 1);
   if (r0 == r1) return;  // finished inside one range by decode_kernel
+  const int64_t nr = r1 - r0 + 1;
   const int64_t slot0 = range_start(plan, r0) == S ? 0 : 1;
   const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
-  for (int j = 0; j < G; ++j) {
+  auto row_of = [&](int64_t c, int h) -> int64_t {  // partial row of range r0 + c, head h
+    return (2 * (r0 + c) + (c == 0 ? slot0 : 0)) * a.num_q_heads + h;
+  };
+
+  for (int j = wave; j < G; j += nwaves) {
     const int h = kvh * G + j;
-    float M = -INFINITY;
-    for (int64_t r = r0; r <= r1; ++r) {
-      const int64_t rec = 2 * r + (r == r0 ? slot0 : 0);
-      M = fmaxf(M, a.ws_m[rec * a.num_q_heads + h]);
+    float mloc = -INFINITY, lloc = 0.0f;
+    for (int64_t c = lane; c < nr; c += kWave) {
+      const int64_t row = row_of(c, h);
+      const float m = a.ws_m[row];
+      const float l = a.ws_l[row];
+      if (m > mloc) {
+        lloc = lloc * exp2_fast(mloc - m) + l;
+        mloc = m;
+      } else {
+        lloc += l * exp2_fast(m - mloc);
+      }
     }
-    float Ls = 0.0f, O = 0.0f;
-    for (int64_t r = r0; r <= r1; ++r) {
-      const int64_t row = (2 * r + (r == r0 ? slot0 : 0)) * a.num_q_heads + h;
-      const float wt = exp2_fast(a.ws_m[row] - M);
-      Ls += wt * a.ws_l[row];
-      O += wt * a.ws_acc[row * kHeadDim + d];
+    const float M = wave_max_f(mloc);
+    const float lsum = wave_sum_f(mloc == -INFINITY ? 0.0f : lloc * exp2_fast(mloc - M));
+    const float inv = lsum > 0.0f ? vscale / lsum : 0.0f;
+
+    f32x4 O = (f32x4)(0.0f);
+    for (int64_t cb = 0; cb < nr; cb += kWave) {
+      const int cnt = (int)(nr - cb < kWave ? nr - cb : kWave);
+      const float wl = lane < cnt ? exp2_fast(a.ws_m[row_of(cb + lane, h)] - M) : 0.0f;
+      for (int kk = 0; kk < cnt; kk += 8) {
+        float w[4];
+        f32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int k = kk + rs + 2 * u;
+          w[u] = __shfl(wl, k & (kWave - 1));
+          if (k < cnt) {
+            v[u] = *reinterpret_cast<const f32x4*>(a.ws_acc + row_of(cb + k, h) * kHeadDim + 4 * c4);
+          } else {
+            v[u] = (f32x4)(0.0f);
+            w[u] = 0.0f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) O += w[u] * v[u];
+      }
     }
-    const float o = Ls > 0.0f ? O * vscale / Ls : 0.0f;
-    if constexpr (QT == kF32) {
-      *reinterpret_cast<float*>(ob + j * a.o_sh * 4) = o;
-    } else if constexpr (QT == kF16) {
-      *reinterpret_cast<_Float16*>(ob + j * a.o_sh * 2) = (_Float16)o;
-    } else {
-      *reinterpret_cast<__bf16*>(ob + j * a.o_sh * 2) = (__bf16)o;
-    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) O[e] += __shfl_xor(O[e], 32);
+    if (rs == 0)
+      store4<QT>(a.out + (b * a.o_sb + (int64_t)h * a.o_sh + 4 * c4) * QE, O * inv);
   }
 }
 
@@ -628,7 +742,7 @@ constexpr int kWavesPerCU = 8;  // resident decode waves per CU the automatic ra
 
 // Waves per workgroup: the largest of 4, 3, 2, 1 dividing num_kv_heads.
 int waves_per_wg(int32_t num_kv_heads) {
-  for (int w = 4; w > 1; --w)
+  for (int w = kMaxWavesPerWG; w > 1; --w)
     if (num_kv_heads % w == 0) return w;
   return 1;
 }
@@ -674,7 +788,7 @@ int launch(const DecodeArgs& a, uint32_t flags, hipStream_t s) {
   }
   if (flags & INT8KV_DECODE_MERGE) {
     dim3 grid((unsigned)a.batch, (unsigned)a.num_kv_heads);
-    hipLaunchKernelGGL((merge_kernel<CACHE, QT>), grid, dim3(kHeadDim), 0, s, a);
+    hipLaunchKernelGGL((merge_kernel<CACHE, QT>), grid, dim3(4 * kWave), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }
@@ -793,6 +907,7 @@ extern "C" int int8kv_paged_decode(
   a.width = (int32_t)table_width;
   a.max_ranges = num_ranges;
   a.min_tiles = min_tiles;
+  a.tile_tokens = kBlock * (cache_dtype == INT8KV_I8 ? tile_blocks<kI8>() : tile_blocks<kBF16>());
   a.bt_is64 = table_dtype == INT8KV_I64;
   a.sl_is64 = seq_lens_dtype == INT8KV_I64;
   a.sm_scale_log2e = sm_scale * kLog2e;
