@@ -109,3 +109,29 @@ def test_synthetic_generators():
     assert int(slots[21]) == int(bt[2, 0]) * 16 + 0 and int(slots[37]) == int(bt[2, 1]) * 16 + 0
     r = syn.ragged_lengths(64, 32768, 3)
     assert r.min() >= 1 and r.max() <= 32768
+
+
+def test_reference_module_aliases():
+    """Unmodified reference callers import the operators from src.triton_ops.* (see
+    vllm_int8/vllm_int8_attention_patch.py:8-10); the aliases must bind those names here."""
+    import sys
+
+    from int8kv import compat
+
+    saved = {k: sys.modules.get(k) for k in ("src", "src.triton_ops", *compat.ALIASES)}
+    try:
+        names = compat.install_reference_aliases()
+        assert sorted(names) == sorted(compat.ALIASES)
+        from src.triton_ops.bf16_paged_attention import bf16_paged_attention
+        from src.triton_ops.int8_cache_write import int8_kv_cache_write
+        from src.triton_ops.int8_paged_attention import int8_paged_attention
+
+        assert int8_paged_attention is int8kv.int8_paged_attention
+        assert int8_kv_cache_write is int8kv.int8_kv_cache_write
+        assert bf16_paged_attention is int8kv.bf16_paged_attention
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                sys.modules.pop(k, None)
+            else:
+                sys.modules[k] = v
