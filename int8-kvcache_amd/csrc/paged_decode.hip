@@ -20,8 +20,8 @@
 //     A sequence cut by range bounds leaves (max, sum, accumulator) partials in the workspace,
 //     at most two per range and head; merge_kernel combines them.
 //   * Per 32-token tile and wave:  S^T = K * Q^T  (2 x 4 MFMA 16x16x32; rows = tokens, cols =
-//     heads), online softmax in the exp2 domain, then out^T += V^T * P^T (8 MFMA 16x16x32;
-//     rows = head_dim, cols = heads).  The MFMA accumulator layout puts one head per lane
+//     heads), online softmax in the exp2 domain, then out^T += V^T * P^T (2 x 8 MFMA 16x16x32,
+//     P split into 16-bit hi + lo parts; rows = head_dim, cols = heads).  The MFMA accumulator layout puts one head per lane
 //     column, so the probabilities never leave registers.  The next tile's loads are in flight
 //     while a tile is computed; block-table entries are read 64 at a time into one register
 //     (one lane per block) ahead of use, so no table read sits on the tile critical path.
@@ -261,14 +261,17 @@ __device__ __forceinline__ void issue_v(VTile<CACHE, NB>& r, const char* vb,
 }
 
 // Scores of one tile (NB cache blocks) and the online-softmax update: rescales acc/l_part when
-// the running max moves and returns the P^T operands (one per MFMA k-step of 32 tokens).
+// the running max moves and returns the P^T operands (one per MFMA k-step of 32 tokens) as a
+// hi + lo pair of 16-bit values (p = hi + lo to about 2^-22 relative), so that P*V on the
+// 16-bit matrix cores keeps fp32 accuracy: the rounding of p would otherwise dominate the error
+// (2^-12 relative for fp16, 2^-9 for bf16).
 //   valid: number of tokens of this tile inside the sequence (1..16 NB).
 template <int CACHE, int NB>
 __device__ __forceinline__ void tile_scores(const KTile<CACHE, NB>& r,
                                             const typename MfmaOp<CACHE>::T (&qop)[4],
                                             f32x4 (&acc)[8], float& m_run, float& l_part,
                                             int valid, int lg, float s_scale,
-                                            typename MfmaOp<CACHE>::T (&pop)[NB / 2]) {
+                                            typename MfmaOp<CACHE>::T (&pop)[NB / 2][2]) {
   typedef typename MfmaOp<CACHE>::T OpT;
   constexpr int kTileTokens = NB * kBlock;
   // ---- scores S^T[token][head] for each block of the tile ----
@@ -317,11 +320,14 @@ __device__ __forceinline__ void tile_scores(const KTile<CACHE, NB>& r,
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
   }
+  typedef typename MfmaOp<CACHE>::E E;
 #pragma unroll
   for (int e = 0; e < 4 * NB; ++e) {
     const float pe = exp2_fast(sv[e] - m_run);
     l_part += pe;
-    pop[e / 8][e % 8] = (typename MfmaOp<CACHE>::E)pe;
+    const E hi = (E)pe;
+    pop[e / 8][0][e % 8] = hi;
+    pop[e / 8][1][e % 8] = (E)(pe - (float)hi);
   }
 }
 
@@ -330,7 +336,7 @@ __device__ __forceinline__ void tile_scores(const KTile<CACHE, NB>& r,
 // kst is token (block 2 kst + e / 4, row 4g + e % 4), matching the P^T operands.
 template <int CACHE, int NB>
 __device__ __forceinline__ void tile_pv(VTile<CACHE, NB>& r,
-                                        const typename MfmaOp<CACHE>::T (&pop)[NB / 2],
+                                        const typename MfmaOp<CACHE>::T (&pop)[NB / 2][2],
                                         f32x4 (&acc)[8], int valid, int lg) {
   typedef typename MfmaOp<CACHE>::T OpT;
   if constexpr (CACHE != kI8) {
@@ -369,7 +375,8 @@ __device__ __forceinline__ void tile_pv(VTile<CACHE, NB>& r,
         w[2] = perm(kMagic, pk[1][0][hsel][bp], sel);
         w[3] = perm(kMagic, pk[1][1][hsel][bp], sel);
         const f16x8 vop = __builtin_bit_cast(f16x8, w) - (f16x8)(_Float16)1152.0f;
-        acc[dt] = mfma(vop, pop[kst], acc[dt]);
+        acc[dt] = mfma(vop, pop[kst][0], acc[dt]);
+        acc[dt] = mfma(vop, pop[kst][1], acc[dt]);
       }
     } else {
 #pragma unroll
@@ -381,7 +388,9 @@ __device__ __forceinline__ void tile_pv(VTile<CACHE, NB>& r,
         w[1] = perm(r.v[s0][3][wd], r.v[s0][2][wd], sel);
         w[2] = perm(r.v[s0 + 1][1][wd], r.v[s0 + 1][0][wd], sel);
         w[3] = perm(r.v[s0 + 1][3][wd], r.v[s0 + 1][2][wd], sel);
-        acc[dt] = mfma(__builtin_bit_cast(OpT, w), pop[kst], acc[dt]);
+        const OpT vop = __builtin_bit_cast(OpT, w);
+        acc[dt] = mfma(vop, pop[kst][0], acc[dt]);
+        acc[dt] = mfma(vop, pop[kst][1], acc[dt]);
       }
     }
   }
@@ -502,7 +511,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     KTile<CACHE, NB> ka, kb2;
     VTile<CACHE, NB> va, vb2;
     int64_t pha[NB], phb[NB];
-    OpT pop[NB / 2];
+    OpT pop[NB / 2][2];
     const int64_t last = c1 - 1;
     int64_t t = c0;
     blocks_of(t, pha);

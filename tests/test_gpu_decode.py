@@ -200,3 +200,18 @@ def test_write_then_decode_end_to_end(cuda):
                                 c.block_tables.numpy(), c.seq_lens.numpy(), c.k_scale.numpy(),
                                 c.v_scale.numpy())
     _check(out, ref, "write->decode")
+
+
+@pytest.mark.parametrize("lens", [[512], [1, 4096, 3, 777, 2048, 1500]])
+def test_fp32_query_is_fp32_accurate(cuda, lens):
+    """With an fp32 query (and so fp32 output) the kernel matches the fp32 oracle to ~1e-5: the
+    scores are exact products accumulated in fp32 and P*V uses a hi + lo split of P."""
+    c = decode_case(lens, seed=21)
+    q = c.query.float()
+    q_d, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    out = int8kv.int8_paged_attention(q.to(cuda), kc, vc, bt, sl, ks, vs)
+    torch.cuda.synchronize()
+    ref = oracle_int8(c, query=q)
+    err, cos, _ = metrics(out.cpu().numpy(), ref)
+    print(f"fp32 {lens}: max|diff|={err:.3e} cos={cos:.9f}", flush=True)
+    assert err <= 1e-4 and cos >= 0.9999999

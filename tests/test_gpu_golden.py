@@ -41,10 +41,14 @@ def test_write_kernel_matches_golden_codes(cuda, golden, layer):  # noqa: F811
 
 @pytest.mark.parametrize("layer", LAYERS)
 @pytest.mark.parametrize("num_splits", [None, 1, 3])
-def test_decode_kernel_matches_golden(cuda, golden, layer, num_splits):  # noqa: F811
+@pytest.mark.parametrize("qdtype", [torch.float32, torch.bfloat16])
+def test_decode_kernel_matches_golden(cuda, golden, layer, num_splits, qdtype):  # noqa: F811
+    """The output has the query's dtype.  With an fp32 query (the bf16 values widened exactly) the
+    bar is the north-star one; a bf16 output adds its own rounding (up to 2^-8 of |out|; layer 27's
+    outputs reach 49, where a bf16 ulp is 0.25)."""
     out_ref = golden[f"l{layer}_out"]
     rows = out_ref.shape[0]
-    q = torch.from_numpy(golden[f"l{layer}_q_bf16_bits"]).view(torch.bfloat16)
+    q = torch.from_numpy(golden[f"l{layer}_q_bf16_bits"]).view(torch.bfloat16).to(qdtype)
     kc, vc, bt, sl = paged_from_dense(golden[f"l{layer}_kq"][:rows], golden[f"l{layer}_vq"][:rows],
                                       seed=10 + layer)
     ks = torch.from_numpy(golden["k_scale"][layer].copy()).to(cuda)
@@ -53,7 +57,13 @@ def test_decode_kernel_matches_golden(cuda, golden, layer, num_splits):  # noqa:
                                       torch.from_numpy(bt).to(cuda), torch.from_numpy(sl).to(cuda), ks, vs,
                                       num_splits=num_splits)
     torch.cuda.synchronize()
+    assert out.dtype == qdtype
     got = out.float().cpu().numpy()
     err, cos, _ = metrics(got, out_ref)
-    print(f"layer {layer} splits={num_splits}: max|diff|={err:.3e} cos={cos:.7f}", flush=True)
-    assert err <= MAX_ABS and cos >= MIN_COS
+    print(f"layer {layer} splits={num_splits} {qdtype}: max|diff|={err:.3e} cos={cos:.7f}", flush=True)
+    assert cos >= MIN_COS
+    if qdtype == torch.float32:
+        assert err <= MAX_ABS
+    else:
+        excess = np.abs(got - out_ref) - (MAX_ABS + np.abs(out_ref) * 2.0 ** -8)
+        assert excess.max() <= 0, f"beyond 2e-2 + bf16 rounding by {excess.max():.3e}"
