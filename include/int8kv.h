@@ -58,6 +58,7 @@ enum int8kv_dtype {
 #define INT8KV_DECODE_MAIN 1u   /* run the range decode kernel */
 #define INT8KV_DECODE_MERGE 2u  /* run the split merge kernel */
 #define INT8KV_DECODE_ALL 3u
+#define INT8KV_DECODE_QUANTIZE_Q 4u  /* quantise q to int8 per (sequence, head) first */
 
 /*
  * Static per-head INT8 quantisation of K and V plus the slot_mapping scatter into the paged
@@ -124,14 +125,19 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *                 16-byte aligned.
  *   workspace:    at least int8kv_decode_workspace_bytes(...) bytes, 16-byte aligned; it needs
  *                 no initialisation.
- *   num_ranges:   the 32-token tiles of all sequences form one stream per kv head, cut into
- *                 P = min(num_ranges, ceil(tiles / min_tiles)) equal ranges, one workgroup
+ *   num_ranges:   the 32-token tiles of all sequences (each non-empty sequence also charged
+ *                 a fixed start cost) form one stream per kv head, cut into
+ *                 P = min(num_ranges, ceil(units / min_tiles)) equal ranges, one workgroup
  *                 each; a sequence cut by range bounds is combined by the merge kernel.
  *                 0 = automatic (int8kv_decode_auto_ranges).  num_ranges = batch gives one
  *                 range per sequence when all lengths are equal (a single pass).
  *   min_tiles:    smallest range in tiles (0 = automatic, 2).
  *   flags:        INT8KV_DECODE_ALL normally; MAIN and MERGE separately let a caller time the
  *                 two kernels on their own (MERGE must follow MAIN with identical arguments).
+ *                 OR INT8KV_DECODE_QUANTIZE_Q to quantise each (sequence, query head) row of q
+ *                 to int8 first, as the reference's quantize_q=True
+ *                 (src/triton_ops/int8_paged_attention.py:137-146): q_scale = max(absmax/127,
+ *                 1e-6), q8 = clamp(round_half_away_from_zero(q / q_scale), -127, 127).
  *
  * Supported sizes: head_dim = 128, block_size = 16, group = num_q_heads / num_kv_heads in
  * [1, 16].  Other sizes return INT8KV_E_SHAPE.

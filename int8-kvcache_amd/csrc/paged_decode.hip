@@ -32,6 +32,8 @@
 //   * A running max is only moved when a tile's max exceeds it by more than 8 (log2 units), so
 //     most tiles skip the accumulator rescale; probabilities are then <= 2^8 (fits fp16/bf16).
 
+#include <type_traits>
+
 #include "int8kv_common.h"
 
 namespace int8kv {
@@ -74,7 +76,9 @@ struct DecodeArgs {
   int32_t group;
   int32_t width;       // block-table width in blocks
   int32_t max_ranges;  // P upper bound (= grid.x of decode_kernel)
-  int32_t min_tiles;   // P <= ceil(T / min_tiles)
+  int32_t min_tiles;   // P <= ceil(U / min_tiles)
+  int32_t seq_cost;    // stream units charged for starting a sequence (see make_plan)
+  int32_t quantize_q;  // quantise q per (sequence, head) to int8 first (the reference's option)
   int32_t tile_tokens;  // 16 * tile_blocks<CACHE>()
   int32_t bt_is64;
   int32_t sl_is64;
@@ -105,8 +109,11 @@ __device__ __forceinline__ int64_t readlane64(int64_t x, int lane) {
 
 // ------------------------------------------------------------------------ work plan
 // Sequence b's token count L_b = clamp(seq_lens[b], 0, width * 16) and tile count
-// n_b = ceil(L_b / tile_tokens); T = sum_b n_b; P = clamp(ceil(T / min_tiles), 1, max_ranges);
-// range r covers stream tiles [r * T / P, (r + 1) * T / P).
+// n_b = ceil(L_b / tile_tokens).  The batch becomes a stream of units: a non-empty sequence
+// contributes seq_cost "start" units (the latency of its first block ids and tiles, which a
+// range pays again for every sequence it starts) followed by its n_b tiles.  With U units in
+// all, P = clamp(ceil(U / min_tiles), 1, max_ranges) and range r covers units
+// [r * U / P, (r + 1) * U / P), so every workgroup gets the same cost whatever the lengths.
 __device__ __forceinline__ int64_t seq_len_of(const DecodeArgs& a, int64_t b) {
   if (b >= a.batch) return 0;
   int64_t L = load_index(a.sl, b, a.sl_is64);
@@ -118,25 +125,35 @@ __device__ __forceinline__ int64_t tiles_of(const DecodeArgs& a, int64_t L) {
   return (L + a.tile_tokens - 1) / a.tile_tokens;
 }
 
+__device__ __forceinline__ int64_t units_of(const DecodeArgs& a, int64_t n) {
+  return n > 0 ? n + a.seq_cost : 0;
+}
+
 struct Plan {
-  int64_t T;
+  int64_t U;
   int64_t P;
 };
 
 __device__ __forceinline__ Plan make_plan(const DecodeArgs& a, int lane) {
-  int64_t T = 0;
-  for (int64_t base = 0; base < a.batch; base += kWave) T += wave_sum(tiles_of(a, seq_len_of(a, base + lane)));
-  int64_t P = (T + a.min_tiles - 1) / a.min_tiles;
+  int64_t U = 0;
+  for (int64_t base = 0; base < a.batch; base += kWave)
+    U += wave_sum(units_of(a, tiles_of(a, seq_len_of(a, base + lane))));
+  int64_t P = (U + a.min_tiles - 1) / a.min_tiles;
   P = P < 1 ? 1 : (P > a.max_ranges ? a.max_ranges : P);
-  return {T, P};
+  return {U, P};
 }
 
-__device__ __forceinline__ int64_t range_start(const Plan& p, int64_t r) { return r * p.T / p.P; }
+__device__ __forceinline__ int64_t range_start(const Plan& p, int64_t r) { return r * p.U / p.P; }
 
-// The range holding stream tile x (0 <= x < T): the largest r with range_start(r) <= x.
+// The range holding stream unit x (0 <= x < U): the largest r with range_start(r) <= x.
 __device__ __forceinline__ int64_t range_of(const Plan& p, int64_t x) {
-  return ((x + 1) * p.P - 1) / p.T;
+  return ((x + 1) * p.P - 1) / p.U;
 }
+
+// Partial-record slot of a sequence cut by a range: 0 if it started in an earlier range, 1 if
+// it starts in this range and continues after it.  A range cuts at most one sequence of each
+// kind (its first and its last), so the two slots never collide.
+__device__ __forceinline__ int64_t cut_slot(int64_t first_tile) { return first_tile > 0 ? 0 : 1; }
 
 // ------------------------------------------------------------------------ tile registers
 // Registers holding the K or the V half of one tile (NB cache blocks) for one lane.
@@ -396,35 +413,83 @@ __device__ __forceinline__ void tile_pv(VTile<CACHE, NB>& r,
   }
 }
 
-// Q^T operand of one wave: lane (head li, group lg) holds q[li][32lg + 8ks + e].  Returns the
-// fp32 factor that turns the MFMA scores into log2-domain logits.
-template <int CACHE, int QT>
-__device__ __forceinline__ float load_query(const DecodeArgs& a, int64_t b, int kvh, int li,
-                                            int lg, typename MfmaOp<CACHE>::T (&qop)[4]) {
+// Raw query row piece of one lane: head li, elements [32 lg, 32 lg + 32) as loaded.
+template <int QT>
+struct QueryRaw {
+  u32x4 w[4];  // 32 16-bit elements
+};
+template <>
+struct QueryRaw<kF32> {
+  f32x4 w[8];  // 32 fp32 elements
+};
+
+// Issues the query loads (no wait): lane (head li, group lg) fetches q[b, kvh * G + li,
+// 32 lg .. 32 lg + 31]; lanes of padding heads (li >= G) hold zeros.
+template <int QT>
+__device__ __forceinline__ void issue_query(const DecodeArgs& a, int64_t b, int kvh, int li,
+                                            int lg, QueryRaw<QT>& raw) {
   constexpr int QE = esize<QT>();
-  float x[4][8];
-  float amax = 0.0f;
+  typedef typename std::remove_reference<decltype(raw.w[0])>::type Vec;
+  constexpr int N = sizeof(raw.w) / sizeof(raw.w[0]);
   if (li < a.group) {
-    const char* qp =
-        a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh + 32 * lg) * QE;
+    const Vec* qp = reinterpret_cast<const Vec*>(
+        a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh + 32 * lg) * QE);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      load8_f32<QT>(qp + 8 * ks * QE, x[ks]);
+    for (int i = 0; i < N; ++i) raw.w[i] = qp[i];
+  } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[ks][e]));
-    }
+    for (int i = 0; i < N; ++i) raw.w[i] = (Vec)(0);
+  }
+}
+
+__device__ __forceinline__ float round_half_away(float x) {
+  return x >= 0.0f ? floorf(x + 0.5f) : -floorf(-x + 0.5f);
+}
+
+// Builds the Q^T operand (lane (li, lg) holds q[li][32 lg + 8 ks + e]) from the raw loads and
+// returns the lane's fp32 factor turning MFMA scores into log2-domain logits.
+//   * default: q is scaled by 2^e so the largest |q| of the wave lands in [2^14, 2^15) for fp16
+//     operands (exact for bf16 input, never overflows); bf16 operands take q as is;
+//   * quantize_q: per (sequence, head) q_scale = max(absmax / 127, 1e-6) and
+//     q8 = clamp(round_half_away(q / q_scale), -127, 127) (src/triton_ops/int8_paged_attention.py:
+//     137-146, :798-802); the operand is q8 and q_scale joins the score factor.
+template <int CACHE, int QT>
+__device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRaw<QT>& raw,
+                                              int kvh, typename MfmaOp<CACHE>::T (&qop)[4]) {
+  float x[4][8];
+  if constexpr (QT == kF32) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[ks][e] = raw.w[2 * ks + e / 4][e % 4];
   } else {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[ks][e] = 0.0f;
+      for (int e = 0; e < 4; ++e) unpack2<QT>(raw.w[ks][e], x[ks][2 * e], x[ks][2 * e + 1]);
   }
+  float amax = 0.0f;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[ks][e]));
   float s_scale = a.sm_scale_log2e;
   if constexpr (CACHE == kI8) s_scale *= fmaxf(a.k_scale[kvh], 1e-6f);
+  if (a.quantize_q) {
+    // absmax over the head's 128 elements: the 4 lanes (li, lg = 0..3) of this head column
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const float qs = fmaxf(amax / 127.0f, 1e-6f);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        qop[ks][e] = (typename MfmaOp<CACHE>::E)fminf(fmaxf(round_half_away(x[ks][e] / qs), -127.0f),
+                                                      127.0f);
+    return s_scale * qs;
+  }
   float qmul = 1.0f;
   if constexpr (CACHE != kBF16) {
-    // fp16 operands: scale q by 2^e so that the largest |q| of the wave lands in [2^14, 2^15).
-    // A power of two is exact, and the range of fp16 is never exceeded.
     amax = fmaxf(amax, __shfl_xor(amax, 1));
     amax = fmaxf(amax, __shfl_xor(amax, 2));
     amax = fmaxf(amax, __shfl_xor(amax, 4));
@@ -460,6 +525,18 @@ __device__ __forceinline__ void stage_block_ids(const DecodeArgs& a, int32_t* id
   }
 }
 
+// Output rows of an empty sequence: zeros for the kv head's query heads (one wave).
+template <int QT>
+__device__ __forceinline__ void write_zero_rows(const DecodeArgs& a, int64_t b, int kvh, int lane) {
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  if (li >= a.group) return;
+  char* op = a.out + (b * a.o_sb + (int64_t)(kvh * a.group + li) * a.o_sh) * esize<QT>();
+  const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) store8<QT>(op + (32 * lg + 8 * rr) * esize<QT>(), z);
+}
+
 // Processes tiles [ta, tb) of sequence b (length L) for kv head kvh with one wave, then writes
 // either the final output (full == true) or a partial record.  ids: this wave's LDS slots.
 template <int CACHE, int QT>
@@ -470,9 +547,6 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   const int li = lane & 15;
   const int lg = lane >> 4;
   const int G = a.group;
-
-  OpT qop[4];
-  const float s_scale = load_query<CACHE, QT>(a, b, kvh, li, lg, qop);
 
   f32x4 acc[8];
 #pragma unroll
@@ -491,35 +565,51 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     return v >= kTileTokens ? kTileTokens : (int)v;
   };
 
-  for (int64_t c0 = ta; c0 < tb; c0 += kChunkTiles) {
-    const int64_t c1 = (tb - c0 > kChunkTiles) ? c0 + kChunkTiles : tb;
-    stage_block_ids<NB>(a, ids, b, c0, c1, nblk, lane);
-      // Block ids come from LDS (the LDS counter), so the waits on tile loads below only ever
-    // count tile loads.
-    auto blocks_of = [&](int64_t t, int64_t (&ph)[NB]) {
-      const int j = NB * (int)(t - c0);
+  // The tiles are processed in chunks of at most kChunkTiles whose block ids are staged in LDS
+  // (read through the LDS counter, so the waits on tile loads below only ever count tile loads).
+  int64_t c0 = ta;
+  int64_t c1 = (tb - c0 > kChunkTiles) ? c0 + kChunkTiles : tb;
+  auto blocks_of = [&](int64_t t, int64_t (&ph)[NB]) {
+    const int j = NB * (int)(t - c0);
 #pragma unroll
-      for (int s = 0; s < NB; ++s) ph[s] = __builtin_amdgcn_readfirstlane(ids[j + s]);
-    };
+    for (int s = 0; s < NB; ++s) ph[s] = __builtin_amdgcn_readfirstlane(ids[j + s]);
+  };
 
-    // Two K and two V register buffers, refilled as soon as they are consumed: K(t + 2) is
-    // requested right after the scores of tile t, V(t + 2) right after its P*V, so up to two
-    // tiles of loads are in flight while a tile is computed.  The loop body handles a pair of
-    // tiles as one straight-line block and every load in it is unconditional (a request past
-    // the chunk repeats its last tile, which the caches still hold), so the compiler's wait
-    // counts are exact and no wait drains the pipeline.
-    KTile<CACHE, NB> ka, kb2;
-    VTile<CACHE, NB> va, vb2;
-    int64_t pha[NB], phb[NB];
-    OpT pop[NB / 2][2];
-    const int64_t last = c1 - 1;
-    int64_t t = c0;
-    blocks_of(t, pha);
+  // Two K and two V register buffers, refilled as soon as they are consumed: K(t + 2) is
+  // requested right after the scores of tile t, V(t + 2) right after its P*V, so up to two
+  // tiles of loads are in flight while a tile is computed.  The loop body handles a pair of
+  // tiles as one straight-line block and every load in it is unconditional (a request past the
+  // chunk repeats its last tile, which the caches still hold), so the compiler's wait counts
+  // are exact and no wait drains the pipeline.
+  KTile<CACHE, NB> ka, kb2;
+  VTile<CACHE, NB> va, vb2;
+  int64_t pha[NB], phb[NB];
+  OpT pop[NB / 2][2];
+  auto chunk_prologue = [&]() {
+    stage_block_ids<NB>(a, ids, b, c0, c1, nblk, lane);
+    blocks_of(c0, pha);
     issue_k<CACHE, NB>(ka, kb, pha, a, li, lg);
     issue_v<CACHE, NB>(va, vb, pha, a, li, lg);
-    blocks_of(t + 1 < c1 ? t + 1 : last, phb);
+    blocks_of(c0 + 1 < c1 ? c0 + 1 : c1 - 1, phb);
     issue_k<CACHE, NB>(kb2, kb, phb, a, li, lg);
     issue_v<CACHE, NB>(vb2, vb, phb, a, li, lg);
+  };
+
+  // The query, the first chunk's block ids and its first two tiles are requested back to back;
+  // the query operand is built once they are all in flight (otherwise three memory latencies
+  // would line up at every segment start).
+  OpT qop[4];
+  float s_scale;
+  {
+    QueryRaw<QT> qraw;
+    issue_query<QT>(a, b, kvh, li, lg, qraw);
+    chunk_prologue();
+    s_scale = finish_query<CACHE, QT>(a, qraw, kvh, qop);
+  }
+
+  while (true) {
+    const int64_t last = c1 - 1;
+    int64_t t = c0;
     // sched_barrier(0) keeps the compiler's scheduler from sinking the refills past the
     // compute that follows them (which would shorten the prefetch distance).
     for (; t + 1 < c1; t += 2) {
@@ -546,6 +636,10 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
       tile_scores<CACHE, NB>(ka, qop, acc, m_run, l_part, valid, lg, s_scale, pop);
       tile_pv<CACHE, NB>(va, pop, acc, valid, lg);
     }
+    if (c1 >= tb) break;
+    c0 = c1;
+    c1 = (tb - c0 > kChunkTiles) ? c0 + kChunkTiles : tb;
+    chunk_prologue();
   }
 
   l_part += __shfl_xor(l_part, 16);
@@ -592,33 +686,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
 
   const Plan plan = make_plan(a, lane);
   if (r >= plan.P) return;
-  const int64_t t0 = range_start(plan, r);
-  const int64_t t1 = range_start(plan, r + 1);
+  const int64_t u0 = range_start(plan, r);
+  const int64_t u1 = range_start(plan, r + 1);
+  const bool last_range = r == plan.P - 1;
 
-  int64_t cum = 0;  // tiles of the sequences before this 64-sequence chunk
+  int64_t cum = 0;  // units of the sequences before this 64-sequence chunk
   for (int64_t base = 0; base < a.batch; base += kWave) {
     const int64_t L = seq_len_of(a, base + lane);
     const int64_t n = tiles_of(a, L);
-    const int64_t incl = wave_inclusive_scan(n, lane) + cum;
-    const int64_t excl = incl - n;
+    const int64_t u = units_of(a, n);
+    const int64_t incl = wave_inclusive_scan(u, lane) + cum;
+    const int64_t excl = incl - u;
     const int64_t chunk_end = readlane64(incl, kWave - 1);
-    if (chunk_end > t0) {
-      uint64_t mask = __ballot(n > 0 && incl > t0 && excl < t1);
+    if (chunk_end >= u0) {
+      // Empty sequences occupy no units: the range holding their position writes their zeros.
+      uint64_t zmask = __ballot(base + lane < a.batch && n == 0 && excl >= u0 &&
+                                (excl < u1 || (last_range && excl == plan.U)));
+      while (zmask) {
+        const int j = __builtin_ctzll(zmask);
+        zmask &= zmask - 1;
+        write_zero_rows<QT>(a, base + j, kvh, lane);
+      }
+      // Sequences whose tiles (units past the start cost) meet [u0, u1).
+      uint64_t mask = __ballot(n > 0 && incl > u0 && excl + a.seq_cost < u1);
       while (mask) {
         const int j = __builtin_ctzll(mask);
         mask &= mask - 1;
-        const int64_t S = readlane64(excl, j);
+        const int64_t first = readlane64(excl, j) + a.seq_cost;  // unit of tile 0
         const int64_t nb = readlane64(n, j);
         const int64_t Lb = readlane64(L, j);
-        const int64_t ta = (t0 > S ? t0 : S) - S;
-        const int64_t te = (t1 < S + nb ? t1 : S + nb) - S;
+        const int64_t ta = (u0 > first ? u0 : first) - first;
+        const int64_t te = (u1 < first + nb ? u1 : first + nb) - first;
+        if (ta >= te) continue;
         const bool full = ta == 0 && te == nb;
-        const int64_t slot = (S + ta == t0) ? 0 : 1;
-        run_segment<CACHE, QT>(a, s_ids[wave], base + j, Lb, kvh, ta, te, full, 2 * r + slot,
-                               lane);
+        run_segment<CACHE, QT>(a, s_ids[wave], base + j, Lb, kvh, ta, te, full,
+                               2 * r + cut_slot(ta), lane);
       }
     }
-    if (chunk_end >= t1) break;
+    if (chunk_end >= u1 && !last_range) break;
     cum = chunk_end;
   }
 }
@@ -651,8 +756,7 @@ __device__ __forceinline__ float wave_sum_f(float x) {
   return x;
 }
 
-// Combines the partials of every sequence cut by range bounds and writes zeros for empty
-// sequences.  grid (batch, num_kv_heads), 4 waves; wave w merges query heads w, w + 4, ... of
+// Combines the partials of every sequence cut by range bounds.  grid (batch, num_kv_heads), 4 waves; wave w merges query heads w, w + 4, ... of
 // the kv head's group.  A wave first reduces (max, sum) over the sequence's ranges with one
 // range per lane, then accumulates the weighted partial rows with lane = (range parity,
 // 4-element column), four rows in flight per lane.
@@ -668,29 +772,22 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
   const int c4 = lane & 31;  // head_dim elements [4 c4, 4 c4 + 4)
 
   const Plan plan = make_plan(a, lane);
-  int64_t S = 0;  // stream tiles before sequence b
+  int64_t S = 0;  // stream units before sequence b
   for (int64_t base = 0; base < b; base += kWave) {
     const int64_t bb = base + lane;
-    S += wave_sum(bb < b ? tiles_of(a, seq_len_of(a, bb)) : 0);
+    S += wave_sum(bb < b ? units_of(a, tiles_of(a, seq_len_of(a, bb))) : 0);
   }
   const int64_t n = tiles_of(a, seq_len_of(a, b));
   constexpr int QE = esize<QT>();
-  if (n == 0) {
-    for (int j = wave; j < G; j += nwaves) {
-      if (rs == 0)
-        store4<QT>(a.out + (b * a.o_sb + (int64_t)(kvh * G + j) * a.o_sh + 4 * c4) * QE,
-                   (f32x4)(0.0f));
-    }
-    return;
-  }
-  const int64_t r0 = range_of(plan, S);
-  const int64_t r1 = range_of(plan, S + n - 1);
+  if (n == 0) return;  // zeros written by decode_kernel
+  const int64_t first = S + a.seq_cost;  // unit of tile 0
+  const int64_t r0 = range_of(plan, first);
+  const int64_t r1 = range_of(plan, first + n - 1);
   if (r0 == r1) return;  // finished inside one range by decode_kernel
   const int64_t nr = r1 - r0 + 1;
-  const int64_t slot0 = range_start(plan, r0) == S ? 0 : 1;
   const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
   auto row_of = [&](int64_t c, int h) -> int64_t {  // partial row of range r0 + c, head h
-    return (2 * (r0 + c) + (c == 0 ? slot0 : 0)) * a.num_q_heads + h;
+    return (2 * (r0 + c) + cut_slot(c)) * a.num_q_heads + h;  // tile 0 lies in range r0
   };
 
   for (int j = wave; j < G; j += nwaves) {
@@ -747,6 +844,7 @@ using namespace int8kv;
 namespace {
 
 constexpr int kMaxRangesLimit = 1 << 20;
+constexpr int kSeqStartCost = 2;  // stream units per sequence start (about one tile's time each)
 constexpr int kWavesPerCU = 8;  // resident decode waves per CU the automatic range count targets
 
 // Waves per workgroup: the largest of 4, 3, 2, 1 dividing num_kv_heads.
@@ -916,6 +1014,8 @@ extern "C" int int8kv_paged_decode(
   a.width = (int32_t)table_width;
   a.max_ranges = num_ranges;
   a.min_tiles = min_tiles;
+  a.seq_cost = kSeqStartCost;
+  a.quantize_q = (flags & INT8KV_DECODE_QUANTIZE_Q) != 0;
   a.tile_tokens = kBlock * (cache_dtype == INT8KV_I8 ? tile_blocks<kI8>() : tile_blocks<kBF16>());
   a.bt_is64 = table_dtype == INT8KV_I64;
   a.sl_is64 = seq_lens_dtype == INT8KV_I64;

@@ -24,7 +24,7 @@ DTYPE_CODE = {
     torch.int64: I64,
 }
 
-DECODE_MAIN, DECODE_MERGE, DECODE_ALL = 1, 2, 3
+DECODE_MAIN, DECODE_MERGE, DECODE_ALL, DECODE_QUANTIZE_Q = 1, 2, 3, 4
 
 ERRORS = {
     -1: "INT8KV_E_NULL (a required pointer is NULL)",

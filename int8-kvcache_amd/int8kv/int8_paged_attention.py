@@ -16,14 +16,17 @@ libint8kv.so.  Differences that a caller can observe:
   (:767-768).
 * ``num_splits``: an integer S asks for S splits per sequence, i.e. S * B ranges (the reference
   splits the logical blocks of the longest sequence into S ranges, :156-162).
-* ``num_warps`` is accepted and ignored; ``quantize_q=True`` raises NotImplementedError.
+* ``quantize_q=True`` quantises each (sequence, query head) row of q to int8 first, as the
+  reference does (:137-146, :798-802): q_scale = max(absmax / 127, 1e-6),
+  q8 = clamp(round_half_away_from_zero(q / q_scale), -127, 127), scores scaled by q_scale.
+* ``num_warps`` is accepted and ignored.
 """
 
 from __future__ import annotations
 
 import torch
 
-from . import _decode
+from . import _decode, _lib
 
 
 def int8_paged_attention(
@@ -61,8 +64,6 @@ def int8_paged_attention(
     assert all(t.device == query.device for t in tensors), "all tensors must be on one device"
     if impl not in ("auto", "v3", "v4"):
         raise ValueError(f"Unknown impl={impl!r}; expected 'auto', 'v3' or 'v4'")
-    if quantize_q:
-        raise NotImplementedError("quantize_q=True is not implemented by the HIP kernels yet")
     if _decode.DEBUG_CHECKS:
         _decode.debug_check(block_tables, seq_lens, num_blocks, block_size, True)
 
@@ -72,6 +73,8 @@ def int8_paged_attention(
         num_splits = 1
     ranges = _decode.ranges_for(B, num_splits)
     output = torch.empty((B, Hq, D), device=query.device, dtype=query.dtype)
+    flags = _lib.DECODE_ALL | (_lib.DECODE_QUANTIZE_Q if quantize_q else 0)
     return _decode.paged_decode(
-        query, key_cache, value_cache, block_tables, seq_lens, k_scale, v_scale, output, ranges
+        query, key_cache, value_cache, block_tables, seq_lens, k_scale, v_scale, output, ranges,
+        flags,
     )

@@ -153,6 +153,7 @@ def paged_attention_ref(
     k_scale: np.ndarray | None = None,
     v_scale: np.ndarray | None = None,
     dtype=np.float32,
+    quantize_q: bool = False,
 ) -> np.ndarray:
     """Decode attention over a paged cache -> [B, Hq, D] in ``dtype``.
 
@@ -162,6 +163,8 @@ def paged_attention_ref(
     With k_scale/v_scale None the cache is used as is (the BF16 path,
     src/triton_ops/bf16_paged_attention.py:64-111).  Scales are floored at 1e-6 like the
     kernels (:150-151).  An empty sequence yields zeros (the reference asserts len > 0).
+    quantize_q=True first replaces each query row by its int8 quantisation, dequantised
+    (:798-802): q_scale = max(absmax / 127, 1e-6), q = clamp(round_half_away(q / q_scale)) * q_scale.
     """
     B, hq, d = query.shape
     hkv = key_cache.shape[2]
@@ -180,10 +183,25 @@ def paged_attention_ref(
         if vs is not None:
             v = v * vs[None, :, None]
         for h in range(hkv):
-            out[b, h * g:(h + 1) * g] = _softmax_attend(
-                np.asarray(query[b, h * g:(h + 1) * g], np.float32), k[:, h], v[:, h], dtype
-            )
+            qh = np.asarray(query[b, h * g:(h + 1) * g], np.float32)
+            if quantize_q:
+                qh = quantize_query_rows(qh)
+            out[b, h * g:(h + 1) * g] = _softmax_attend(qh, k[:, h], v[:, h], dtype)
     return out
+
+
+def round_half_away(x: np.ndarray) -> np.ndarray:
+    """Round half away from zero (src/triton_ops/int8_paged_attention.py:772-773)."""
+    x = np.asarray(x, np.float32)
+    return np.where(x >= 0, np.floor(x + np.float32(0.5)), -np.floor(-x + np.float32(0.5)))
+
+
+def quantize_query_rows(q: np.ndarray) -> np.ndarray:
+    """Per-row int8 quantise + dequantise of q [H, D] in float32 (int8_paged_attention.py:798-802)."""
+    q = np.asarray(q, np.float32)
+    qs = np.maximum(np.abs(q).max(axis=-1, keepdims=True) / np.float32(127.0), SCALE_FLOOR)
+    q8 = np.clip(round_half_away(q / qs), -127, 127)
+    return (q8 * qs).astype(np.float32)
 
 
 def decode_bytes(seq_lens, num_kv_heads: int, head_dim: int, cache_elem: int, batch: int,

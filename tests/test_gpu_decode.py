@@ -215,3 +215,22 @@ def test_fp32_query_is_fp32_accurate(cuda, lens):
     err, cos, _ = metrics(out.cpu().numpy(), ref)
     print(f"fp32 {lens}: max|diff|={err:.3e} cos={cos:.9f}", flush=True)
     assert err <= 1e-4 and cos >= 0.9999999
+
+
+@pytest.mark.parametrize("lens", [[127, 301], [1, 4096, 3, 777]])
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float32])
+def test_quantize_q(cuda, lens, qdtype):
+    """quantize_q=True (src/triton_ops/int8_paged_attention.py:137-146, :798-802) against the
+    oracle's quantise-dequantise of every query row."""
+    c = decode_case(lens, seed=31)
+    q = c.query.to(qdtype)
+    q_d, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    out = int8kv.int8_paged_attention(q.to(cuda), kc, vc, bt, sl, ks, vs, quantize_q=True)
+    torch.cuda.synchronize()
+    ref = O.paged_attention_ref(q.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
+                                quantize_q=True)
+    _check(out, ref, f"quantize_q {lens} {qdtype}")
+    if qdtype == torch.float32:
+        err, _, _ = metrics(out.cpu().numpy(), ref)
+        assert err <= 1e-4

@@ -286,3 +286,38 @@ def test_decode_bytes_formula():
     # B=1, one 512-token sequence: 512*4*128*2 (K+V int8) + 32 table entries*4 + q/out + lens + scales
     n = O.decode_bytes([512], 4, 128, 1, 1, 28)
     assert n == 512 * 4 * 128 * 2 + 32 * 4 + 2 * 28 * 128 * 2 + 4 + 2 * 4 * 4
+
+
+def test_query_quantisation_known_answers():
+    """quantize_q rounds half away from zero (src/triton_ops/int8_paged_attention.py:772-773):
+    with absmax 127 the scale is exactly 1, so q/scale = q."""
+    q = np.array([[127.0, 2.5, -2.5, 0.5, -0.5, 1.49, -126.5, 3.0]], np.float32)
+    got = O.quantize_query_rows(q)
+    assert got.tolist() == [[127.0, 3.0, -3.0, 1.0, -1.0, 1.0, -127.0, 3.0]]
+    assert O.round_half_away(np.array([2.5, -2.5, 3.5, -0.4], np.float32)).tolist() == [3, -3, 4, -0]
+    # all-zero row: scale floor 1e-6, codes 0
+    assert (O.quantize_query_rows(np.zeros((1, 8), np.float32)) == 0).all()
+    # brute force on random rows
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((4, 16)).astype(np.float32)
+    ref = np.empty_like(x)
+    for i in range(4):
+        s = max(float(np.float32(np.abs(x[i]).max() / np.float32(127))), float(np.float32(1e-6)))
+        s = np.float32(s)
+        for j in range(16):
+            v = float(np.float32(x[i, j] / s))
+            r = math.floor(v + 0.5) if v >= 0 else -math.floor(-v + 0.5)
+            ref[i, j] = np.float32(max(-127, min(127, r)) * s)
+    assert np.array_equal(O.quantize_query_rows(x), ref)
+
+
+def test_paged_attention_quantize_q_changes_only_q():
+    rng = np.random.default_rng(11)
+    q, kc, vc, bt, sl = _random_paged(rng, [9, 20], hq=8, hkv=2, d=16, bs=4)
+    ks = np.array([0.02, 0.05], np.float32)
+    vs = np.array([0.03, 0.01], np.float32)
+    qq = np.stack([O.quantize_query_rows(q[b]) for b in range(2)])
+    a = O.paged_attention_ref(q, kc, vc, bt, sl, ks, vs, quantize_q=True)
+    b = O.paged_attention_ref(qq, kc, vc, bt, sl, ks, vs)
+    assert np.array_equal(a, b)
+    assert not np.array_equal(a, O.paged_attention_ref(q, kc, vc, bt, sl, ks, vs))
