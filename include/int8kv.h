@@ -18,6 +18,7 @@
  *
  * Reference interfaces replaced (paths relative to the cjsmt/Int8-kvcache checkout):
  *   int8kv_cache_write   <- src/triton_ops/int8_cache_write.py:85-149  (int8_kv_cache_write)
+ *   int8kv_dynamic_cache_write <- vllm_int8/vllm_int8_cache_ops.py:134-210 (reshape_and_cache_int8)
  *   int8kv_paged_decode  <- src/triton_ops/int8_paged_attention.py:683-769 (int8_paged_attention,
  *                           the V4 kernel :61-327 plus the split merge :330-388) and
  *                           src/triton_ops/bf16_paged_attention.py:118-165 (bf16_paged_attention)
@@ -84,6 +85,33 @@ int int8kv_cache_write(const void* key, const void* value, int src_dtype, int64_
                        int64_t num_blocks, int32_t block_size, const int64_t key_cache_strides[4],
                        const int64_t value_cache_strides[4], const void* slot_mapping,
                        int slot_dtype, const float* k_scale, const float* v_scale, void* stream);
+
+/*
+ * Dynamic per-(token, head) INT8 quantisation of K and V plus the slot_mapping scatter, with the
+ * scales stored beside the codes (replaces reshape_and_cache_int8 and its Triton kernel,
+ * vllm_int8/vllm_int8_cache_ops.py:13-210):
+ *
+ *   for every token t with s = slot_mapping[t] in [0, num_blocks * block_size), every head h:
+ *     scale = max(absmax(key[t, h, :]) / 127, 1e-6)                       (IEEE fp32)
+ *     key_cache[s / block_size, s % block_size, h, :] =
+ *         round_half_away_from_zero(clamp(key[t, h, :] / scale, -127, 127))
+ *     k_scale_cache[s / block_size, s % block_size, h] = scale
+ *   (value likewise into value_cache / v_scale_cache).  Tokens with s < 0 (or past the cache)
+ *   are skipped; nothing else is written.
+ *
+ *   Layouts as int8kv_cache_write; k_scale_cache/v_scale_cache: fp32 [num_blocks, block_size,
+ *   num_kv_heads], any element strides.  head_dim / 8 must be a power of two <= 64
+ *   (head_dim in {8, 16, ..., 512}).
+ */
+int int8kv_dynamic_cache_write(const void* key, const void* value, int src_dtype,
+                               int64_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                               const int64_t key_strides[3], const int64_t value_strides[3],
+                               void* key_cache, void* value_cache, int64_t num_blocks,
+                               int32_t block_size, const int64_t key_cache_strides[4],
+                               const int64_t value_cache_strides[4], float* k_scale_cache,
+                               float* v_scale_cache, const int64_t k_scale_cache_strides[3],
+                               const int64_t v_scale_cache_strides[3], const void* slot_mapping,
+                               int slot_dtype, void* stream);
 
 /*
  * Automatic range count of int8kv_paged_decode (num_ranges = 0) on the current device: the

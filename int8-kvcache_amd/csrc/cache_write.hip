@@ -82,6 +82,86 @@ __global__ __launch_bounds__(256) void cache_write_kernel(WriteArgs a) {
   *reinterpret_cast<u32x2*>(a.vc + blk * a.vc_sb + off * a.vc_ss + h * a.vc_sh + 8 * dv) = vq;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Dynamic per-(token, head) INT8 write (replaces the Triton kernel
+// vllm_int8/vllm_int8_cache_ops.py:13-131): scale = max(absmax(x[t, h, :]) / 127, 1e-6),
+// q = clamp(x / scale, -127, 127) rounded half away from zero, codes and the fp32 scale stored at
+// the slot.  Same lane mapping as the static write: vecs_per_row lanes (a power of two) own one
+// (token, head) row of K and V, 8 elements each; the row absmax is a butterfly over those lanes.
+struct DynWriteArgs {
+  WriteArgs w;
+  float* ksc;
+  float* vsc;
+  int64_t ksc_sb, ksc_ss, ksc_sh;  // element strides of the [NB, BS, Hkv] scale caches
+  int64_t vsc_sb, vsc_ss, vsc_sh;
+};
+
+__device__ __forceinline__ float round_half_away(float x) {
+  return x >= 0.0f ? floorf(x + 0.5f) : ceilf(x - 0.5f);
+}
+
+__device__ __forceinline__ uint32_t quant4_dyn(const float* x, float s) {
+  uint32_t w = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // IEEE fp32 quotient, clamped before rounding as the reference kernel does (:80-92).
+    float q = fminf(fmaxf(x[i] / s, -127.0f), 127.0f);
+    q = round_half_away(q);
+    w |= ((uint32_t)((int32_t)q) & 0xffu) << (8 * i);
+  }
+  return w;
+}
+
+__device__ __forceinline__ float row_absmax(const float* x, int lanes_per_row) {
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(x[i]));
+  for (int o = 1; o < lanes_per_row; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  return m;
+}
+
+template <int SRC>
+__global__ __launch_bounds__(256) void dynamic_write_kernel(DynWriteArgs d) {
+  const WriteArgs& a = d.w;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t rows = a.num_tokens * a.num_kv_heads;
+  const int64_t row = gid / a.vecs_per_row;
+  // Whole rows share a wave (vecs_per_row divides 64), so a row's lanes agree on every branch
+  // below and the butterfly only mixes lanes of one row.
+  const bool in_range = row < rows;
+  const int dv = (int)(gid - row * a.vecs_per_row);
+  const int h = in_range ? (int)(row % a.num_kv_heads) : 0;
+  const int64_t t = in_range ? row / a.num_kv_heads : 0;
+  constexpr int esize = SRC == kF32 ? 4 : 2;
+
+  float x[8], y[8];
+  if (in_range) {
+    load8_f32<SRC>(a.key + (t * a.k_st + h * a.k_sh + 8 * dv) * esize, x);
+    load8_f32<SRC>(a.value + (t * a.v_st + h * a.v_sh + 8 * dv) * esize, y);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = y[i] = 0.0f;
+  }
+  const float ks = fmaxf(row_absmax(x, a.vecs_per_row) / 127.0f, 1e-6f);
+  const float vs = fmaxf(row_absmax(y, a.vecs_per_row) / 127.0f, 1e-6f);
+  if (!in_range) return;
+  const int64_t slot = load_index(a.slots, t, a.slots_is64);
+  if (slot < 0 || slot >= a.capacity) return;
+  const int64_t blk = slot / a.block_size;
+  const int64_t off = slot - blk * a.block_size;
+  u32x2 kq, vq;
+  kq[0] = quant4_dyn(x, ks);
+  kq[1] = quant4_dyn(x + 4, ks);
+  vq[0] = quant4_dyn(y, vs);
+  vq[1] = quant4_dyn(y + 4, vs);
+  *reinterpret_cast<u32x2*>(a.kc + blk * a.kc_sb + off * a.kc_ss + h * a.kc_sh + 8 * dv) = kq;
+  *reinterpret_cast<u32x2*>(a.vc + blk * a.vc_sb + off * a.vc_ss + h * a.vc_sh + 8 * dv) = vq;
+  if (dv == 0) {
+    d.ksc[blk * d.ksc_sb + off * d.ksc_ss + h * d.ksc_sh] = ks;
+    d.vsc[blk * d.vsc_sb + off * d.vsc_ss + h * d.vsc_sh] = vs;
+  }
+}
+
 }  // namespace int8kv
 
 using namespace int8kv;
@@ -90,14 +170,15 @@ static bool aligned(const void* p, int64_t stride_bytes, int64_t align) {
   return ((uintptr_t)p % align) == 0 && (stride_bytes % align) == 0;
 }
 
-extern "C" int int8kv_cache_write(const void* key, const void* value, int src_dtype,
-                                  int64_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
-                                  const int64_t key_strides[3], const int64_t value_strides[3],
-                                  void* key_cache, void* value_cache, int64_t num_blocks,
-                                  int32_t block_size, const int64_t key_cache_strides[4],
-                                  const int64_t value_cache_strides[4], const void* slot_mapping,
-                                  int slot_dtype, const float* k_scale, const float* v_scale,
-                                  void* stream) {
+namespace {
+
+// Validates the arguments shared by the static and the dynamic write and fills WriteArgs.
+int prepare_write(WriteArgs& a, const void* key, const void* value, int src_dtype,
+                  int64_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                  const int64_t key_strides[3], const int64_t value_strides[3], void* key_cache,
+                  void* value_cache, int64_t num_blocks, int32_t block_size,
+                  const int64_t key_cache_strides[4], const int64_t value_cache_strides[4],
+                  const void* slot_mapping, int slot_dtype) {
   if (!key_strides || !value_strides || !key_cache_strides || !value_cache_strides)
     return INT8KV_E_NULL;
   if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 8 != 0 ||
@@ -107,8 +188,7 @@ extern "C" int int8kv_cache_write(const void* key, const void* value, int src_dt
     return INT8KV_E_DTYPE;
   if (slot_dtype != INT8KV_I32 && slot_dtype != INT8KV_I64) return INT8KV_E_DTYPE;
   if (num_tokens == 0) return INT8KV_OK;
-  if (!key || !value || !key_cache || !value_cache || !slot_mapping || !k_scale || !v_scale)
-    return INT8KV_E_NULL;
+  if (!key || !value || !key_cache || !value_cache || !slot_mapping) return INT8KV_E_NULL;
 
   // Each lane loads 8 source elements with 16-byte vector loads.
   const int64_t esize = src_dtype == INT8KV_F32 ? 4 : 2;
@@ -124,15 +204,13 @@ extern "C" int int8kv_cache_write(const void* key, const void* value, int src_dt
         !aligned(value_cache, value_cache_strides[i], 8))
       return INT8KV_E_STRIDE;
   }
-
-  WriteArgs a;
   a.key = static_cast<const char*>(key);
   a.value = static_cast<const char*>(value);
   a.kc = static_cast<int8_t*>(key_cache);
   a.vc = static_cast<int8_t*>(value_cache);
   a.slots = slot_mapping;
-  a.k_scale = k_scale;
-  a.v_scale = v_scale;
+  a.k_scale = nullptr;
+  a.v_scale = nullptr;
   a.k_st = key_strides[0];
   a.k_sh = key_strides[1];
   a.v_st = value_strides[0];
@@ -149,6 +227,28 @@ extern "C" int int8kv_cache_write(const void* key, const void* value, int src_dt
   a.vecs_per_row = head_dim / 8;
   a.block_size = block_size;
   a.slots_is64 = slot_dtype == INT8KV_I64;
+  return 1;  // launch needed
+}
+
+}  // namespace
+
+extern "C" int int8kv_cache_write(const void* key, const void* value, int src_dtype,
+                                  int64_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                                  const int64_t key_strides[3], const int64_t value_strides[3],
+                                  void* key_cache, void* value_cache, int64_t num_blocks,
+                                  int32_t block_size, const int64_t key_cache_strides[4],
+                                  const int64_t value_cache_strides[4], const void* slot_mapping,
+                                  int slot_dtype, const float* k_scale, const float* v_scale,
+                                  void* stream) {
+  WriteArgs a;
+  const int st = prepare_write(a, key, value, src_dtype, num_tokens, num_kv_heads, head_dim,
+                               key_strides, value_strides, key_cache, value_cache, num_blocks,
+                               block_size, key_cache_strides, value_cache_strides, slot_mapping,
+                               slot_dtype);
+  if (st <= 0) return st;
+  if (!k_scale || !v_scale) return INT8KV_E_NULL;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
 
   const int64_t lanes = num_tokens * num_kv_heads * (int64_t)a.vecs_per_row;
   const int threads = 256;
@@ -164,6 +264,54 @@ extern "C" int int8kv_cache_write(const void* key, const void* value, int src_dt
       break;
     default:
       hipLaunchKernelGGL(cache_write_kernel<kBF16>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+      break;
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int int8kv_dynamic_cache_write(
+    const void* key, const void* value, int src_dtype, int64_t num_tokens, int32_t num_kv_heads,
+    int32_t head_dim, const int64_t key_strides[3], const int64_t value_strides[3],
+    void* key_cache, void* value_cache, int64_t num_blocks, int32_t block_size,
+    const int64_t key_cache_strides[4], const int64_t value_cache_strides[4],
+    float* k_scale_cache, float* v_scale_cache, const int64_t k_scale_cache_strides[3],
+    const int64_t v_scale_cache_strides[3], const void* slot_mapping, int slot_dtype,
+    void* stream) {
+  if (!k_scale_cache_strides || !v_scale_cache_strides) return INT8KV_E_NULL;
+  const int32_t vpr = head_dim / 8;
+  if (head_dim <= 0 || head_dim % 8 != 0 || vpr > kWave || (vpr & (vpr - 1)) != 0)
+    return INT8KV_E_SHAPE;  // a row's lanes must form a power-of-two group inside one wave
+  DynWriteArgs d;
+  const int st = prepare_write(d.w, key, value, src_dtype, num_tokens, num_kv_heads, head_dim,
+                               key_strides, value_strides, key_cache, value_cache, num_blocks,
+                               block_size, key_cache_strides, value_cache_strides, slot_mapping,
+                               slot_dtype);
+  if (st <= 0) return st;
+  if (!k_scale_cache || !v_scale_cache) return INT8KV_E_NULL;
+  if (((uintptr_t)k_scale_cache % 4) || ((uintptr_t)v_scale_cache % 4)) return INT8KV_E_STRIDE;
+  d.ksc = k_scale_cache;
+  d.vsc = v_scale_cache;
+  d.ksc_sb = k_scale_cache_strides[0];
+  d.ksc_ss = k_scale_cache_strides[1];
+  d.ksc_sh = k_scale_cache_strides[2];
+  d.vsc_sb = v_scale_cache_strides[0];
+  d.vsc_ss = v_scale_cache_strides[1];
+  d.vsc_sh = v_scale_cache_strides[2];
+
+  const int64_t lanes = num_tokens * num_kv_heads * (int64_t)vpr;
+  const int threads = 256;
+  const int64_t blocks = (lanes + threads - 1) / threads;
+  if (blocks > 0x7fffffffLL) return INT8KV_E_SHAPE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (src_dtype) {
+    case INT8KV_F32:
+      hipLaunchKernelGGL(dynamic_write_kernel<kF32>, dim3((unsigned)blocks), dim3(threads), 0, s, d);
+      break;
+    case INT8KV_F16:
+      hipLaunchKernelGGL(dynamic_write_kernel<kF16>, dim3((unsigned)blocks), dim3(threads), 0, s, d);
+      break;
+    default:
+      hipLaunchKernelGGL(dynamic_write_kernel<kBF16>, dim3((unsigned)blocks), dim3(threads), 0, s, d);
       break;
   }
   return (int)hipGetLastError();

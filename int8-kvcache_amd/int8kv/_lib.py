@@ -59,6 +59,11 @@ def load() -> ctypes.CDLL:
         _vp, _vp, ctypes.c_int, i64, i32, i32, _c_i64p, _c_i64p, _vp, _vp, i64, i32,
         _c_i64p, _c_i64p, _vp, ctypes.c_int, _vp, _vp, _vp,
     ]
+    lib.int8kv_dynamic_cache_write.restype = ctypes.c_int
+    lib.int8kv_dynamic_cache_write.argtypes = [
+        _vp, _vp, ctypes.c_int, i64, i32, i32, _c_i64p, _c_i64p, _vp, _vp, i64, i32,
+        _c_i64p, _c_i64p, _vp, _vp, _c_i64p, _c_i64p, _vp, ctypes.c_int, _vp,
+    ]
     lib.int8kv_decode_workspace_bytes.restype = sz
     lib.int8kv_decode_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
     lib.int8kv_decode_auto_ranges.restype = i32

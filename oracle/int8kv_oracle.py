@@ -15,6 +15,8 @@ calls it.  It is a numpy restatement of the reference's PyTorch math (cjsmt/Int8
     paged_attention_ref          src/triton_ops/int8_paged_attention.py:776-814 (fp32 output kept;
                                  the reference casts to query.dtype at :814)
     dequantize_paged_cache       src/triton_ops/int8_cache_write.py:186-189
+    reshape_and_cache_int8       vllm_int8/vllm_int8_cache_ops.py:13-131 (dynamic per-(token, head)
+                                 scales, clamp then round half away from zero)
 
 How each function is pinned (tests/test_oracle.py): known-answer tests for the rounding,
 clamping, scale floor and slot mapping; brute-force pure-Python loops on tiny inputs; closed
@@ -76,6 +78,33 @@ def int8_kv_cache_write(
     flat_v = value_cache.reshape(nb * bs, hkv, d)
     flat_k[slots[ok]] = kq
     flat_v[slots[ok]] = vq
+
+
+def reshape_and_cache_int8(
+    key: np.ndarray,
+    value: np.ndarray,
+    key_cache: np.ndarray,
+    value_cache: np.ndarray,
+    k_scale_cache: np.ndarray,
+    v_scale_cache: np.ndarray,
+    slot_mapping: np.ndarray,
+) -> None:
+    """In-place dynamic INT8 write (vllm_int8/vllm_int8_cache_ops.py:13-131).
+
+    Per token t with slot s >= 0 and head h: scale = max(absmax(x[t, h]) / 127, 1e-6) in
+    float32 (:70-79); code = round_half_away(clamp(x / scale, -127, 127)) (:80-92); codes to
+    cache[s // BS, s % BS, h] and the scale to scale_cache[s // BS, s % BS, h] (:93-131).
+    """
+    nb, bs, hkv, d = key_cache.shape
+    slots = np.asarray(slot_mapping, np.int64).reshape(-1)
+    ok = (slots >= 0) & (slots < nb * bs)
+    for src, dst, sdst in ((key, key_cache, k_scale_cache), (value, value_cache, v_scale_cache)):
+        x = np.asarray(src, np.float32)[ok]  # [n, Hkv, D]
+        scale = np.maximum(np.abs(x).max(axis=-1) / np.float32(127.0), SCALE_FLOOR)  # [n, Hkv]
+        q = np.clip(x / scale[..., None], np.float32(-127), np.float32(127))
+        code = np.where(q >= 0, np.floor(q + np.float32(0.5)), np.ceil(q - np.float32(0.5)))
+        dst.reshape(nb * bs, hkv, d)[slots[ok]] = code.astype(np.int8)
+        sdst.reshape(nb * bs, hkv)[slots[ok]] = scale.astype(np.float32)
 
 
 # --------------------------------------------------------------------------- paged layout

@@ -33,6 +33,7 @@ def test_header_declares_expected_entry_points():
         "int8kv_cache_write",
         "int8kv_decode_auto_ranges",
         "int8kv_decode_workspace_bytes",
+        "int8kv_dynamic_cache_write",
         "int8kv_paged_decode",
         "int8kv_version",
     ]
@@ -114,5 +115,27 @@ def test_write_rejects_bad_arguments_without_launching(lib):
     assert call(d=100) == -3
     assert call(key=None) == -1
     assert call(kcs=(ctypes.c_int64 * 4)(16 * 512, 512, 128, 2)) == -4
+    assert call(key=8) == -4
+    assert call(T=0) == 0
+
+
+def test_dynamic_write_rejects_bad_arguments_without_launching(lib):
+    st3 = (ctypes.c_int64 * 3)(512, 128, 1)
+    st4 = (ctypes.c_int64 * 4)(16 * 512, 512, 128, 1)
+    sc3 = (ctypes.c_int64 * 3)(64, 4, 1)
+
+    def call(**over):
+        a = dict(key=16, value=16, src=2, T=4, hkv=4, d=128, ks_=st3, vs_=st3, kc=16, vc=16,
+                 nb=4, bs=16, kcs=st4, vcs=st4, ksc=16, vsc=16, kscs=sc3, vscs=sc3, slots=16,
+                 sdt=5, stream=None)
+        a.update(over)
+        return lib.int8kv_dynamic_cache_write(*a.values())
+
+    assert call(src=3) == -2
+    assert call(d=96) == -3  # 12 lanes per row: not a power of two
+    assert call(d=1024) == -3  # more than one wave per row
+    assert call(ksc=None) == -1
+    assert call(kscs=None) == -1
+    assert call(ksc=18) == -4  # misaligned fp32 scale cache
     assert call(key=8) == -4
     assert call(T=0) == 0

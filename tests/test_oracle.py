@@ -321,3 +321,56 @@ def test_paged_attention_quantize_q_changes_only_q():
     b = O.paged_attention_ref(qq, kc, vc, bt, sl, ks, vs)
     assert np.array_equal(a, b)
     assert not np.array_equal(a, O.paged_attention_ref(q, kc, vc, bt, sl, ks, vs))
+
+
+# ----------------------------------------------------------------------------- dynamic write
+def test_dynamic_write_known_answers():
+    """vllm_int8/vllm_int8_cache_ops.py:70-92: a row whose absmax is 127 has scale 1, so codes are
+    x rounded half away from zero; an all-zero row has the 1e-6 floor and zero codes."""
+    nb, bs, hkv, d = 2, 4, 2, 8
+    key = np.zeros((3, hkv, d), np.float32)
+    key[0, 0] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.49, -126.5, 3.0]
+    key[0, 1] = [254.0, 5.0, -5.0, 1.0, -1.0, 0, 0, 0]  # scale 2 -> same codes as halves
+    value = key * 0.5
+    kc = np.full((nb, bs, hkv, d), 0x5A, np.int8)
+    vc = kc.copy()
+    ksc = np.full((nb, bs, hkv), -1.0, np.float32)
+    vsc = ksc.copy()
+    O.reshape_and_cache_int8(key, value, kc, vc, ksc, vsc, np.array([5, 2, -1]))
+    assert kc[1, 1, 0].tolist() == [127, 3, -3, 1, -1, 1, -127, 3]
+    assert kc[1, 1, 1].tolist()[:5] == [127, 3, -3, 1, -1]
+    assert ksc[1, 1].tolist() == [1.0, 2.0] and vsc[1, 1].tolist() == [0.5, 1.0]
+    assert (kc[0, 2] == 0).all() and ksc[0, 2].tolist() == [np.float32(1e-6)] * 2
+    written = np.zeros((nb, bs), bool)
+    written[1, 1] = written[0, 2] = True
+    assert (kc[~written] == 0x5A).all() and (ksc[~written] == -1.0).all()
+
+
+def test_dynamic_write_matches_brute_force():
+    rng = np.random.default_rng(4)
+    T, hkv, d, nb, bs = 7, 3, 16, 3, 4
+    key = (rng.standard_normal((T, hkv, d)) * 2).astype(np.float32)
+    value = rng.standard_normal((T, hkv, d)).astype(np.float32)
+    slots = rng.permutation(nb * bs)[:T].astype(np.int64)
+    slots[2] = -1
+    got = [np.zeros((nb, bs, hkv, d), np.int8) for _ in range(2)] + \
+        [np.zeros((nb, bs, hkv), np.float32) for _ in range(2)]
+    O.reshape_and_cache_int8(key, value, got[0], got[1], got[2], got[3], slots)
+    exp = [np.zeros((nb, bs, hkv, d), np.int8) for _ in range(2)] + \
+        [np.zeros((nb, bs, hkv), np.float32) for _ in range(2)]
+    for t in range(T):
+        s = int(slots[t])
+        if s < 0:
+            continue
+        for h in range(hkv):
+            for src, dst, sdst in ((key, exp[0], exp[2]), (value, exp[1], exp[3])):
+                amax = max(abs(float(v)) for v in src[t, h])
+                scale = np.float32(max(float(np.float32(np.float32(amax) / np.float32(127))),
+                                       float(np.float32(1e-6))))
+                sdst[s // bs, s % bs, h] = scale
+                for i in range(d):
+                    q = float(np.float32(src[t, h, i] / scale))
+                    q = max(-127.0, min(127.0, q))
+                    dst[s // bs, s % bs, h, i] = math.floor(q + 0.5) if q >= 0 else math.ceil(q - 0.5)
+    for g, e in zip(got, exp):
+        assert np.array_equal(g, e)
