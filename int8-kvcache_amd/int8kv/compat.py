@@ -21,6 +21,13 @@ ALIASES = {
     "src.triton_ops.bf16_paged_attention": "int8kv.bf16_paged_attention",
 }
 
+# The integration layer itself, for callers that import the reference's vllm_int8 modules.
+VLLM_INT8_ALIASES = {
+    f"vllm_int8.{m}": f"int8kv.vllm_int8.{m}"
+    for m in ("cache_manager", "static_scales", "vllm_int8_kvcache_adapter",
+              "vllm_int8_cache_ops", "vllm_shadow_cache_patch", "vllm_int8_attention_patch")
+}
+
 
 def _ensure_package(name: str) -> None:
     if name in sys.modules:
@@ -37,10 +44,14 @@ def _ensure_package(name: str) -> None:
     sys.modules[name] = mod
 
 
-def install_reference_aliases() -> list:
-    """Makes ``import src.triton_ops.<op>`` resolve to this package; returns the aliased names."""
+def install_reference_aliases(include_vllm_int8: bool = False) -> list:
+    """Makes ``import src.triton_ops.<op>`` (and, with ``include_vllm_int8``, the reference's
+    ``vllm_int8.<module>`` imports) resolve to this package; returns the aliased names."""
     done = []
-    for alias, target in ALIASES.items():
+    table = dict(ALIASES)
+    if include_vllm_int8:
+        table.update(VLLM_INT8_ALIASES)
+    for alias, target in table.items():
         parent = alias.rsplit(".", 1)[0]
         _ensure_package(parent.split(".")[0])
         _ensure_package(parent)

@@ -135,3 +135,27 @@ def test_reference_module_aliases():
                 sys.modules.pop(k, None)
             else:
                 sys.modules[k] = v
+
+
+def test_vllm_int8_module_aliases():
+    import sys
+
+    from int8kv import compat
+
+    names = ("vllm_int8", *compat.ALIASES, *compat.VLLM_INT8_ALIASES, "src", "src.triton_ops")
+    saved = {k: sys.modules.get(k) for k in names}
+    try:
+        compat.install_reference_aliases(include_vllm_int8=True)
+        from vllm_int8.cache_manager import allocate_layer_cache
+        from vllm_int8.vllm_int8_cache_ops import runtime_int8_cache_write
+
+        from int8kv.vllm_int8 import cache_manager, vllm_int8_cache_ops
+
+        assert allocate_layer_cache is cache_manager.allocate_layer_cache
+        assert runtime_int8_cache_write is vllm_int8_cache_ops.runtime_int8_cache_write
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                sys.modules.pop(k, None)
+            else:
+                sys.modules[k] = v
