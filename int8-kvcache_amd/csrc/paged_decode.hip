@@ -744,32 +744,44 @@ __device__ __forceinline__ void store4(char* p, f32x4 x) {
   }
 }
 
-__device__ __forceinline__ float wave_max_f(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
+// Online-softmax merge of one more partial (m, l, acc) into a running (M, L, O).  A partial
+// without a finite maximum is added unscaled, so non-finite scores (a NaN query) still reach the
+// output as NaN, as they do in the reference.
+__device__ __forceinline__ void merge_in(float& M, float& L, f32x4& O, float m, float l, f32x4 acc) {
+  const float Mn = fmaxf(M, m);
+  if (Mn == -INFINITY) {
+    L += l;
+    O += acc;
+    return;
+  }
+  const float a = exp2_fast(M - Mn);
+  const float c = exp2_fast(m - Mn);
+  L = L * a + l * c;
+  O = O * a + acc * c;
+  M = Mn;
 }
 
-__device__ __forceinline__ float wave_sum_f(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
+// Combines the partials of every sequence cut by range bounds.  grid (batch, num_q_heads),
+// kMergeWaves waves per query head.  Lane (range parity, column) of wave w owns 4 head_dim
+// elements of ranges 2w + parity, 2w + parity + 2 kMergeWaves, ... and folds them in with one
+// online-softmax pass, four ranges' loads in flight at a time (32 ranges per round for the
+// workgroup); the 2 kMergeWaves running states per column are then merged through LDS.  A
+// sequence's merge costs about 1 + nr / 32 dependent memory latencies.
+constexpr int kMergeWaves = 4;
 
-// Combines the partials of every sequence cut by range bounds.  grid (batch, num_kv_heads), 4 waves; wave w merges query heads w, w + 4, ... of
-// the kv head's group.  A wave first reduces (max, sum) over the sequence's ranges with one
-// range per lane, then accumulates the weighted partial rows with lane = (range parity,
-// 4-element column), four rows in flight per lane.
 template <int CACHE, int QT>
-__global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kMergeWaves * 64) void merge_kernel(DecodeArgs a) {
+  __shared__ float s_m[2 * kMergeWaves][32];
+  __shared__ float s_l[2 * kMergeWaves][32];
+  __shared__ f32x4 s_o[2 * kMergeWaves][32];
   const int64_t b = blockIdx.x;
-  const int kvh = blockIdx.y;
+  const int h = blockIdx.y;
+  const int kvh = h / a.group;
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int nwaves = blockDim.x / kWave;
-  const int G = a.group;
   const int rs = lane >> 5;  // range parity handled by this lane
   const int c4 = lane & 31;  // head_dim elements [4 c4, 4 c4 + 4)
+  const int slot = 2 * wave + rs;  // 0 .. 2 kMergeWaves - 1
 
   const Plan plan = make_plan(a, lane);
   int64_t S = 0;  // stream units before sequence b
@@ -778,63 +790,52 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeArgs a) {
     S += wave_sum(bb < b ? units_of(a, tiles_of(a, seq_len_of(a, bb))) : 0);
   }
   const int64_t n = tiles_of(a, seq_len_of(a, b));
-  constexpr int QE = esize<QT>();
   if (n == 0) return;  // zeros written by decode_kernel
   const int64_t first = S + a.seq_cost;  // unit of tile 0
   const int64_t r0 = range_of(plan, first);
   const int64_t r1 = range_of(plan, first + n - 1);
   if (r0 == r1) return;  // finished inside one range by decode_kernel
   const int64_t nr = r1 - r0 + 1;
-  const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
-  auto row_of = [&](int64_t c, int h) -> int64_t {  // partial row of range r0 + c, head h
+  auto row_of = [&](int64_t c) -> int64_t {  // partial row of range r0 + c, head h
     return (2 * (r0 + c) + cut_slot(c)) * a.num_q_heads + h;  // tile 0 lies in range r0
   };
 
-  for (int j = wave; j < G; j += nwaves) {
-    const int h = kvh * G + j;
-    float mloc = -INFINITY, lloc = 0.0f;
-    for (int64_t c = lane; c < nr; c += kWave) {
-      const int64_t row = row_of(c, h);
-      const float m = a.ws_m[row];
-      const float l = a.ws_l[row];
-      if (m > mloc) {
-        lloc = lloc * exp2_fast(mloc - m) + l;
-        mloc = m;
+  constexpr int kStride = 2 * kMergeWaves;
+  float M = -INFINITY, L = 0.0f;
+  f32x4 O = (f32x4)(0.0f);
+  for (int64_t cb = slot; cb < nr; cb += 4 * kStride) {
+    float m[4], l[4];
+    f32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t c = cb + u * kStride;
+      if (c < nr) {
+        const int64_t row = row_of(c);
+        m[u] = a.ws_m[row];
+        l[u] = a.ws_l[row];
+        v[u] = *reinterpret_cast<const f32x4*>(a.ws_acc + row * kHeadDim + 4 * c4);
       } else {
-        lloc += l * exp2_fast(m - mloc);
-      }
-    }
-    const float M = wave_max_f(mloc);
-    const float lsum = wave_sum_f(mloc == -INFINITY ? 0.0f : lloc * exp2_fast(mloc - M));
-    const float inv = lsum > 0.0f ? vscale / lsum : 0.0f;
-
-    f32x4 O = (f32x4)(0.0f);
-    for (int64_t cb = 0; cb < nr; cb += kWave) {
-      const int cnt = (int)(nr - cb < kWave ? nr - cb : kWave);
-      const float wl = lane < cnt ? exp2_fast(a.ws_m[row_of(cb + lane, h)] - M) : 0.0f;
-      for (int kk = 0; kk < cnt; kk += 8) {
-        float w[4];
-        f32x4 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int k = kk + rs + 2 * u;
-          w[u] = __shfl(wl, k & (kWave - 1));
-          if (k < cnt) {
-            v[u] = *reinterpret_cast<const f32x4*>(a.ws_acc + row_of(cb + k, h) * kHeadDim + 4 * c4);
-          } else {
-            v[u] = (f32x4)(0.0f);
-            w[u] = 0.0f;
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) O += w[u] * v[u];
+        m[u] = -INFINITY;
+        l[u] = 0.0f;
+        v[u] = (f32x4)(0.0f);
       }
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) O[e] += __shfl_xor(O[e], 32);
-    if (rs == 0)
-      store4<QT>(a.out + (b * a.o_sb + (int64_t)h * a.o_sh + 4 * c4) * QE, O * inv);
+    for (int u = 0; u < 4; ++u) merge_in(M, L, O, m[u], l[u], v[u]);
   }
+  s_m[slot][c4] = M;
+  s_l[slot][c4] = L;
+  s_o[slot][c4] = O;
+  __syncthreads();
+  if (threadIdx.x >= 32) return;
+  M = -INFINITY;
+  L = 0.0f;
+  O = (f32x4)(0.0f);
+#pragma unroll
+  for (int k = 0; k < kStride; ++k) merge_in(M, L, O, s_m[k][c4], s_l[k][c4], s_o[k][c4]);
+  const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
+  const float inv = L > 0.0f ? vscale / L : 0.0f;
+  store4<QT>(a.out + (b * a.o_sb + (int64_t)h * a.o_sh + 4 * c4) * esize<QT>(), O * inv);
 }
 
 }  // namespace int8kv
@@ -845,6 +846,9 @@ namespace {
 
 constexpr int kMaxRangesLimit = 1 << 20;
 constexpr int kSeqStartCost = 2;  // stream units per sequence start (about one tile's time each)
+// Smallest automatic range: 4 tiles keep the partial records (3.6 KB per kv head and range)
+// under a quarter of a range's K/V bytes and bound the merge of one long sequence.
+constexpr int kAutoMinTiles = 4;
 constexpr int kWavesPerCU = 8;  // resident decode waves per CU the automatic range count targets
 
 // Waves per workgroup: the largest of 4, 3, 2, 1 dividing num_kv_heads.
@@ -894,8 +898,8 @@ int launch(const DecodeArgs& a, uint32_t flags, hipStream_t s) {
     if (e != hipSuccess) return (int)e;
   }
   if (flags & INT8KV_DECODE_MERGE) {
-    dim3 grid((unsigned)a.batch, (unsigned)a.num_kv_heads);
-    hipLaunchKernelGGL((merge_kernel<CACHE, QT>), grid, dim3(4 * kWave), 0, s, a);
+    dim3 grid((unsigned)a.batch, (unsigned)a.num_q_heads);
+    hipLaunchKernelGGL((merge_kernel<CACHE, QT>), grid, dim3(kMergeWaves * kWave), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }
@@ -975,7 +979,7 @@ extern "C" int int8kv_paged_decode(
   }
 
   if (num_ranges == 0) num_ranges = auto_ranges(num_kv_heads);
-  if (min_tiles == 0) min_tiles = 2;
+  if (min_tiles == 0) min_tiles = kAutoMinTiles;
   const size_t need = workspace_bytes(num_q_heads, num_ranges);
   if (workspace == nullptr || workspace_bytes_given < need || ((uintptr_t)workspace % 16) != 0)
     return INT8KV_E_WORKSPACE;
