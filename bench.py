@@ -116,6 +116,36 @@ def time_events(fn, steps: int, warmup: int) -> float:
     return sum(a.elapsed_time(b) for a, b in pairs) / len(pairs)
 
 
+def time_graph(fn, calls: int = 20, replays: int = 10) -> float:
+    """Device time per call (ms) of ``fn`` captured ``calls`` times in one HIP graph and replayed:
+    removes the host's per-call launch cost, which dominates calls of a few microseconds."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    torch.cuda.synchronize()
+    for _ in range(2):
+        graph.replay()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(replays):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / (replays * calls)
+
+
 def cpu_baseline(w, out_gpu, budget_s: float = 10.0):
     """Times the CPU oracle (one thread) over the workload's sequences, pass after pass, until
     ``budget_s`` seconds of oracle work are done; the first pass also measures the agreement of
@@ -187,6 +217,83 @@ def read_traffic():
         return None
 
 
+def sweep_configs(dev, out_path: str | None) -> dict:
+    """The two smaller benchmark configurations, reported beside the headline line:
+    cfg1 -- the prefill cache write alone (8 x 2048 tokens + 512 padding slots into a
+    2048-block cache through a random-permutation slot mapping); cfg2 -- INT8 and BF16 decode at
+    B in {1, 2, 4, 8} x uniform ctx in {512, 1024, 2048, 4096}, automatic split vs one range per
+    sequence.  Both working sets fit the 256 MB Infinity Cache, so their GB/s are cache-resident
+    rates and µs/call is the meaningful figure.  Times are device times per call from HIP-graph
+    replays (a few-microsecond call is otherwise dominated by the host's launch cost)."""
+    import torch
+
+    import int8kv
+    from int8kv import synthetic as syn
+    from oracle import int8kv_oracle as O
+
+    res = {}
+    g = torch.Generator().manual_seed(11)
+    dist = syn.make_distribution(11)
+    ks, vs = syn.calibrate_scales(dist, seed=12)
+    n_tok, n_pad, nb = 16384, 512, 2048
+    k, v = syn.sample_kv(n_tok + n_pad, dist, g)
+    slots = torch.randperm(nb * 16, generator=g)[: n_tok + n_pad].to(torch.int64)
+    slots[torch.randperm(n_tok + n_pad, generator=g)[:n_pad]] = -1
+    kc = torch.zeros(nb, 16, 4, 128, dtype=torch.int8, device=dev)
+    vc = torch.zeros_like(kc)
+    k, v, slots_d, ks_d, vs_d = k.to(dev), v.to(dev), slots.to(dev), ks.to(dev), vs.to(dev)
+
+    def write():
+        int8kv.int8_kv_cache_write(k, v, kc, vc, slots_d, ks_d, vs_d)
+
+    ms_w = time_graph(write)
+    wbytes = n_tok * 4 * 128 * (2 + 2 + 1 + 1) + (n_tok + n_pad) * 8 + 2 * 4 * 4
+    res["cfg1_write"] = {"tokens": n_tok, "padding_slots": n_pad, "us_per_call": round(ms_w * 1e3, 2),
+                         "algorithmic_bytes": wbytes, "GBps": round(wbytes / ms_w / 1e6, 1)}
+    log(f"cfg1 write: {ms_w * 1e3:.1f} us ({wbytes / ms_w / 1e6:.0f} GB/s)")
+
+    rows = []
+    for B in (1, 2, 4, 8):
+        for ctx in (512, 1024, 2048, 4096):
+            gq = torch.Generator().manual_seed(B * 7 + ctx)
+            nblk = B * ctx // 16
+            pool = nblk * 2
+            bt = syn.random_block_tables([ctx] * B, pool, gq)
+            sl = syn.slot_mapping_for(bt, [ctx] * B)
+            kk, vv = syn.sample_kv(B * ctx, dist, gq)
+            q = syn.sample_query(B, gq).to(dev)
+            kc8 = torch.zeros(pool, 16, 4, 128, dtype=torch.int8, device=dev)
+            vc8 = torch.zeros_like(kc8)
+            int8kv.int8_kv_cache_write(kk.to(dev), vv.to(dev), kc8, vc8, sl.to(dev), ks_d, vs_d)
+            kc16 = torch.zeros(pool * 16, 4, 128, dtype=torch.bfloat16, device=dev)
+            vc16 = torch.zeros_like(kc16)
+            kc16[sl.to(dev)] = kk.to(dev)
+            vc16[sl.to(dev)] = vv.to(dev)
+            kc16, vc16 = kc16.view(pool, 16, 4, 128), vc16.view(pool, 16, 4, 128)
+            btd = bt.to(dev)
+            lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+            row = {"B": B, "ctx": ctx}
+            for name, fn in (
+                ("int8_auto", lambda: int8kv.int8_paged_attention(q, kc8, vc8, btd, lens, ks_d, vs_d)),
+                ("int8_single_pass", lambda: int8kv.int8_paged_attention(q, kc8, vc8, btd, lens, ks_d, vs_d,
+                                                                         num_splits=1)),
+                ("bf16_auto", lambda: int8kv.bf16_paged_attention(q, kc16, vc16, btd, lens)),
+            ):
+                ms = time_graph(fn)
+                e = 2 if name.startswith("bf16") else 1
+                nbytes = O.decode_bytes([ctx] * B, 4, 128, e, B, 28)
+                row[name + "_us"] = round(ms * 1e3, 2)
+                row[name + "_GBps"] = round(nbytes / ms / 1e6, 1)
+            rows.append(row)
+            log(f"cfg2 B={B} ctx={ctx}: int8 {row['int8_auto_us']} us (single pass "
+                f"{row['int8_single_pass_us']}), bf16 {row['bf16_auto_us']} us")
+    res["cfg2_sweep"] = rows
+    if out_path:
+        Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+        Path(out_path).write_text(json.dumps(res, indent=1))
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -196,6 +303,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU-oracle work for the cpu_baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--sweep", metavar="JSON", default=None,
+                    help="also measure the cfg1 write and the cfg2 decode sweep, written to JSON")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run 3 plain 1 GiB device copies (the reference kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
@@ -304,6 +413,8 @@ def main() -> int:
             "sequences": check["sequences"], "max_abs": round(check["max_abs"], 6),
             "cos": round(check["cos"], 7)}
         log(f"cpu baseline {cb['value']} GB/s; GPU vs oracle on sample: {check}")
+    if args.sweep:
+        sweep_configs(dev, args.sweep)
     if args.calibrate_copy:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
