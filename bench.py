@@ -294,6 +294,60 @@ def sweep_configs(dev, out_path: str | None) -> dict:
     return res
 
 
+def tpot_config4(dev, out_path: str | None, batch: int = 32, context: int = 8192,
+                 new_tokens: int = 128, layers: int = 28) -> dict:
+    """Config 4: greedy decode of a random-init Qwen2.5-7B-shaped bf16 model, INT8 vs BF16 KV.
+
+    B sequences of ``context`` random prompt ids, ``new_tokens`` greedy tokens each; attention
+    runs on this library (INT8: static per-head write + INT8 decode; BF16: bf16 cache + BF16
+    decode), the rest on torch (hipBLASLt GEMMs, SDPA for the prefill).  Each decode step is one
+    HIP-graph replay.  TPOT = (T128 - T1) / 127 as in the reference's
+    bench/benchmark_decode_tpot.py:64-68; KV bytes are the paged caches of all layers.
+    """
+    import dataclasses
+
+    import torch
+
+    from int8kv import decode_loop as DL
+
+    shape = dataclasses.replace(DL.QWEN25_7B, layers=layers)
+    torch.zeros(1, device=dev)  # initialises the allocator before its statistics are reset
+    torch.cuda.reset_peak_memory_stats(dev)
+    t0 = time.perf_counter()
+    weights = DL.random_weights(shape, dev, seed=0)
+    torch.cuda.synchronize(dev)
+    log(f"cfg4: weights {weights.nbytes() / 1e9:.2f} GB in {time.perf_counter() - t0:.1f} s")
+    calib = torch.randint(0, shape.vocab, (4, 512), generator=torch.Generator().manual_seed(3))
+    scales = DL.calibrate_static_scales(weights, calib)
+    res = {"config": {"model": "random-init Qwen2.5-7B shape (bf16)", **dataclasses.asdict(shape),
+                      "batch": batch, "context": context, "new_tokens": new_tokens,
+                      "calibration": "4 x 512 random ids, absmax/127 of post-rotary K and V"},
+           "runs": []}
+    gens = {}
+    for mode in DL.MODES:
+        rec = DL.run_tpot(weights, batch, context, new_tokens, mode,
+                          scales=scales if mode == "int8" else None, log=lambda m, **k: log(m))
+        loop = rec.pop("_loop")
+        gens[mode] = loop.generated.cpu()
+        res["runs"].append(rec)
+        del loop
+        torch.cuda.empty_cache()
+    i8, bf = res["runs"]
+    res["int8_vs_bf16"] = {
+        "tpot_speedup": round(bf["decode_tpot_ms"] / i8["decode_tpot_ms"], 4),
+        "kv_bytes_ratio": round(i8["kv_cache_bytes"] / bf["kv_cache_bytes"], 4),
+        "greedy_token_agreement": round(float((gens["int8"] == gens["bf16"]).float().mean()), 4),
+        "first_divergence_step_median": int(torch.tensor(
+            [int((r != s).nonzero()[0]) if (r != s).any() else new_tokens
+             for r, s in zip(gens["int8"], gens["bf16"])]).median()),
+    }
+    log(f"cfg4: {json.dumps(res['int8_vs_bf16'])}")
+    if out_path:
+        Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+        Path(out_path).write_text(json.dumps(res, indent=1))
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -308,6 +362,13 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run 3 plain 1 GiB device copies (the reference kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
+    ap.add_argument("--tpot", metavar="JSON", default=None,
+                    help="also run config 4 (28-layer random-init Qwen2.5-7B decode loop, INT8 vs "
+                         "BF16 KV: TPOT and KV bytes), written to JSON")
+    ap.add_argument("--tpot-only", action="store_true",
+                    help="run only config 4 (no headline line)")
+    ap.add_argument("--tpot-shape", default="32,8192,128,28", metavar="B,CTX,NEW,LAYERS",
+                    help="config-4 batch, prompt length, new tokens and layer count")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -325,6 +386,10 @@ def main() -> int:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     _lib.load()
     dev = torch.device("cuda:0")
+    tpot_args = [int(x) for x in args.tpot_shape.split(",")]
+    if args.tpot_only:
+        tpot_config4(dev, args.tpot, *tpot_args)
+        return 0
     log("building workload (B=64, ctx ~ U[1, 32768]) ...")
     w = build_workload(dev, seed=args.seed)
     lens = w["lens"]
@@ -415,6 +480,10 @@ def main() -> int:
         log(f"cpu baseline {cb['value']} GB/s; GPU vs oracle on sample: {check}")
     if args.sweep:
         sweep_configs(dev, args.sweep)
+    if args.tpot:
+        del w
+        torch.cuda.empty_cache()
+        tpot_config4(dev, args.tpot, *tpot_args)
     if args.calibrate_copy:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)

@@ -1,4 +1,4 @@
-"""Builds libint8kv.so (the HIP kernels plus the C ABI of include/int8kv.h) for gfx950.
+"""Builds libint8kv.so (the HIP kernels plus the C ABI of include/int8kv*.h) for gfx950.
 
 The library is compiled in-tree with hipcc, next to this file, so that it travels with the
 source tree.  Usage: ``python -m int8kv._build`` (from the ``int8-kvcache_amd`` directory) or
@@ -18,7 +18,7 @@ CSRC_DIR = PKG_DIR.parent / "csrc"
 INCLUDE_DIR = PKG_DIR.parent.parent / "include"
 LIB_PATH = PKG_DIR / "libint8kv.so"
 
-SOURCES = ["cache_write.hip", "paged_decode.hip"]
+SOURCES = ["cache_write.hip", "paged_decode.hip", "decode_loop_ops.hip"]
 
 # -packed-fp32-ops keeps hipcc from emitting packed fp32 VALU instructions (v_pk_fma_f32 and
 # friends) from ordinary float code; the host pass merely warns that it does not know it.

@@ -1,4 +1,5 @@
-"""ctypes binding of libint8kv.so (the C ABI declared in include/int8kv.h).
+"""ctypes binding of libint8kv.so (the C ABI declared in include/int8kv.h and
+include/int8kv_decode_loop.h).
 
 The library is required: if it is missing every operator raises instead of computing anything
 elsewhere.  Torch is used only to read tensor metadata (pointers, strides, the current stream).
@@ -74,6 +75,12 @@ def load() -> ctypes.CDLL:
         _c_i64p, _c_i64p, _vp, ctypes.c_int, i64, _c_i64p, _vp, ctypes.c_int, _vp, _vp, f32,
         _vp, _c_i64p, _vp, sz, i32, i32, u32, _vp,
     ]
+    lib.int8kv_add_rms_norm.restype = ctypes.c_int
+    lib.int8kv_add_rms_norm.argtypes = [_vp, _vp, _vp, _vp, i64, i32, i64, i64, i64, f32, _vp]
+    lib.int8kv_rotary_inplace.restype = ctypes.c_int
+    lib.int8kv_rotary_inplace.argtypes = [_vp, i64, i64, i32, i32, _vp, _vp, _vp, i64, _vp]
+    lib.int8kv_silu_mul.restype = ctypes.c_int
+    lib.int8kv_silu_mul.argtypes = [_vp, _vp, i64, i32, i64, i64, _vp]
     lib.int8kv_version.restype = ctypes.c_char_p
     lib.int8kv_version.argtypes = []
     _lib = lib

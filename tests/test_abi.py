@@ -10,13 +10,15 @@ import pytest
 
 from conftest import REPO
 
-HEADER = REPO / "include" / "int8kv.h"
+HEADERS = sorted((REPO / "include").glob("*.h"))
 
 
 def _declared_functions():
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(int8kv_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names.update(re.findall(r"\b(int8kv_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 @pytest.fixture(scope="module")
@@ -29,12 +31,16 @@ def lib():
 
 
 def test_header_declares_expected_entry_points():
+    assert [h.name for h in HEADERS] == ["int8kv.h", "int8kv_decode_loop.h"]
     assert _declared_functions() == [
+        "int8kv_add_rms_norm",
         "int8kv_cache_write",
         "int8kv_decode_auto_ranges",
         "int8kv_decode_workspace_bytes",
         "int8kv_dynamic_cache_write",
         "int8kv_paged_decode",
+        "int8kv_rotary_inplace",
+        "int8kv_silu_mul",
         "int8kv_version",
     ]
 
@@ -139,3 +145,36 @@ def test_dynamic_write_rejects_bad_arguments_without_launching(lib):
     assert call(ksc=18) == -4  # misaligned fp32 scale cache
     assert call(key=8) == -4
     assert call(T=0) == 0
+
+
+def test_loop_ops_reject_bad_arguments_without_launching(lib):
+    """Fake device pointers; every call below fails validation before any launch."""
+    E_NULL, E_SHAPE, E_STRIDE = -1, -3, -4
+    P = 256  # 16-byte aligned fake pointer
+    # add_rms_norm(residual, delta, weight, out, rows, hidden, rs, ds, os, eps, stream)
+    ok = dict(r=P, d=P, w=P, o=P, rows=4, hidden=512, rs=512, ds=512, os=512, eps=1e-6, s=None)
+
+    def norm(**kw):
+        a = dict(ok, **kw)
+        return lib.int8kv_add_rms_norm(*a.values())
+
+    assert norm(r=None) == E_NULL and norm(w=None) == E_NULL and norm(o=None) == E_NULL
+    assert norm(hidden=12) == E_SHAPE and norm(hidden=8200) == E_SHAPE and norm(rows=-1) == E_SHAPE
+    assert norm(r=P + 2) == E_STRIDE and norm(rs=500) == E_STRIDE and norm(ds=4) == E_STRIDE
+    assert norm(rows=0) == 0  # nothing to do, nothing launched
+    # rotary_inplace(qkv, rows, row_stride, num_heads, head_dim, positions, cos, sin, max_pos, stream)
+    rot = dict(q=P, rows=4, rs=4608, heads=32, d=128, pos=P, c=P, s=P, maxp=10, st=None)
+
+    def rope(**kw):
+        a = dict(rot, **kw)
+        return lib.int8kv_rotary_inplace(*a.values())
+
+    assert rope(pos=None) == E_NULL and rope(c=None) == E_NULL
+    assert rope(d=120) == E_SHAPE and rope(maxp=0) == E_SHAPE and rope(heads=0) == E_SHAPE
+    assert rope(rs=4000) == E_STRIDE and rope(c=P + 4) == E_STRIDE
+    assert rope(rows=0) == 0
+    # silu_mul(gate_up, out, rows, ffn, in_stride, out_stride, stream)
+    assert lib.int8kv_silu_mul(None, P, 4, 64, 128, 64, None) == E_NULL
+    assert lib.int8kv_silu_mul(P, P, 4, 60, 120, 60, None) == E_SHAPE
+    assert lib.int8kv_silu_mul(P, P, 4, 64, 64, 64, None) == E_STRIDE
+    assert lib.int8kv_silu_mul(P, P, 0, 64, 128, 64, None) == 0
