@@ -323,17 +323,24 @@ def tpot_config4(dev, out_path: str | None, batch: int = 32, context: int = 8192
                       "batch": batch, "context": context, "new_tokens": new_tokens,
                       "calibration": "4 x 512 random ids, absmax/127 of post-rotary K and V"},
            "runs": []}
-    gens = {}
+    gens, step1, first = {}, {}, {}
     for mode in DL.MODES:
         rec = DL.run_tpot(weights, batch, context, new_tokens, mode,
                           scales=scales if mode == "int8" else None, log=lambda m, **k: log(m))
         loop = rec.pop("_loop")
         gens[mode] = loop.generated.cpu()
+        step1[mode] = rec.pop("_step1_logits").cpu().double()
+        first[mode] = rec.pop("_first_tokens").cpu()
         res["runs"].append(rec)
         del loop
         torch.cuda.empty_cache()
     i8, bf = res["runs"]
+    a, b = step1["int8"], step1["bf16"]
     res["int8_vs_bf16"] = {
+        "step1_logits_cos_min": round(float(torch.nn.functional.cosine_similarity(a, b, dim=1).min()), 6),
+        "step1_logits_rel_l2": round(float((a - b).norm() / b.norm()), 6),
+        "step1_top1_agreement": round(float((a.argmax(1) == b.argmax(1)).float().mean()), 4),
+        "prefill_first_tokens_equal": bool(torch.equal(first["int8"], first["bf16"])),
         "tpot_speedup": round(bf["decode_tpot_ms"] / i8["decode_tpot_ms"], 4),
         "kv_bytes_ratio": round(i8["kv_cache_bytes"] / bf["kv_cache_bytes"], 4),
         "greedy_token_agreement": round(float((gens["int8"] == gens["bf16"]).float().mean()), 4),

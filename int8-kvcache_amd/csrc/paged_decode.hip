@@ -7,28 +7,36 @@
 // weights times v_t * v_scale, with v_scale applied once at the end (:291-292).
 //
 // Work decomposition (MI355X-first, not the reference's grid):
-//   * Every sequence is cut into 32-token tiles; the tiles of all sequences, in batch order,
-//     form one stream of T tiles per kv head.  The stream is divided into P equal contiguous
-//     ranges (P = a few workgroups per CU), so a ragged batch costs every workgroup the same
-//     number of tiles (+-1) whatever the length distribution.  T and the range bounds are
-//     computed on the device from seq_lens; the host never reads them.
+//   * Every sequence is cut into 32-token tiles.  The batch, in order, becomes one stream of
+//     units per kv head: a non-empty sequence is a few "start" units (the cost of reaching its
+//     first tile) followed by its tiles.  The stream is divided into P equal contiguous ranges
+//     (P = a few workgroups per CU, fewer for short batches: at least min_tiles units per
+//     range), so a ragged batch costs every workgroup the same whatever the length
+//     distribution.  The unit counts and the range bounds are computed on the device from
+//     seq_lens; the host never reads them.
 //   * A workgroup owns one range for W kv heads, one wave per kv head.  The W waves read the
 //     same cache blocks (their head slices of the same 16-token rows) at the same time.  A wave
 //     handles all query heads of its GQA group on the matrix cores, so every K/V byte is read
-//     from HBM exactly once, and needs no LDS and no barrier.
+//     from HBM exactly once, and needs no barrier.
 //   * A sequence wholly inside one range is finished by that wave (output written directly).
 //     A sequence cut by range bounds leaves (max, sum, accumulator) partials in the workspace,
 //     at most two per range and head; merge_kernel combines them.
 //   * Per 32-token tile and wave:  S^T = K * Q^T  (2 x 4 MFMA 16x16x32; rows = tokens, cols =
 //     heads), online softmax in the exp2 domain, then out^T += V^T * P^T (2 x 8 MFMA 16x16x32,
-//     P split into 16-bit hi + lo parts; rows = head_dim, cols = heads).  The MFMA accumulator layout puts one head per lane
-//     column, so the probabilities never leave registers.  The next tile's loads are in flight
-//     while a tile is computed; block-table entries are read 64 at a time into one register
-//     (one lane per block) ahead of use, so no table read sits on the tile critical path.
+//     P split into 16-bit hi + lo parts; rows = head_dim, cols = heads).  The MFMA accumulator
+//     layout puts one head per lane column, so the probabilities never leave registers.
+//   * Two tiles are in flight per wave: K(t+2) is requested as soon as the scores of tile t are
+//     formed and V(t+2) as soon as its P*V is done.  The block ids of up to 256 tiles are staged
+//     in LDS per wave ahead of use, every load in the tile loop is unconditional (requests past
+//     the end of a range repeat its last tile), and the loop body is straight-line code per
+//     tile pair, so no wait for a table read or a branch drains the pipeline.
 //   * INT8 K/V are dequantised in registers to fp16 with the exact magic-number conversion
 //     (0x6400 | (x ^ 0x80)) - 1152 = x, two elements per v_pk_add_f16.  Q is scaled by a power
 //     of two into the upper fp16 range (exact for bf16 input); k_scale * sm_scale * log2(e) and
-//     that power of two are applied to the fp32 scores, v_scale to the final output.
+//     that power of two are applied to the fp32 scores, v_scale to the final output.  With
+//     INT8KV_DECODE_QUANTIZE_Q, q is first quantised per (sequence, head) to int8 with
+//     half-away rounding (src/triton_ops/int8_paged_attention.py:137-149) and its scale folded
+//     into the score scale.
 //   * A running max is only moved when a tile's max exceeds it by more than 8 (log2 units), so
 //     most tiles skip the accumulator rescale; probabilities are then <= 2^8 (fits fp16/bf16).
 

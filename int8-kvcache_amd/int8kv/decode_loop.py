@@ -481,6 +481,7 @@ def run_tpot(weights: ModelWeights, batch: int, prompt_len: int, new_tokens: int
     torch.cuda.synchronize(dev)
     t1 = time.perf_counter() - t0
     log(f"[{mode}] prefill + first token: {t1 * 1e3:.1f} ms", flush=True)
+    after_prefill = loop.state()
     loop.capture()
     steps = new_tokens - 1
     stream = torch.cuda.current_stream(dev)
@@ -513,6 +514,13 @@ def run_tpot(weights: ModelWeights, batch: int, prompt_len: int, new_tokens: int
     }
     log(f"[{mode}] TPOT {tpot:.3f} ms (device {rec['decode_tpot_device_ms']:.3f} ms), "
         f"{rec['decode_tok_s']:.0f} tok/s, KV {kv['kv_bytes'] / 1e9:.3f} GB", flush=True)
+    # First decode step again from the post-prefill state (it rewrites the same cache slot with
+    # the same value): its logits compare the cache modes on an identical prefix.
+    loop.restore(after_prefill)
+    loop.replay()
+    torch.cuda.synchronize(dev)
+    rec["_step1_logits"] = loop.logits.float().clone()
+    rec["_first_tokens"] = loop.generated[:, 0].clone()
     rec["_loop"] = loop
     return rec
 
