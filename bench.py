@@ -328,7 +328,7 @@ def tpot_config4(dev, out_path: str | None, batch: int = 32, context: int = 8192
         rec = DL.run_tpot(weights, batch, context, new_tokens, mode,
                           scales=scales if mode == "int8" else None, log=lambda m, **k: log(m))
         loop = rec.pop("_loop")
-        gens[mode] = loop.generated.cpu()
+        gens[mode] = rec.pop("_generated").cpu()
         step1[mode] = rec.pop("_step1_logits").cpu().double()
         first[mode] = rec.pop("_first_tokens").cpu()
         res["runs"].append(rec)

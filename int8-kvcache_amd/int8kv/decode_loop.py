@@ -516,6 +516,7 @@ def run_tpot(weights: ModelWeights, batch: int, prompt_len: int, new_tokens: int
         f"{rec['decode_tok_s']:.0f} tok/s, KV {kv['kv_bytes'] / 1e9:.3f} GB", flush=True)
     # First decode step again from the post-prefill state (it rewrites the same cache slot with
     # the same value): its logits compare the cache modes on an identical prefix.
+    rec["_generated"] = loop.generated.clone()
     loop.restore(after_prefill)
     loop.replay()
     torch.cuda.synchronize(dev)
