@@ -12,6 +12,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from .torch_reference import torch_int8_kv_cache_write_reference  # noqa: F401  (reference checker)
 
 _SRC_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 

@@ -27,6 +27,7 @@ from __future__ import annotations
 import torch
 
 from . import _decode, _lib
+from .torch_reference import torch_int8_paged_attention_reference  # noqa: F401  (reference checker)
 
 
 def int8_paged_attention(

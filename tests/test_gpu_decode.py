@@ -234,3 +234,26 @@ def test_quantize_q(cuda, lens, qdtype):
     if qdtype == torch.float32:
         err, _, _ = metrics(out.cpu().numpy(), ref)
         assert err <= 1e-4
+
+
+def test_matches_reference_torch_checkers_on_device(cuda):
+    """The reference's own test pattern: operator vs its torch checker, both on the GPU
+    (tests/test_int8_paged_attention.py:108-323, tests/test_cache_write.py)."""
+    from int8kv.torch_reference import (torch_int8_kv_cache_write_reference,
+                                        torch_int8_paged_attention_reference)
+
+    c = decode_case([33, 300, 1, 129], seed=21, randn_kv=True, extra_blocks=9)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    for quantize_q in (False, True):
+        out = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs, quantize_q=quantize_q)
+        ref = torch_int8_paged_attention_reference(q.float(), kc, vc, bt, sl, ks, vs, quantize_q=quantize_q)
+        _check(out, ref.cpu().numpy(), f"vs torch checker quantize_q={quantize_q}")
+    # Cache write: operator and checker into two copies of the same sentinel-filled caches.
+    k, v, slots = c.key.to(cuda), c.value.to(cuda), c.slots.to(cuda)
+    a_k = torch.full_like(kc, 0x5A)
+    a_v = torch.full_like(vc, 0x5A)
+    b_k, b_v = a_k.clone(), a_v.clone()
+    int8kv.int8_kv_cache_write(k, v, a_k, a_v, slots, ks, vs)
+    torch_int8_kv_cache_write_reference(k, v, b_k, b_v, slots, ks, vs)
+    torch.cuda.synchronize()
+    assert torch.equal(a_k, b_k) and torch.equal(a_v, b_v)
