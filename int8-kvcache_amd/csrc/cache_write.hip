@@ -7,10 +7,13 @@
 // zero (:59-63); this kernel deliberately does not.  The scale is clamped to >= 1e-6 as the
 // Triton kernel does (:50-51); calibrated scales already satisfy that (scripts/04 :55-65).
 //
-// Mapping: one lane owns 8 consecutive head_dim elements of one (token, kv-head) row of both
-// K and V, so a wave64 covers a whole 4 x 128 token row with 16-byte loads and 8-byte stores
-// (fully coalesced 128-byte segments per head).  The slot index and the two scales are
-// wave-uniform for head_dim * num_kv_heads = 512.
+// Mapping (wide kernels, head_dim % 16 == 0 and 16-byte aligned cache rows): grid.y = kv head,
+// one lane owns 16 consecutive head_dim elements of one (token, head) row of both K and V --
+// 32-byte source loads, 16-byte cache stores, 8 lanes per 128-element row.  The slot and the
+// K/V loads are all issued before the slot is tested.  Sources are read and caches written
+// with the non-temporal hint: both are streamed once (262k-token write on MI355X: 193 ->
+// 166 us, 4.2 -> 4.9 TB/s).  Other layouts (head_dim % 16 == 8, or cache rows only 8-byte
+// aligned) use the narrow kernels: one lane per 8 elements, 8-byte stores.
 
 #include "int8kv_common.h"
 
@@ -80,6 +83,73 @@ __global__ __launch_bounds__(256) void cache_write_kernel(WriteArgs a) {
 
   *reinterpret_cast<u32x2*>(a.kc + blk * a.kc_sb + off * a.kc_ss + h * a.kc_sh + 8 * dv) = kq;
   *reinterpret_cast<u32x2*>(a.vc + blk * a.vc_sb + off * a.vc_ss + h * a.vc_sh + 8 * dv) = vq;
+}
+
+
+// ------------------------------------------------------------------ wide kernels (16 per lane)
+template <bool NT>
+__device__ __forceinline__ u32x4 ld16(const char* p) {
+  if constexpr (NT)
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  else
+    return *reinterpret_cast<const u32x4*>(p);
+}
+
+// 16 consecutive elements of type DT at p (16-byte aligned), widened to fp32, non-temporal.
+template <int DT>
+__device__ __forceinline__ void load16_f32(const char* p, float (&x)[16]) {
+  if constexpr (DT == kF32) {
+    // Typed f32x4 loads: element reads of a bit-cast u32x4 were miscompiled here (repeated
+    // elements), as in the decode kernel's fp32 query path.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 w = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 16 * j));
+      x[4 * j + 0] = w[0];
+      x[4 * j + 1] = w[1];
+      x[4 * j + 2] = w[2];
+      x[4 * j + 3] = w[3];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const u32x4 w = ld16<true>(p + 16 * j);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) unpack2<DT>(w[i], x[8 * j + 2 * i], x[8 * j + 2 * i + 1]);
+    }
+  }
+}
+
+__device__ __forceinline__ void store16_nt(int8_t* p, const u32x4& v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
+// grid (ceil(num_tokens * vecs_per_row / 256), num_kv_heads); vecs_per_row = head_dim / 16.
+template <int SRC>
+__global__ __launch_bounds__(256) void cache_write16_kernel(WriteArgs a) {
+  const int h = blockIdx.y;
+  const uint32_t lpr = (uint32_t)a.vecs_per_row;
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t t = gid / lpr;
+  if ((int64_t)t >= a.num_tokens) return;
+  const int dv = (int)(gid - t * lpr);
+  constexpr int esize = SRC == kF32 ? 4 : 2;
+  const int64_t slot = load_index(a.slots, t, a.slots_is64);
+  float x[16], y[16];
+  load16_f32<SRC>(a.key + ((int64_t)t * a.k_st + h * a.k_sh + 16 * dv) * esize, x);
+  load16_f32<SRC>(a.value + ((int64_t)t * a.v_st + h * a.v_sh + 16 * dv) * esize, y);
+  const float ks = fmaxf(a.k_scale[h], 1e-6f);
+  const float vs = fmaxf(a.v_scale[h], 1e-6f);
+  if (slot < 0 || slot >= a.capacity) return;
+  const int64_t blk = slot / a.block_size;
+  const int64_t off = slot - blk * a.block_size;
+  u32x4 kq, vq;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    kq[i] = quant4(x + 4 * i, ks);
+    vq[i] = quant4(y + 4 * i, vs);
+  }
+  store16_nt(a.kc + blk * a.kc_sb + off * a.kc_ss + h * a.kc_sh + 16 * dv, kq);
+  store16_nt(a.vc + blk * a.vc_sb + off * a.vc_ss + h * a.vc_sh + 16 * dv, vq);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -162,6 +232,59 @@ __global__ __launch_bounds__(256) void dynamic_write_kernel(DynWriteArgs d) {
   }
 }
 
+
+// Wide dynamic write: grid (ceil(num_tokens * vecs_per_row / 256), num_kv_heads), 16 elements
+// per lane; vecs_per_row = head_dim / 16 is a power of two <= 64, so a row's lanes sit in one
+// wave and the absmax butterfly stays inside the row.
+template <int SRC>
+__global__ __launch_bounds__(256) void dynamic_write16_kernel(DynWriteArgs d) {
+  const WriteArgs& a = d.w;
+  const int h = blockIdx.y;
+  const uint32_t lpr = (uint32_t)a.vecs_per_row;
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t t = gid / lpr;
+  const bool in_range = (int64_t)t < a.num_tokens;
+  const int dv = (int)(gid - t * lpr);
+  constexpr int esize = SRC == kF32 ? 4 : 2;
+  float x[16], y[16];
+  int64_t slot = -1;
+  if (in_range) {
+    slot = load_index(a.slots, t, a.slots_is64);
+    load16_f32<SRC>(a.key + ((int64_t)t * a.k_st + h * a.k_sh + 16 * dv) * esize, x);
+    load16_f32<SRC>(a.value + ((int64_t)t * a.v_st + h * a.v_sh + 16 * dv) * esize, y);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = y[i] = 0.0f;
+  }
+  float km = 0.0f, vm = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    km = fmaxf(km, fabsf(x[i]));
+    vm = fmaxf(vm, fabsf(y[i]));
+  }
+  for (uint32_t o = 1; o < lpr; o <<= 1) {
+    km = fmaxf(km, __shfl_xor(km, (int)o));
+    vm = fmaxf(vm, __shfl_xor(vm, (int)o));
+  }
+  const float ks = fmaxf(km / 127.0f, 1e-6f);
+  const float vs = fmaxf(vm / 127.0f, 1e-6f);
+  if (!in_range || slot < 0 || slot >= a.capacity) return;
+  const int64_t blk = slot / a.block_size;
+  const int64_t off = slot - blk * a.block_size;
+  u32x4 kq, vq;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    kq[i] = quant4_dyn(x + 4 * i, ks);
+    vq[i] = quant4_dyn(y + 4 * i, vs);
+  }
+  store16_nt(a.kc + blk * a.kc_sb + off * a.kc_ss + h * a.kc_sh + 16 * dv, kq);
+  store16_nt(a.vc + blk * a.vc_sb + off * a.vc_ss + h * a.vc_sh + 16 * dv, vq);
+  if (dv == 0) {
+    d.ksc[blk * d.ksc_sb + off * d.ksc_ss + h * d.ksc_sh] = ks;
+    d.vsc[blk * d.vsc_sb + off * d.vsc_ss + h * d.vsc_sh] = vs;
+  }
+}
+
 }  // namespace int8kv
 
 using namespace int8kv;
@@ -171,6 +294,15 @@ static bool aligned(const void* p, int64_t stride_bytes, int64_t align) {
 }
 
 namespace {
+
+// The wide kernels need head_dim % 16 == 0, 16-byte aligned cache rows and a 32-bit lane index.
+bool wide_ok(const void* key_cache, const void* value_cache, const int64_t kcs[4],
+             const int64_t vcs[4], int64_t num_tokens, int32_t num_kv_heads, int32_t head_dim) {
+  if (head_dim % 16 != 0 || num_kv_heads > 65535) return false;
+  for (int i = 0; i < 3; ++i)
+    if (!aligned(key_cache, kcs[i], 16) || !aligned(value_cache, vcs[i], 16)) return false;
+  return num_tokens * (int64_t)(head_dim / 16) <= 0x7fffffffLL;
+}
 
 // Validates the arguments shared by the static and the dynamic write and fills WriteArgs.
 int prepare_write(WriteArgs& a, const void* key, const void* value, int src_dtype,
@@ -249,12 +381,31 @@ extern "C" int int8kv_cache_write(const void* key, const void* value, int src_dt
   if (!k_scale || !v_scale) return INT8KV_E_NULL;
   a.k_scale = k_scale;
   a.v_scale = v_scale;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  if (wide_ok(key_cache, value_cache, key_cache_strides, value_cache_strides, num_tokens,
+              num_kv_heads, head_dim)) {
+    a.vecs_per_row = head_dim / 16;
+    const int64_t blocks16 = (num_tokens * a.vecs_per_row + 255) / 256;
+    const dim3 grid((unsigned)blocks16, (unsigned)num_kv_heads);
+    switch (src_dtype) {
+      case INT8KV_F32:
+        hipLaunchKernelGGL(cache_write16_kernel<kF32>, grid, dim3(256), 0, s, a);
+        break;
+      case INT8KV_F16:
+        hipLaunchKernelGGL(cache_write16_kernel<kF16>, grid, dim3(256), 0, s, a);
+        break;
+      default:
+        hipLaunchKernelGGL(cache_write16_kernel<kBF16>, grid, dim3(256), 0, s, a);
+        break;
+    }
+    return (int)hipGetLastError();
+  }
 
   const int64_t lanes = num_tokens * num_kv_heads * (int64_t)a.vecs_per_row;
   const int threads = 256;
   const int64_t blocks = (lanes + threads - 1) / threads;
   if (blocks > 0x7fffffffLL) return INT8KV_E_SHAPE;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   switch (src_dtype) {
     case INT8KV_F32:
       hipLaunchKernelGGL(cache_write_kernel<kF32>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
@@ -297,12 +448,33 @@ extern "C" int int8kv_dynamic_cache_write(
   d.vsc_sb = v_scale_cache_strides[0];
   d.vsc_ss = v_scale_cache_strides[1];
   d.vsc_sh = v_scale_cache_strides[2];
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  const int32_t vpr16 = head_dim / 16;
+  if (wide_ok(key_cache, value_cache, key_cache_strides, value_cache_strides, num_tokens,
+              num_kv_heads, head_dim) &&
+      (vpr16 & (vpr16 - 1)) == 0) {
+    d.w.vecs_per_row = vpr16;
+    const int64_t blocks16 = (num_tokens * vpr16 + 255) / 256;
+    const dim3 grid((unsigned)blocks16, (unsigned)num_kv_heads);
+    switch (src_dtype) {
+      case INT8KV_F32:
+        hipLaunchKernelGGL(dynamic_write16_kernel<kF32>, grid, dim3(256), 0, s, d);
+        break;
+      case INT8KV_F16:
+        hipLaunchKernelGGL(dynamic_write16_kernel<kF16>, grid, dim3(256), 0, s, d);
+        break;
+      default:
+        hipLaunchKernelGGL(dynamic_write16_kernel<kBF16>, grid, dim3(256), 0, s, d);
+        break;
+    }
+    return (int)hipGetLastError();
+  }
 
   const int64_t lanes = num_tokens * num_kv_heads * (int64_t)vpr;
   const int threads = 256;
   const int64_t blocks = (lanes + threads - 1) / threads;
   if (blocks > 0x7fffffffLL) return INT8KV_E_SHAPE;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   switch (src_dtype) {
     case INT8KV_F32:
       hipLaunchKernelGGL(dynamic_write_kernel<kF32>, dim3((unsigned)blocks), dim3(threads), 0, s, d);

@@ -25,10 +25,11 @@
 //     heads), online softmax in the exp2 domain, then out^T += V^T * P^T (2 x 8 MFMA 16x16x32,
 //     P split into 16-bit hi + lo parts; rows = head_dim, cols = heads).  The MFMA accumulator
 //     layout puts one head per lane column, so the probabilities never leave registers.
-//   * INT8 K/V are read with non-temporal loads: every byte is used once, and keeping the stream
-//     out of L2 and the Infinity Cache raises the delivered bandwidth by ~10 % on MI355X (measured
-//     on the large ragged batch, 5.4 -> 6.1 TB/s).  16-bit caches keep plain loads (see
-//     stream_load).
+//   * INT8 K/V are read with non-temporal loads when a call can stream more than the 256 MB
+//     Infinity Cache holds: every byte is used once, and keeping the stream out of L2 and the
+//     Infinity Cache raises the delivered bandwidth by ~10 % on MI355X (large ragged batch,
+//     5.4 -> 6.1 TB/s).  Smaller pools, which the cache keeps between calls, and 16-bit caches use
+//     plain loads (see stream_load).
 //   * Two tiles are in flight per wave: K(t+2) is requested as soon as the scores of tile t are
 //     formed and V(t+2) as soon as its P*V is done.  The block ids of up to 256 tiles are staged
 //     in LDS per wave ahead of use, every load in the tile loop is unconditional (requests past
@@ -261,18 +262,20 @@ __device__ __forceinline__ void store8(char* p, const float (&x)[8]) {
   }
 }
 
-// Cache-stream load: non-temporal for INT8 caches (+10 % delivered bandwidth on MI355X), plain
-// for 16-bit caches, whose wider per-lane rows (64 B of K per lane) measured ~12 % slower with
-// the non-temporal hint.
-template <int CACHE, typename T>
+// Cache-stream load.  NT (chosen per call by the host, INT8 caches only): the non-temporal hint,
+// +10 % delivered bandwidth on MI355X when the call streams more K/V than the Infinity Cache
+// holds; a small pool that the cache keeps between calls is read faster without it.  16-bit
+// caches always use plain loads: their wider per-lane rows (64 B of K per lane) measured ~12 %
+// slower with the hint.
+template <int CACHE, bool NT, typename T>
 __device__ __forceinline__ T stream_load(const T* p) {
-  if constexpr (CACHE == kI8)
+  if constexpr (CACHE == kI8 && NT)
     return __builtin_nontemporal_load(p);
   else
     return *p;
 }
 
-template <int CACHE, int NB>
+template <int CACHE, int NB, bool NT>
 __device__ __forceinline__ void issue_k(KTile<CACHE, NB>& r, const char* kb,
                                         const int64_t (&ph)[NB], const DecodeArgs& a, int li,
                                         int lg) {
@@ -282,11 +285,11 @@ __device__ __forceinline__ void issue_k(KTile<CACHE, NB>& r, const char* kb,
     const u32x4* k4 =
         reinterpret_cast<const u32x4*>(kb + ph[s] * a.kc_sb + li * a.kc_ss + lg * (32 * E));
 #pragma unroll
-    for (int i = 0; i < 2 * E; ++i) r.k[s][i] = stream_load<CACHE>(&k4[i]);
+    for (int i = 0; i < 2 * E; ++i) r.k[s][i] = stream_load<CACHE, NT>(&k4[i]);
   }
 }
 
-template <int CACHE, int NB>
+template <int CACHE, int NB, bool NT>
 __device__ __forceinline__ void issue_v(VTile<CACHE, NB>& r, const char* vb,
                                         const int64_t (&ph)[NB], const DecodeArgs& a, int li,
                                         int lg) {
@@ -297,7 +300,7 @@ __device__ __forceinline__ void issue_v(VTile<CACHE, NB>& r, const char* vb,
     const char* vp = vb + ph[s] * a.vc_sb + (4 * lg) * a.vc_ss + li * (8 * E);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr)
-      r.v[s][rr] = stream_load<CACHE>(reinterpret_cast<const Row*>(vp + rr * a.vc_ss));
+      r.v[s][rr] = stream_load<CACHE, NT>(reinterpret_cast<const Row*>(vp + rr * a.vc_ss));
   }
 }
 
@@ -563,7 +566,7 @@ __device__ __forceinline__ void write_zero_rows(const DecodeArgs& a, int64_t b, 
 
 // Processes tiles [ta, tb) of sequence b (length L) for kv head kvh with one wave, then writes
 // either the final output (full == true) or a partial record.  ids: this wave's LDS slots.
-template <int CACHE, int QT>
+template <int CACHE, int QT, bool NT>
 __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, int64_t b,
                                             int64_t L, int kvh, int64_t ta, int64_t tb,
                                             bool full, int64_t rec, int lane) {
@@ -612,11 +615,11 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   auto chunk_prologue = [&]() {
     stage_block_ids<NB>(a, ids, b, c0, c1, nblk, lane);
     blocks_of(c0, pha);
-    issue_k<CACHE, NB>(ka, kb, pha, a, li, lg);
-    issue_v<CACHE, NB>(va, vb, pha, a, li, lg);
+    issue_k<CACHE, NB, NT>(ka, kb, pha, a, li, lg);
+    issue_v<CACHE, NB, NT>(va, vb, pha, a, li, lg);
     blocks_of(c0 + 1 < c1 ? c0 + 1 : c1 - 1, phb);
-    issue_k<CACHE, NB>(kb2, kb, phb, a, li, lg);
-    issue_v<CACHE, NB>(vb2, vb, phb, a, li, lg);
+    issue_k<CACHE, NB, NT>(kb2, kb, phb, a, li, lg);
+    issue_v<CACHE, NB, NT>(vb2, vb, phb, a, li, lg);
   };
 
   // The query, the first chunk's block ids and its first two tiles are requested back to back;
@@ -640,19 +643,19 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
       int valid = valid_of(t);
       tile_scores<CACHE, NB>(ka, qop, acc, m_run, l_part, valid, lg, s_scale, pop);
       blocks_of(t + 2 < c1 ? t + 2 : last, pha);
-      issue_k<CACHE, NB>(ka, kb, pha, a, li, lg);
+      issue_k<CACHE, NB, NT>(ka, kb, pha, a, li, lg);
       __builtin_amdgcn_sched_barrier(0);
       tile_pv<CACHE, NB>(va, pop, acc, valid, lg);
-      issue_v<CACHE, NB>(va, vb, pha, a, li, lg);
+      issue_v<CACHE, NB, NT>(va, vb, pha, a, li, lg);
       __builtin_amdgcn_sched_barrier(0);
 
       valid = valid_of(t + 1);
       tile_scores<CACHE, NB>(kb2, qop, acc, m_run, l_part, valid, lg, s_scale, pop);
       blocks_of(t + 3 < c1 ? t + 3 : last, phb);
-      issue_k<CACHE, NB>(kb2, kb, phb, a, li, lg);
+      issue_k<CACHE, NB, NT>(kb2, kb, phb, a, li, lg);
       __builtin_amdgcn_sched_barrier(0);
       tile_pv<CACHE, NB>(vb2, pop, acc, valid, lg);
-      issue_v<CACHE, NB>(vb2, vb, phb, a, li, lg);
+      issue_v<CACHE, NB, NT>(vb2, vb, phb, a, li, lg);
       __builtin_amdgcn_sched_barrier(0);
     }
     if (t < c1) {  // odd tile count: the last tile is in the A buffers
@@ -700,7 +703,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
 
 // grid (max_ranges, num_kv_heads / W), block W waves; wave w of workgroup (r, y) handles
 // kv head y * W + w over stream range r.
-template <int CACHE, int QT>
+template <int CACHE, int QT, bool NT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(DecodeArgs a) {
   __shared__ int32_t s_ids[kMaxWavesPerWG][kChunkTiles * tile_blocks<CACHE>()];
   const int lane = threadIdx.x % kWave;
@@ -743,7 +746,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
         const int64_t te = (u1 < first + nb ? u1 : first + nb) - first;
         if (ta >= te) continue;
         const bool full = ta == 0 && te == nb;
-        run_segment<CACHE, QT>(a, s_ids[wave], base + j, Lb, kvh, ta, te, full,
+        run_segment<CACHE, QT, NT>(a, s_ids[wave], base + j, Lb, kvh, ta, te, full,
                                2 * r + cut_slot(ta), lane);
       }
     }
@@ -874,6 +877,7 @@ constexpr int kSeqStartCost = 2;  // stream units per sequence start (about one 
 // under a quarter of a range's K/V bytes and bound the merge of one long sequence.
 constexpr int kAutoMinTiles = 4;
 constexpr int kWavesPerCU = 8;  // resident decode waves per CU the automatic range count targets
+constexpr int64_t kInfinityCacheBytes = 256LL << 20;  // MI355X last-level (MALL) capacity
 
 // Waves per workgroup: the largest of 4, 3, 2, 1 dividing num_kv_heads.
 int waves_per_wg(int32_t num_kv_heads) {
@@ -913,11 +917,14 @@ bool shape_ok(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32
 }
 
 template <int CACHE, int QT>
-int launch(const DecodeArgs& a, uint32_t flags, hipStream_t s) {
+int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
   const int W = waves_per_wg(a.num_kv_heads);
   if (flags & INT8KV_DECODE_MAIN) {
     dim3 grid((unsigned)a.max_ranges, (unsigned)(a.num_kv_heads / W));
-    hipLaunchKernelGGL((decode_kernel<CACHE, QT>), grid, dim3(W * kWave), 0, s, a);
+    if (CACHE == kI8 && nt)
+      hipLaunchKernelGGL((decode_kernel<CACHE, QT, true>), grid, dim3(W * kWave), 0, s, a);
+    else
+      hipLaunchKernelGGL((decode_kernel<CACHE, QT, false>), grid, dim3(W * kWave), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }
@@ -931,14 +938,14 @@ int launch(const DecodeArgs& a, uint32_t flags, hipStream_t s) {
 }
 
 template <int CACHE>
-int launch_q(const DecodeArgs& a, int query_dtype, uint32_t flags, hipStream_t s) {
+int launch_q(const DecodeArgs& a, int query_dtype, uint32_t flags, bool nt, hipStream_t s) {
   switch (query_dtype) {
     case INT8KV_F32:
-      return launch<CACHE, kF32>(a, flags, s);
+      return launch<CACHE, kF32>(a, flags, nt, s);
     case INT8KV_F16:
-      return launch<CACHE, kF16>(a, flags, s);
+      return launch<CACHE, kF16>(a, flags, nt, s);
     default:
-      return launch<CACHE, kBF16>(a, flags, s);
+      return launch<CACHE, kBF16>(a, flags, nt, s);
   }
 }
 
@@ -1049,13 +1056,18 @@ extern "C" int int8kv_paged_decode(
   a.sl_is64 = seq_lens_dtype == INT8KV_I64;
   a.sm_scale_log2e = sm_scale * kLog2e;
 
+  // Non-temporal K/V loads when the call may stream more than the Infinity Cache holds: the
+  // most it can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).
+  const int64_t touch_blocks = batch * table_width < num_blocks ? batch * table_width : num_blocks;
+  const bool nt = (double)touch_blocks * block_size * num_kv_heads * head_dim * ce * 2 >
+                  (double)kInfinityCacheBytes;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (cache_dtype) {
     case INT8KV_I8:
-      return launch_q<kI8>(a, query_dtype, flags, s);
+      return launch_q<kI8>(a, query_dtype, flags, nt, s);
     case INT8KV_BF16:
-      return launch_q<kBF16>(a, query_dtype, flags, s);
+      return launch_q<kBF16>(a, query_dtype, flags, nt, s);
     default:
-      return launch_q<kF16>(a, query_dtype, flags, s);
+      return launch_q<kF16>(a, query_dtype, flags, nt, s);
   }
 }

@@ -136,6 +136,26 @@ def test_write_strided_views(cuda):
     _assert_equal(kc, vc, kr, vr)
 
 
+@pytest.mark.parametrize("head_dim,pad", [(72, 0), (128, 8), (136, 0)])
+def test_write_narrow_layouts(cuda, head_dim, pad):
+    """Layouts the 16-element kernel does not take -- head_dim % 16 == 8, or cache rows only
+    8-byte aligned (a view 8 bytes into a wider row) -- run the 8-element kernel, bit-exact."""
+    g = torch.Generator().manual_seed(head_dim + pad)
+    T, hkv, nb = 61, 4, 6
+    k = (torch.randn(T, hkv, head_dim, generator=g) * 2).to(torch.bfloat16)
+    v = torch.randn(T, hkv, head_dim, generator=g).to(torch.bfloat16)
+    ks = (k.float().abs().amax(dim=(0, 2)) / 127).clamp_min(1e-6)
+    vs = (v.float().abs().amax(dim=(0, 2)) / 127).clamp_min(1e-6)
+    slots = torch.randperm(nb * 16, generator=g)[:T]
+    slots[::9] = -1
+    big = torch.full((2, nb, 16, hkv, head_dim + 2 * pad), SENTINEL, dtype=torch.int8, device=cuda)
+    kc, vc = big[0, ..., pad:pad + head_dim], big[1, ..., pad:pad + head_dim]
+    kc, vc, kr, vr = _run(k, v, slots, ks, vs, nb, cuda, kc=kc, vc=vc)
+    _assert_equal(kc, vc, kr, vr)
+    if pad:
+        assert (big[..., :pad] == SENTINEL).all() and (big[..., pad + head_dim:] == SENTINEL).all()
+
+
 def test_write_empty_and_out_of_range(cuda):
     k = torch.zeros(0, 4, 128, dtype=torch.bfloat16, device=cuda)
     kc = torch.full((2, 16, 4, 128), SENTINEL, dtype=torch.int8, device=cuda)
@@ -216,6 +236,19 @@ def test_dynamic_write_reference_scenario(cuda):
     vd = cache_ops.dequantize_int8_cache(vc, vsc).cpu().reshape(-1, 4, 128)[slots]
     assert float((kd - key.float()).abs().mean()) < 0.02
     assert float((vd - value.float()).abs().mean()) < 0.02
+
+
+def test_dynamic_write_narrow_layout(cuda):
+    """Cache rows only 8-byte aligned: the 8-element dynamic kernel, bit-exact."""
+    g = torch.Generator().manual_seed(31)
+    T, hkv, d, nb = 37, 4, 128, 5
+    k = (torch.randn(T, hkv, d, generator=g) * 3).to(torch.bfloat16)
+    v = torch.randn(T, hkv, d, generator=g).to(torch.bfloat16)
+    big = torch.full((2, nb, 16, hkv, d + 16), SENTINEL, dtype=torch.int8, device=cuda)
+    sc = torch.full((2, nb, 16, hkv), -1.0, device=cuda)
+    slots = torch.randperm(nb * 16, generator=g)[:T]
+    got, ref = _run_dynamic(k, v, slots, nb, cuda, big[0, ..., 8:8 + d], big[1, ..., 8:8 + d], sc[0], sc[1])
+    assert all(np.array_equal(a, b) for a, b in zip(got, ref))
 
 
 def test_dynamic_write_strided_views(cuda):

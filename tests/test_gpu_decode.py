@@ -257,3 +257,24 @@ def test_matches_reference_torch_checkers_on_device(cuda):
     torch_int8_kv_cache_write_reference(k, v, b_k, b_v, slots, ks, vs)
     torch.cuda.synchronize()
     assert torch.equal(a_k, b_k) and torch.equal(a_v, b_v)
+
+
+def test_large_pool_streaming_path(cuda):
+    """A pool larger than the Infinity Cache (the most a call can read exceeds 256 MB) takes the
+    non-temporal streaming loads; results stay within the bar against the oracle, and equal the
+    small-pool call on the same blocks."""
+    c = decode_case([5, 700, 1234, 33], seed=41, extra_blocks=3)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    big_nb, width = 40000, 10000
+    assert 4 * width * 16 * 4 * 128 * 2 > 256 << 20
+    kb = torch.zeros(big_nb, 16, 4, 128, dtype=torch.int8, device=cuda)
+    vb = torch.zeros_like(kb)
+    kb[: kc.shape[0]] = kc
+    vb[: vc.shape[0]] = vc
+    btw = torch.zeros(bt.shape[0], width, dtype=bt.dtype, device=cuda)
+    btw[:, : bt.shape[1]] = bt
+    small = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs)
+    big = int8kv.int8_paged_attention(q, kb, vb, btw, sl, ks, vs)
+    torch.cuda.synchronize()
+    _check(big, oracle_int8(c), "large pool")
+    assert torch.equal(small, big)
