@@ -295,7 +295,8 @@ def sweep_configs(dev, out_path: str | None) -> dict:
 
 
 def tpot_config4(dev, out_path: str | None, batch: int = 32, context: int = 8192,
-                 new_tokens: int = 128, layers: int = 28) -> dict:
+                 new_tokens: int = 128, layers: int = 28, gemm_tuning: str = "use",
+                 tuning_file: str | None = None) -> dict:
     """Config 4: greedy decode of a random-init Qwen2.5-7B-shaped bf16 model, INT8 vs BF16 KV.
 
     B sequences of ``context`` random prompt ids, ``new_tokens`` greedy tokens each; attention
@@ -311,6 +312,7 @@ def tpot_config4(dev, out_path: str | None, batch: int = 32, context: int = 8192
     from int8kv import decode_loop as DL
 
     shape = dataclasses.replace(DL.QWEN25_7B, layers=layers)
+    tuned = DL.configure_gemm_tuning(gemm_tuning, tuning_file or DL.GEMM_TUNING_FILE)
     torch.zeros(1, device=dev)  # initialises the allocator before its statistics are reset
     torch.cuda.reset_peak_memory_stats(dev)
     t0 = time.perf_counter()
@@ -321,7 +323,8 @@ def tpot_config4(dev, out_path: str | None, batch: int = 32, context: int = 8192
     scales = DL.calibrate_static_scales(weights, calib)
     res = {"config": {"model": "random-init Qwen2.5-7B shape (bf16)", **dataclasses.asdict(shape),
                       "batch": batch, "context": context, "new_tokens": new_tokens,
-                      "calibration": "4 x 512 random ids, absmax/127 of post-rotary K and V"},
+                      "calibration": "4 x 512 random ids, absmax/127 of post-rotary K and V",
+                      "gemm_tuning": gemm_tuning if tuned else "off"},
            "runs": []}
     gens, step1, first = {}, {}, {}
     for mode in DL.MODES:
@@ -376,6 +379,10 @@ def main() -> int:
                     help="run only config 4 (no headline line)")
     ap.add_argument("--tpot-shape", default="32,8192,128,28", metavar="B,CTX,NEW,LAYERS",
                     help="config-4 batch, prompt length, new tokens and layer count")
+    ap.add_argument("--gemm-tuning", default="use", choices=("off", "use", "tune"),
+                    help="config 4: torch GEMM solution choice (TunableOp results file, or tune it)")
+    ap.add_argument("--gemm-tuning-file", default=None,
+                    help="config 4: TunableOp results file (default: the one shipped with int8kv)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -395,7 +402,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     tpot_args = [int(x) for x in args.tpot_shape.split(",")]
     if args.tpot_only:
-        tpot_config4(dev, args.tpot, *tpot_args)
+        tpot_config4(dev, args.tpot, *tpot_args, gemm_tuning=args.gemm_tuning,
+                     tuning_file=args.gemm_tuning_file)
         return 0
     log("building workload (B=64, ctx ~ U[1, 32768]) ...")
     w = build_workload(dev, seed=args.seed)
@@ -490,7 +498,8 @@ def main() -> int:
     if args.tpot:
         del w
         torch.cuda.empty_cache()
-        tpot_config4(dev, args.tpot, *tpot_args)
+        tpot_config4(dev, args.tpot, *tpot_args, gemm_tuning=args.gemm_tuning,
+                     tuning_file=args.gemm_tuning_file)
     if args.calibrate_copy:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)

@@ -30,6 +30,7 @@ from __future__ import annotations
 
 import time
 from dataclasses import dataclass, field
+from pathlib import Path
 
 import torch
 import torch.nn.functional as F
@@ -58,6 +59,45 @@ class QwenShape:
 QWEN25_7B = QwenShape()
 BLOCK_SIZE = 16
 MODES = ("int8", "bf16")
+
+# hipBLASLt solutions chosen by torch's TunableOp for the decode step's GEMMs (M = batch rows)
+# on MI355X; written by ``configure_gemm_tuning("tune", ...)`` and read back with "use".
+GEMM_TUNING_FILE = Path(__file__).resolve().parent / "gemm_tuning_mi355x.csv"
+GEMM_TUNING_MODES = ("off", "use", "tune")
+
+
+def configure_gemm_tuning(mode: str, path: Path | str = GEMM_TUNING_FILE) -> bool:
+    """Selects how the decode loop's torch GEMMs pick their hipBLASLt/rocBLAS solutions.
+
+    "off": torch's default heuristics.  "use": TunableOp with the solutions recorded in ``path``
+    (shapes not in the file keep the default; nothing is tuned).  "tune": TunableOp tunes each
+    new GEMM shape the first time it runs eagerly (``DecodeLoop`` tunes only during the decode
+    warm-up step) against a 1 GB rotating buffer, so the timings see cold weights as the model
+    does; the results are written to ``path`` when the process exits.  A file whose validators
+    (torch, HIP, hipBLASLt, rocBLAS versions, GPU arch) do not match is ignored by torch.
+    Returns whether TunableOp is on.
+    """
+    import torch.cuda.tunable as tunable
+
+    if mode not in GEMM_TUNING_MODES:
+        raise ValueError(f"gemm tuning mode must be one of {GEMM_TUNING_MODES}, got {mode!r}")
+    if mode == "off":
+        tunable.enable(False)
+        return False
+    path = Path(path)
+    tunable.enable(True)
+    tunable.tuning_enable(False)
+    tunable.set_filename(str(path), insert_device_ordinal=False)
+    if mode == "tune":
+        tunable.set_rotating_buffer_size(1024)
+        tunable.set_max_tuning_duration(100)
+    if path.exists():
+        tunable.read_file(str(path))
+    _TUNING["tune"] = mode == "tune"
+    return True
+
+
+_TUNING = {"tune": False}
 
 
 def blocks_per_sequence(max_len: int, block_size: int = BLOCK_SIZE) -> int:
@@ -446,8 +486,14 @@ class DecodeLoop:
         saved = self.state()
         side = torch.cuda.Stream(self.dev)
         side.wait_stream(torch.cuda.current_stream(self.dev))
+        if _TUNING["tune"]:
+            import torch.cuda.tunable as tunable
+
+            tunable.tuning_enable(True)
         with torch.cuda.stream(side):
             self.step_eager()
+        if _TUNING["tune"]:
+            tunable.tuning_enable(False)
         torch.cuda.current_stream(self.dev).wait_stream(side)
         self.restore(saved)
         torch.cuda.synchronize(self.dev)
