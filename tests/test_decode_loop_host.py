@@ -122,3 +122,19 @@ def test_calibration_cpu_tiny_model():
     vmax = v.abs().amax(dim=(0, 1, 3))
     assert torch.allclose(ks[0] * 127, kmax, rtol=1e-5)
     assert torch.allclose(vs[0] * 127, vmax, rtol=1e-5)
+
+
+def test_gemm_tuning_modes_and_shipped_file():
+    """The shipped TunableOp file covers exactly the decode step's five GEMM shapes at M = 32."""
+    with pytest.raises(ValueError):
+        DL.configure_gemm_tuning("fast")
+    assert DL.configure_gemm_tuning("off") is False
+    rows = [ln.split(",") for ln in DL.GEMM_TUNING_FILE.read_text().splitlines()]
+    validators = {r[1] for r in rows if r[0] == "Validator"}
+    assert {"PT_VERSION", "HIPBLASLT_VERSION", "GCN_ARCH_NAME"} <= validators
+    shapes = sorted(r[1] for r in rows if r[0] != "Validator")
+    s = DL.QWEN25_7B
+    want = sorted(f"tn_{n}_32_{k}_ld_{k}_{k}_{n}" for n, k in (
+        (s.qkv_width, s.hidden), (s.hidden, s.q_heads * s.head_dim), (2 * s.ffn, s.hidden),
+        (s.hidden, s.ffn), (s.vocab, s.hidden)))
+    assert shapes == want
