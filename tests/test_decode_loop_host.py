@@ -126,9 +126,8 @@ def test_calibration_cpu_tiny_model():
 
 def test_gemm_tuning_modes_and_shipped_file():
     """The shipped TunableOp file covers exactly the decode step's five GEMM shapes at M = 32."""
-    with pytest.raises(ValueError):
+    with pytest.raises(ValueError):  # rejected before torch's TunableOp (which needs a GPU)
         DL.configure_gemm_tuning("fast")
-    assert DL.configure_gemm_tuning("off") is False
     rows = [ln.split(",") for ln in DL.GEMM_TUNING_FILE.read_text().splitlines()]
     validators = {r[1] for r in rows if r[0] == "Validator"}
     assert {"PT_VERSION", "HIPBLASLT_VERSION", "GCN_ARCH_NAME"} <= validators
