@@ -225,6 +225,7 @@ def sweep_configs(dev, out_path: str | None) -> dict:
     sequence.  Both working sets fit the 256 MB Infinity Cache, so their GB/s are cache-resident
     rates and µs/call is the meaningful figure.  Times are device times per call from HIP-graph
     replays (a few-microsecond call is otherwise dominated by the host's launch cost)."""
+    import numpy as np
     import torch
 
     import int8kv
@@ -251,6 +252,67 @@ def sweep_configs(dev, out_path: str | None) -> dict:
     res["cfg1_write"] = {"tokens": n_tok, "padding_slots": n_pad, "us_per_call": round(ms_w * 1e3, 2),
                          "algorithmic_bytes": wbytes, "GBps": round(wbytes / ms_w / 1e6, 1)}
     log(f"cfg1 write: {ms_w * 1e3:.1f} us ({wbytes / ms_w / 1e6:.0f} GB/s)")
+
+    # The dynamic per-(token, head) write (reshape_and_cache_int8) on the same inputs: the same
+    # bytes plus one fp32 scale per (token, head) for K and V.
+    from int8kv import cache_ops
+
+    kcd, vcd = torch.zeros_like(kc), torch.zeros_like(vc)
+    ksc = torch.zeros(nb, 16, 4, dtype=torch.float32, device=dev)
+    vsc = torch.zeros_like(ksc)
+
+    def dyn_write():
+        cache_ops.reshape_and_cache_int8(k, v, kcd, vcd, ksc, vsc, slots_d)
+
+    ms_d = time_graph(dyn_write)
+    dbytes = wbytes - 2 * 4 * 4 + n_tok * 4 * 4 * 2
+    res["cfg1_dynamic_write"] = {"us_per_call": round(ms_d * 1e3, 2), "algorithmic_bytes": dbytes,
+                                 "GBps": round(dbytes / ms_d / 1e6, 1)}
+    log(f"cfg1 dynamic write: {ms_d * 1e3:.1f} us ({dbytes / ms_d / 1e6:.0f} GB/s)")
+
+    # The CPU oracle's static write on the same inputs (numpy, one thread), for comparison.
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    kn, vn, sn = k.float().cpu().numpy(), v.float().cpu().numpy(), slots.numpy()
+    kcn = np.zeros((nb, 16, 4, 128), np.int8)
+    vcn = np.zeros_like(kcn)
+    ctx = threadpool_limits(limits=1) if threadpool_limits else None
+    if ctx:
+        ctx.__enter__()
+    try:
+        t0 = time.perf_counter()
+        O.int8_kv_cache_write(kn, vn, kcn, vcn, sn, ks.numpy(), vs.numpy())
+        t_cpu = time.perf_counter() - t0
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    same = bool(np.array_equal(kcn, kc.cpu().numpy()) and np.array_equal(vcn, vc.cpu().numpy()))
+    res["cfg1_write_cpu_oracle"] = {"seconds": round(t_cpu, 4), "GBps": round(wbytes / t_cpu / 1e9, 3),
+                                    "cores": 1, "kind": "port", "gpu_caches_bit_exact": same}
+    log(f"cfg1 write on the CPU oracle: {t_cpu * 1e3:.1f} ms ({wbytes / t_cpu / 1e9:.2f} GB/s); "
+        f"GPU caches bit-exact: {same}")
+
+    # HBM-sized writes: 262,144 tokens into a 32,768-block pool (the sources alone exceed the
+    # Infinity Cache).
+    n_big, nb_big = 262144, 32768
+    gb = torch.Generator(device=dev).manual_seed(13)
+    kb_, vb_ = syn.sample_kv(n_big, dist, gb, device=dev)
+    sb_ = torch.randperm(nb_big * 16, device=dev, generator=gb)[:n_big]
+    kcb = torch.zeros(nb_big, 16, 4, 128, dtype=torch.int8, device=dev)
+    vcb = torch.zeros_like(kcb)
+    kscb = torch.zeros(nb_big, 16, 4, dtype=torch.float32, device=dev)
+    vscb = torch.zeros_like(kscb)
+    big_bytes = n_big * 4 * 128 * 6 + n_big * 8 + 32
+    ms_sb = time_loop(lambda: int8kv.int8_kv_cache_write(kb_, vb_, kcb, vcb, sb_, ks_d, vs_d), 40, 10)
+    ms_db = time_loop(lambda: cache_ops.reshape_and_cache_int8(kb_, vb_, kcb, vcb, kscb, vscb, sb_), 40, 10)
+    res["hbm_write_262k"] = {
+        "tokens": n_big, "static_us": round(ms_sb * 1e3, 2),
+        "static_GBps": round(big_bytes / ms_sb / 1e6, 1), "dynamic_us": round(ms_db * 1e3, 2),
+        "dynamic_GBps": round((big_bytes - 32 + n_big * 32) / ms_db / 1e6, 1)}
+    log(f"262k-token writes: static {ms_sb * 1e3:.1f} us, dynamic {ms_db * 1e3:.1f} us")
+    del kb_, vb_, sb_, kcb, vcb, kscb, vscb
 
     rows = []
     for B in (1, 2, 4, 8):
@@ -440,11 +502,13 @@ def main() -> int:
     # (an event pair around one launch would mostly measure launch latency).
     ms_merge = time_loop(merge_kernel, args.steps, args.warmup)
     ms16 = time_loop(bf16_call, args.steps, args.warmup)
+    ms_q = time_loop(lambda: int8kv.int8_paged_attention(w["q"], w["kc"], w["vc"], w["bt"], w["sl"], w["ks"],
+                                                         w["vs"], quantize_q=True), args.steps, args.warmup)
     value = nbytes8 / (ms * 1e-3) / 1e9
     achieved = nbytes8 / (ms_main * 1e-3) / 1e9
     log(f"int8 op: {ms * 1e3:.1f} us/call ({value:.0f} GB/s); decode kernel {ms_main * 1e3:.1f} us "
         f"({achieved:.0f} GB/s); merge kernel {ms_merge * 1e3:.1f} us; bf16 op {ms16 * 1e3:.1f} us "
-        f"({nbytes16 / (ms16 * 1e-3) / 1e9:.0f} GB/s)")
+        f"({nbytes16 / (ms16 * 1e-3) / 1e9:.0f} GB/s); int8 quantize_q op {ms_q * 1e3:.1f} us")
 
     result = {
         "metric": METRIC,
@@ -472,6 +536,7 @@ def main() -> int:
             "int8_speedup_vs_bf16": round(ms16 / ms, 3),
             "decode_kernel_us": round(ms_main * 1e3, 2),
             "merge_kernel_us_back_to_back": round(ms_merge * 1e3, 2),
+            "int8_quantize_q_us_per_call": round(ms_q * 1e3, 2),
             "frac_of_hbm_peak_whole_call": round(value / HBM_PEAK_GBS, 4),
         },
         "roofline": {
