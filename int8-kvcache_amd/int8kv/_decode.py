@@ -26,6 +26,30 @@ def _aligned16(t: torch.Tensor, dims) -> bool:
 
 MAX_RANGES = 1 << 20
 
+# Decode workspaces reused across calls, one per (device, stream): calls on one stream run in
+# order, so they never use it at the same time.  A call under HIP-graph capture gets its own
+# (allocated from the graph's pool), so a graph never shares memory with eager calls.
+_WORKSPACES: dict = {}
+_WS_BYTES: dict = {}
+
+
+def _workspace_bytes(lib, Hq, Hkv, D, block_size, num_ranges) -> int:
+    key = (Hq, Hkv, D, block_size, num_ranges)
+    need = _WS_BYTES.get(key)
+    if need is None:
+        need = _WS_BYTES[key] = lib.int8kv_decode_workspace_bytes(Hq, Hkv, D, block_size, num_ranges)
+    return need
+
+
+def _cached_workspace(dev, stream: int, need: int) -> torch.Tensor:
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    key = (dev.index, stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = _WORKSPACES[key] = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    return ws
+
 
 def ranges_for(batch: int, num_splits) -> int:
     """Range count for a forced split count (0 = let the library choose).
@@ -73,11 +97,13 @@ def paged_decode(
         return out
     if not _aligned16(query, (0, 1)):
         query = query.contiguous()
-    seq_lens = seq_lens.contiguous()
+    if not seq_lens.is_contiguous():
+        seq_lens = seq_lens.contiguous()
     lib = _lib.load()
-    need = lib.int8kv_decode_workspace_bytes(Hq, Hkv, D, block_size, num_ranges)
+    stream = _lib.stream_handle(dev)
+    need = _workspace_bytes(lib, Hq, Hkv, D, block_size, num_ranges)
     if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+        workspace = _cached_workspace(dev, stream, need)
     status = lib.int8kv_paged_decode(
         query.data_ptr(),
         _lib.DTYPE_CODE[query.dtype],
@@ -109,7 +135,7 @@ def paged_decode(
         num_ranges,
         min_tiles,
         flags,
-        _lib.stream_handle(dev),
+        stream,
     )
     _lib.check(status, "int8kv_paged_decode")
     return out

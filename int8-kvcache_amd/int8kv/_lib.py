@@ -87,9 +87,19 @@ def load() -> ctypes.CDLL:
     return lib
 
 
+_STRIDE_ARRAYS: dict = {}
+
+
 def strides(t: torch.Tensor):
+    """The tensor's strides as a ctypes int64 array (cached per stride tuple; the library only
+    reads them during the call)."""
     st = t.stride()
-    return (ctypes.c_int64 * len(st))(*st)
+    arr = _STRIDE_ARRAYS.get(st)
+    if arr is None:
+        if len(_STRIDE_ARRAYS) > 4096:
+            _STRIDE_ARRAYS.clear()
+        arr = _STRIDE_ARRAYS[st] = (ctypes.c_int64 * len(st))(*st)
+    return arr
 
 
 def check(status: int, what: str) -> None:
@@ -98,5 +108,13 @@ def check(status: int, what: str) -> None:
         raise Int8KVError(f"{what} failed: {msg}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """hipStream_t of torch's current stream on ``device`` (the raw handle, read without building
+    a torch Stream object)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(idx)
+    return torch.cuda.current_stream(idx).cuda_stream

@@ -35,9 +35,10 @@ def bf16_paged_attention(
     assert cache_D == D and Hq % Hkv == 0
     assert block_tables.shape[0] == B and seq_lens.numel() == B
     assert key_cache.stride(-1) == 1 and value_cache.stride(-1) == 1
-    tensors = (query, key_cache, value_cache, block_tables, seq_lens)
-    assert all(t.is_cuda for t in tensors), "bf16_paged_attention needs GPU tensors"
-    assert all(t.device == query.device for t in tensors), "all tensors must be on one device"
+    dev = query.device
+    assert query.is_cuda, "bf16_paged_attention needs GPU tensors"
+    assert (key_cache.device == dev and value_cache.device == dev and block_tables.device == dev
+            and seq_lens.device == dev), "all tensors must be on one device (the GPU)"
     if _decode.DEBUG_CHECKS:
         _decode.debug_check(block_tables, seq_lens, num_blocks, block_size, False)
     ranges = _decode.ranges_for(B, num_splits)

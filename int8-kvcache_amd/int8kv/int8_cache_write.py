@@ -59,10 +59,11 @@ def int8_kv_cache_write(
     assert k_scale.ndim == 1 and v_scale.ndim == 1
     assert k_scale.numel() == num_kv_heads and v_scale.numel() == num_kv_heads
     assert slot_mapping.dtype in (torch.int32, torch.int64)
-    tensors = (key, value, key_cache, value_cache, slot_mapping, k_scale, v_scale)
-    assert all(t.is_cuda for t in tensors), "int8_kv_cache_write needs GPU tensors"
     dev = key.device
-    assert all(t.device == dev for t in tensors), "all tensors must be on one device"
+    assert key.is_cuda, "int8_kv_cache_write needs GPU tensors"
+    assert (value.device == dev and key_cache.device == dev and value_cache.device == dev
+            and slot_mapping.device == dev and k_scale.device == dev and v_scale.device == dev), \
+        "all tensors must be on one device (the GPU)"
     assert key_cache.stride(-1) == 1 and value_cache.stride(-1) == 1
 
     if num_tokens == 0:
@@ -74,9 +75,12 @@ def int8_kv_cache_write(
         key = key.contiguous()
     if not _aligned16(value):
         value = value.contiguous()
-    k_scale = k_scale.to(torch.float32).contiguous()
-    v_scale = v_scale.to(torch.float32).contiguous()
-    slot_mapping = slot_mapping.contiguous()
+    if k_scale.dtype != torch.float32 or not k_scale.is_contiguous():
+        k_scale = k_scale.to(torch.float32).contiguous()
+    if v_scale.dtype != torch.float32 or not v_scale.is_contiguous():
+        v_scale = v_scale.to(torch.float32).contiguous()
+    if not slot_mapping.is_contiguous():
+        slot_mapping = slot_mapping.contiguous()
 
     lib = _lib.load()
     status = lib.int8kv_cache_write(

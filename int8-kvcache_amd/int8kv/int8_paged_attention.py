@@ -60,20 +60,24 @@ def int8_paged_attention(
     assert k_scale.ndim == 1 and v_scale.ndim == 1
     assert k_scale.numel() == Hkv and v_scale.numel() == Hkv
     assert key_cache.stride(-1) == 1 and value_cache.stride(-1) == 1
-    tensors = (query, key_cache, value_cache, block_tables, seq_lens, k_scale, v_scale)
-    assert all(t.is_cuda for t in tensors), "int8_paged_attention needs GPU tensors"
-    assert all(t.device == query.device for t in tensors), "all tensors must be on one device"
+    dev = query.device
+    assert query.is_cuda, "int8_paged_attention needs GPU tensors"
+    assert (key_cache.device == dev and value_cache.device == dev and block_tables.device == dev
+            and seq_lens.device == dev and k_scale.device == dev and v_scale.device == dev), \
+        "all tensors must be on one device (the GPU)"
     if impl not in ("auto", "v3", "v4"):
         raise ValueError(f"Unknown impl={impl!r}; expected 'auto', 'v3' or 'v4'")
     if _decode.DEBUG_CHECKS:
         _decode.debug_check(block_tables, seq_lens, num_blocks, block_size, True)
 
-    k_scale = k_scale.to(torch.float32).contiguous()
-    v_scale = v_scale.to(torch.float32).contiguous()
+    if k_scale.dtype != torch.float32 or not k_scale.is_contiguous():
+        k_scale = k_scale.to(torch.float32).contiguous()
+    if v_scale.dtype != torch.float32 or not v_scale.is_contiguous():
+        v_scale = v_scale.to(torch.float32).contiguous()
     if impl == "v3" and num_splits is None:
         num_splits = 1
     ranges = _decode.ranges_for(B, num_splits)
-    output = torch.empty((B, Hq, D), device=query.device, dtype=query.dtype)
+    output = torch.empty((B, Hq, D), device=dev, dtype=query.dtype)
     flags = _lib.DECODE_ALL | (_lib.DECODE_QUANTIZE_Q if quantize_q else 0)
     return _decode.paged_decode(
         query, key_cache, value_cache, block_tables, seq_lens, k_scale, v_scale, output, ranges,
