@@ -62,6 +62,17 @@ def ranges_for(batch: int, num_splits) -> int:
     return max(1, min(MAX_RANGES, int(num_splits) * max(1, int(batch))))
 
 
+def debug_check_slots(slot_mapping, num_blocks: int, block_size: int) -> None:
+    """Host-side check of a write's slot_mapping (INT8KV_DEBUG=1): every non-negative slot lies
+    inside the cache and appears once.  The write kernels skip out-of-range slots and give each
+    token its own lanes, so two tokens with one slot would race on that cache row."""
+    s = slot_mapping.to("cpu", torch.int64)
+    s = s[s >= 0]
+    assert bool((s < num_blocks * block_size).all()), "slot_mapping holds a slot beyond the cache"
+    assert int(torch.unique(s).numel()) == int(s.numel()), \
+        "slot_mapping repeats a slot: two tokens would write one cache row concurrently"
+
+
 def debug_check(block_tables, seq_lens, num_blocks, block_size, require_positive) -> None:
     lens = seq_lens.to("cpu", torch.int64)
     if require_positive:

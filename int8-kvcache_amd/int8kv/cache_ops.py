@@ -15,7 +15,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _decode, _lib
 from .int8_cache_write import int8_kv_cache_write
 
 _SRC_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
@@ -65,6 +65,8 @@ def reshape_and_cache_int8(
                                          v_scale_cache, slot_mapping))
     if num_tokens == 0:
         return
+    if _decode.DEBUG_CHECKS:
+        _decode.debug_check_slots(slot_mapping, num_blocks, block_size)
     if value.dtype != key.dtype:
         key, value = key.float(), value.float()
     if not _aligned16(key):

@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _decode, _lib
 from .torch_reference import torch_int8_kv_cache_write_reference  # noqa: F401  (reference checker)
 
 _SRC_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
@@ -68,6 +68,8 @@ def int8_kv_cache_write(
 
     if num_tokens == 0:
         return
+    if _decode.DEBUG_CHECKS:
+        _decode.debug_check_slots(slot_mapping, num_blocks, block_size)
     if value.dtype != key.dtype:
         # One source type per launch; widening to fp32 is exact, so the quotients are unchanged.
         key, value = key.float(), value.float()

@@ -264,3 +264,23 @@ def test_dynamic_write_strided_views(cuda):
     slots = torch.randperm(nb * 16, generator=g)[:T]
     got, ref = _run_dynamic(key, value, slots, nb, cuda, kv[:, 0], kv[:, 1], sc[0], sc[1])
     assert all(np.array_equal(a, b) for a, b in zip(got, ref))
+
+
+def test_debug_checks_reject_duplicate_slots(cuda, monkeypatch):
+    """With INT8KV_DEBUG on, a duplicated slot raises before the write is launched (the caches
+    keep their sentinel)."""
+    from int8kv import _decode, cache_ops
+
+    monkeypatch.setattr(_decode, "DEBUG_CHECKS", True)
+    k = torch.ones(3, 4, 128, dtype=torch.bfloat16, device=cuda)
+    kc = torch.full((2, 16, 4, 128), SENTINEL, dtype=torch.int8, device=cuda)
+    vc = kc.clone()
+    s = torch.ones(4, device=cuda)
+    slots = torch.tensor([4, 9, 4], dtype=torch.int64, device=cuda)
+    with pytest.raises(AssertionError, match="repeats"):
+        int8kv.int8_kv_cache_write(k, k, kc, vc, slots, s, s)
+    ksc = torch.zeros(2, 16, 4, device=cuda)
+    with pytest.raises(AssertionError, match="repeats"):
+        cache_ops.reshape_and_cache_int8(k, k, kc, vc, ksc, ksc.clone(), slots)
+    torch.cuda.synchronize()
+    assert (kc == SENTINEL).all() and (vc == SENTINEL).all()

@@ -159,3 +159,18 @@ def test_vllm_int8_module_aliases():
                 sys.modules.pop(k, None)
             else:
                 sys.modules[k] = v
+
+
+def test_debug_slot_check():
+    """INT8KV_DEBUG's slot_mapping check: duplicates and out-of-cache slots are rejected on the
+    host (before any launch); -1 padding and distinct in-range slots pass."""
+    import pytest
+    import torch
+
+    from int8kv import _decode
+
+    _decode.debug_check_slots(torch.tensor([3, -1, 7, -1, 0]), num_blocks=1, block_size=16)
+    with pytest.raises(AssertionError, match="repeats"):
+        _decode.debug_check_slots(torch.tensor([3, 5, 3]), num_blocks=1, block_size=16)
+    with pytest.raises(AssertionError, match="beyond"):
+        _decode.debug_check_slots(torch.tensor([3, 16]), num_blocks=1, block_size=16)
