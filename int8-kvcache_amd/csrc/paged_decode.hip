@@ -788,19 +788,18 @@ __device__ __forceinline__ void merge_in(float& M, float& L, f32x4& O, float m, 
   M = Mn;
 }
 
-// Combines the partials of every sequence cut by range bounds.  grid (batch, num_q_heads),
-// kMergeWaves waves per query head.  Lane (range parity, column) of wave w owns 4 head_dim
-// elements of ranges 2w + parity, 2w + parity + 2 kMergeWaves, ... and folds them in with one
-// online-softmax pass, four ranges' loads in flight at a time (32 ranges per round for the
-// workgroup); the 2 kMergeWaves running states per column are then merged through LDS.  A
-// sequence's merge costs about 1 + nr / 32 dependent memory latencies.
-constexpr int kMergeWaves = 4;
-
-template <int CACHE, int QT>
-__global__ __launch_bounds__(kMergeWaves * 64) void merge_kernel(DecodeArgs a) {
-  __shared__ float s_m[2 * kMergeWaves][32];
-  __shared__ float s_l[2 * kMergeWaves][32];
-  __shared__ f32x4 s_o[2 * kMergeWaves][32];
+// Combines the partials of every sequence cut by range bounds.  grid (batch, num_q_heads), MW
+// waves per query head.  Lane (range parity, column) of wave w owns 4 head_dim elements of ranges
+// 2w + parity, 2w + parity + 2 MW, ... and folds them in with one online-softmax pass, four
+// ranges' loads in flight at a time (8 MW ranges per round for the workgroup); the 2 MW running
+// states per column are then merged through LDS.  A sequence's merge costs about
+// 1 + nr / (8 MW) dependent memory latencies; the host picks MW from the average number of
+// ranges per sequence (one wave when a round covers them, up to four for a few long sequences).
+template <int CACHE, int QT, int MW>
+__global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
+  __shared__ float s_m[2 * MW][32];
+  __shared__ float s_l[2 * MW][32];
+  __shared__ f32x4 s_o[2 * MW][32];
   const int64_t b = blockIdx.x;
   const int h = blockIdx.y;
   const int kvh = h / a.group;
@@ -808,7 +807,7 @@ __global__ __launch_bounds__(kMergeWaves * 64) void merge_kernel(DecodeArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int rs = lane >> 5;  // range parity handled by this lane
   const int c4 = lane & 31;  // head_dim elements [4 c4, 4 c4 + 4)
-  const int slot = 2 * wave + rs;  // 0 .. 2 kMergeWaves - 1
+  const int slot = 2 * wave + rs;  // 0 .. 2 MW - 1
 
   const Plan plan = make_plan(a, lane);
   int64_t S = 0;  // stream units before sequence b
@@ -827,7 +826,7 @@ __global__ __launch_bounds__(kMergeWaves * 64) void merge_kernel(DecodeArgs a) {
     return (2 * (r0 + c) + cut_slot(c)) * a.num_q_heads + h;  // tile 0 lies in range r0
   };
 
-  constexpr int kStride = 2 * kMergeWaves;
+  constexpr int kStride = 2 * MW;
   float M = -INFINITY, L = 0.0f;
   f32x4 O = (f32x4)(0.0f);
   for (int64_t cb = slot; cb < nr; cb += 4 * kStride) {
@@ -930,7 +929,15 @@ int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
   }
   if (flags & INT8KV_DECODE_MERGE) {
     dim3 grid((unsigned)a.batch, (unsigned)a.num_q_heads);
-    hipLaunchKernelGGL((merge_kernel<CACHE, QT>), grid, dim3(kMergeWaves * kWave), 0, s, a);
+    // Ranges per sequence on average; one round of a wave takes 8 of them.
+    const int64_t per_seq = ((int64_t)a.max_ranges + a.batch - 1) / a.batch;
+    const int64_t mw = (per_seq + 7) / 8;
+    if (mw <= 1)
+      hipLaunchKernelGGL((merge_kernel<CACHE, QT, 1>), grid, dim3(kWave), 0, s, a);
+    else if (mw == 2)
+      hipLaunchKernelGGL((merge_kernel<CACHE, QT, 2>), grid, dim3(2 * kWave), 0, s, a);
+    else
+      hipLaunchKernelGGL((merge_kernel<CACHE, QT, 4>), grid, dim3(4 * kWave), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }
