@@ -52,12 +52,12 @@
 namespace int8kv {
 
 constexpr int kHeadDim = 128;
-constexpr int kBlock = 16;          // tokens per cache block
+constexpr int kRows = 16;           // tokens per MFMA row group (half a tile)
 constexpr int kMaxGroup = 16;       // query heads per kv head (MFMA column count)
 constexpr int kChunkTiles = 256;    // tiles whose block ids a wave stages in LDS at a time
 constexpr int kMaxWavesPerWG = 4;
 
-// Cache blocks per wave iteration ("tile"): 32 tokens, one MFMA k-step of P*V.
+// 16-token row groups per wave iteration ("tile"): 32 tokens, one MFMA k-step of P*V.
 template <int CACHE>
 constexpr int tile_blocks() {
   return 2;
@@ -93,6 +93,7 @@ struct DecodeArgs {
   int32_t seq_cost;    // stream units charged for starting a sequence (see make_plan)
   int32_t quantize_q;  // quantise q per (sequence, head) to int8 first (the reference's option)
   int32_t tile_tokens;  // 16 * tile_blocks<CACHE>()
+  int32_t block_shift;  // log2(cache block size); the block size is a power of two >= 16
   int32_t bt_is64;
   int32_t sl_is64;
   float sm_scale_log2e;
@@ -130,7 +131,7 @@ __device__ __forceinline__ int64_t readlane64(int64_t x, int lane) {
 __device__ __forceinline__ int64_t seq_len_of(const DecodeArgs& a, int64_t b) {
   if (b >= a.batch) return 0;
   int64_t L = load_index(a.sl, b, a.sl_is64);
-  const int64_t cap = (int64_t)a.width * kBlock;
+  const int64_t cap = (int64_t)a.width << a.block_shift;
   return L < 0 ? 0 : (L > cap ? cap : L);
 }
 
@@ -275,15 +276,23 @@ __device__ __forceinline__ T stream_load(const T* p) {
     return *p;
 }
 
+// Where each 16-token row group of a tile starts: its cache block and its first row in the block.
+template <int NB>
+struct TileRows {
+  int32_t id[NB];
+  int32_t row[NB];
+};
+
 template <int CACHE, int NB, bool NT>
 __device__ __forceinline__ void issue_k(KTile<CACHE, NB>& r, const char* kb,
-                                        const int64_t (&ph)[NB], const DecodeArgs& a, int li,
+                                        const TileRows<NB>& ph, const DecodeArgs& a, int li,
                                         int lg) {
   constexpr int E = esize<CACHE>();
 #pragma unroll
   for (int s = 0; s < NB; ++s) {
     const u32x4* k4 =
-        reinterpret_cast<const u32x4*>(kb + ph[s] * a.kc_sb + li * a.kc_ss + lg * (32 * E));
+        reinterpret_cast<const u32x4*>(kb + ph.id[s] * a.kc_sb + (ph.row[s] + li) * a.kc_ss +
+                                       lg * (32 * E));
 #pragma unroll
     for (int i = 0; i < 2 * E; ++i) r.k[s][i] = stream_load<CACHE, NT>(&k4[i]);
   }
@@ -291,13 +300,13 @@ __device__ __forceinline__ void issue_k(KTile<CACHE, NB>& r, const char* kb,
 
 template <int CACHE, int NB, bool NT>
 __device__ __forceinline__ void issue_v(VTile<CACHE, NB>& r, const char* vb,
-                                        const int64_t (&ph)[NB], const DecodeArgs& a, int li,
+                                        const TileRows<NB>& ph, const DecodeArgs& a, int li,
                                         int lg) {
   constexpr int E = esize<CACHE>();
   typedef typename VRow<CACHE>::T Row;
 #pragma unroll
   for (int s = 0; s < NB; ++s) {
-    const char* vp = vb + ph[s] * a.vc_sb + (4 * lg) * a.vc_ss + li * (8 * E);
+    const char* vp = vb + ph.id[s] * a.vc_sb + (ph.row[s] + 4 * lg) * a.vc_ss + li * (8 * E);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr)
       r.v[s][rr] = stream_load<CACHE, NT>(reinterpret_cast<const Row*>(vp + rr * a.vc_ss));
@@ -317,7 +326,7 @@ __device__ __forceinline__ void tile_scores(const KTile<CACHE, NB>& r,
                                             int valid, int lg, float s_scale,
                                             typename MfmaOp<CACHE>::T (&pop)[NB / 2][2]) {
   typedef typename MfmaOp<CACHE>::T OpT;
-  constexpr int kTileTokens = NB * kBlock;
+  constexpr int kTileTokens = NB * kRows;
   // ---- scores S^T[token][head] for each block of the tile ----
   f32x4 S[NB];
 #pragma unroll
@@ -385,7 +394,7 @@ __device__ __forceinline__ void tile_pv(VTile<CACHE, NB>& r,
   typedef typename MfmaOp<CACHE>::T OpT;
   if constexpr (CACHE != kI8) {
     // 16-bit rows past the sequence end may hold non-finite garbage; 0 * NaN would leak.
-    if (valid < NB * kBlock) {
+    if (valid < NB * kRows) {
 #pragma unroll
       for (int s = 0; s < NB; ++s)
 #pragma unroll
@@ -537,15 +546,18 @@ __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRa
 }
 
 // Stages the physical block ids of tiles [c0, c1) of sequence b (nblk blocks) in this wave's
-// LDS slots: ids[NB * (t - c0) + s] = block s of tile t, 0 past the sequence's last block and
-// clamped into [0, num_blocks) so every access stays inside the caches.
+// LDS slots, one per 16-token row group: ids[NB * (t - c0) + s] = the block holding row group s
+// of tile t (tokens 16 (NB t + s) .. + 15; consecutive row groups share a block when the block
+// size exceeds 16), 0 past the sequence's last block and clamped into [0, num_blocks) so every
+// access stays inside the caches.
 template <int NB>
 __device__ __forceinline__ void stage_block_ids(const DecodeArgs& a, int32_t* ids, int64_t b,
                                                 int64_t c0, int64_t c1, int64_t nblk, int lane) {
   const int n = (int)(NB * (c1 - c0));
   const int64_t hi = a.num_blocks - 1;
+  const int gshift = a.block_shift - 4;  // row groups per block = 2^gshift
   for (int j = lane; j < n; j += kWave) {
-    const int64_t blk = NB * c0 + j;
+    const int64_t blk = (NB * c0 + j) >> gshift;
     int64_t p = 0;
     if (blk < nblk) p = load_index(a.bt, b * a.bt_sb + blk * a.bt_sl, a.bt_is64);
     ids[j] = (int32_t)(p < 0 ? 0 : (p > hi ? hi : p));
@@ -583,9 +595,9 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
 
   const char* kb = a.kc + (int64_t)kvh * a.kc_sh;
   const char* vb = a.vc + (int64_t)kvh * a.vc_sh;
-  const int64_t nblk = (L + kBlock - 1) / kBlock;
+  const int64_t nblk = (L + (1 << a.block_shift) - 1) >> a.block_shift;
   constexpr int NB = tile_blocks<CACHE>();
-  constexpr int kTileTokens = NB * kBlock;
+  constexpr int kTileTokens = NB * kRows;
 
   auto valid_of = [&](int64_t t) -> int {
     const int64_t v = L - t * kTileTokens;
@@ -596,10 +608,14 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   // (read through the LDS counter, so the waits on tile loads below only ever count tile loads).
   int64_t c0 = ta;
   int64_t c1 = (tb - c0 > kChunkTiles) ? c0 + kChunkTiles : tb;
-  auto blocks_of = [&](int64_t t, int64_t (&ph)[NB]) {
+  const int gmask = (1 << (a.block_shift - 4)) - 1;  // row group within its block
+  auto blocks_of = [&](int64_t t, TileRows<NB>& ph) {
     const int j = NB * (int)(t - c0);
 #pragma unroll
-    for (int s = 0; s < NB; ++s) ph[s] = __builtin_amdgcn_readfirstlane(ids[j + s]);
+    for (int s = 0; s < NB; ++s) {
+      ph.id[s] = __builtin_amdgcn_readfirstlane(ids[j + s]);
+      ph.row[s] = (((int)t * NB + s) & gmask) * kRows;
+    }
   };
 
   // Two K and two V register buffers, refilled as soon as they are consumed: K(t + 2) is
@@ -610,7 +626,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   // are exact and no wait drains the pipeline.
   KTile<CACHE, NB> ka, kb2;
   VTile<CACHE, NB> va, vb2;
-  int64_t pha[NB], phb[NB];
+  TileRows<NB> pha, phb;
   OpT pop[NB / 2][2];
   auto chunk_prologue = [&]() {
     stage_block_ids<NB>(a, ids, b, c0, c1, nblk, lane);
@@ -910,9 +926,17 @@ bool aligned16(const void* p, int64_t stride_bytes) {
   return ((uintptr_t)p % 16) == 0 && (stride_bytes % 16) == 0;
 }
 
+// Cache block sizes: powers of two from one 16-token row group up to kMaxBlock.
+constexpr int32_t kMaxBlock = 1 << 16;
+
+bool block_size_ok(int32_t block_size) {
+  return block_size >= kRows && block_size <= kMaxBlock && (block_size & (block_size - 1)) == 0;
+}
+
 bool shape_ok(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size) {
   return num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0 &&
-         num_q_heads / num_kv_heads <= kMaxGroup && head_dim == kHeadDim && block_size == kBlock;
+         num_q_heads / num_kv_heads <= kMaxGroup && head_dim == kHeadDim &&
+         block_size_ok(block_size);
 }
 
 template <int CACHE, int QT>
@@ -1058,7 +1082,8 @@ extern "C" int int8kv_paged_decode(
   a.min_tiles = min_tiles;
   a.seq_cost = kSeqStartCost;
   a.quantize_q = (flags & INT8KV_DECODE_QUANTIZE_Q) != 0;
-  a.tile_tokens = kBlock * (cache_dtype == INT8KV_I8 ? tile_blocks<kI8>() : tile_blocks<kBF16>());
+  a.block_shift = __builtin_ctz((unsigned)block_size);
+  a.tile_tokens = kRows * (cache_dtype == INT8KV_I8 ? tile_blocks<kI8>() : tile_blocks<kBF16>());
   a.bt_is64 = table_dtype == INT8KV_I64;
   a.sl_is64 = seq_lens_dtype == INT8KV_I64;
   a.sm_scale_log2e = sm_scale * kLog2e;

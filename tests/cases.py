@@ -16,7 +16,7 @@ class DecodeCase:
     query: torch.Tensor  # CPU bf16 [B, Hq, D]
     key: torch.Tensor  # CPU bf16 [T_total, Hkv, D] (token order, sequences concatenated)
     value: torch.Tensor
-    kc: np.ndarray  # oracle int8 caches [NB, 16, Hkv, D]
+    kc: np.ndarray  # oracle int8 caches [NB, BS, Hkv, D]
     vc: np.ndarray
     block_tables: torch.Tensor  # CPU int32 [B, width]
     seq_lens: torch.Tensor  # CPU int32 [B]
@@ -24,10 +24,11 @@ class DecodeCase:
     k_scale: torch.Tensor  # CPU fp32 [Hkv]
     v_scale: torch.Tensor
     num_blocks: int
+    block_size: int = 16
 
 
 def decode_case(lens, seed=0, hq=28, hkv=4, extra_blocks=17, width=None, randn_kv=False,
-                fill=None) -> DecodeCase:
+                fill=None, block_size=16) -> DecodeCase:
     """Sequences of the given lengths written into a shuffled block pool.
 
     randn_kv=True uses the reference tests' inputs (K, V ~ N(0, 1), scales = absmax/127 of the
@@ -47,13 +48,14 @@ def decode_case(lens, seed=0, hq=28, hkv=4, extra_blocks=17, width=None, randn_k
         ks, vs = syn.calibrate_scales(dist, seed=seed + 1)
         k, v = syn.sample_kv(total, dist, g)
     q = torch.randn(len(lens), hq, 128, generator=g).to(torch.bfloat16)
-    nblk = sum((n + 15) // 16 for n in lens)
+    bs = block_size
+    nblk = sum((n + bs - 1) // bs for n in lens)
     nb = nblk + extra_blocks
     if fill is None:
         fill = nb - 1
-    bt = syn.random_block_tables(lens, nb, g, width=width, fill=fill)
-    slots = syn.slot_mapping_for(bt, lens)
-    kc = np.zeros((nb, 16, hkv, 128), np.int8)
+    bt = syn.random_block_tables(lens, nb, g, width=width, block_size=bs, fill=fill)
+    slots = syn.slot_mapping_for(bt, lens, block_size=bs)
+    kc = np.zeros((nb, bs, hkv, 128), np.int8)
     vc = np.zeros_like(kc)
     # Unwritten slots hold random bytes: the kernels must never read them into a result.
     rng = np.random.default_rng(seed + 7)
@@ -61,7 +63,8 @@ def decode_case(lens, seed=0, hq=28, hkv=4, extra_blocks=17, width=None, randn_k
     vc[:] = rng.integers(-128, 128, vc.shape, dtype=np.int8)
     O.int8_kv_cache_write(k.float().numpy(), v.float().numpy(), kc, vc, slots.numpy(),
                           ks.numpy(), vs.numpy())
-    return DecodeCase(q, k, v, kc, vc, bt, torch.tensor(lens, dtype=torch.int32), slots, ks, vs, nb)
+    return DecodeCase(q, k, v, kc, vc, bt, torch.tensor(lens, dtype=torch.int32), slots, ks, vs, nb,
+                      bs)
 
 
 def oracle_int8(c: DecodeCase, query=None) -> np.ndarray:
@@ -75,11 +78,12 @@ def bf16_caches(c: DecodeCase, dtype=torch.bfloat16):
     nb = c.num_blocks
     hkv = c.key.shape[1]
     g = torch.Generator().manual_seed(123)
-    kc = torch.randn(nb * 16, hkv, 128, generator=g).to(dtype)
-    vc = torch.randn(nb * 16, hkv, 128, generator=g).to(dtype)
+    bs = c.block_size
+    kc = torch.randn(nb * bs, hkv, 128, generator=g).to(dtype)
+    vc = torch.randn(nb * bs, hkv, 128, generator=g).to(dtype)
     kc[c.slots] = c.key.to(dtype)
     vc[c.slots] = c.value.to(dtype)
-    return kc.view(nb, 16, hkv, 128), vc.view(nb, 16, hkv, 128)
+    return kc.view(nb, bs, hkv, 128), vc.view(nb, bs, hkv, 128)
 
 
 def to_dev(c: DecodeCase, dev):

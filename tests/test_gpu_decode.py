@@ -278,3 +278,54 @@ def test_large_pool_streaming_path(cuda):
     torch.cuda.synchronize()
     _check(big, oracle_int8(c), "large pool")
     assert torch.equal(small, big)
+
+
+@pytest.mark.parametrize("block_size", [32, 64, 256])
+def test_block_sizes(cuda, block_size):
+    """Cache blocks of 32+ tokens (vLLM's other block sizes): oracle parity, INT8 and BF16, at
+    block, tile and split boundaries."""
+    lens = [1, 31, 32, 33, 63, 64, 65, 255, 256, 257, 1000, 2049]
+    c = decode_case(lens, seed=block_size, block_size=block_size, extra_blocks=5)
+    ref = oracle_int8(c)
+    for splits in (None, 1, 3, 7):
+        _check(_int8(c, cuda, num_splits=splits), ref, f"int8 bs={block_size} splits={splits}")
+    kc, vc = bf16_caches(c)
+    ref16 = O.paged_attention_ref(c.query.float().numpy(), kc.float().numpy(), vc.float().numpy(),
+                                  c.block_tables.numpy(), c.seq_lens.numpy())
+    for splits in (None, 3):
+        out = int8kv.bf16_paged_attention(c.query.to(cuda), kc.to(cuda), vc.to(cuda),
+                                          c.block_tables.to(cuda), c.seq_lens.to(cuda),
+                                          num_splits=splits)
+        torch.cuda.synchronize()
+        _check(out, ref16, f"bf16 bs={block_size} splits={splits}")
+
+
+def test_block_size_relabelling_is_bit_exact(cuda):
+    """A 32-token-block cache read as 16-token blocks (ids 2p, 2p + 1) is the same bytes in the
+    same token order: the two calls must agree bit for bit, INT8 and BF16."""
+    lens = [5, 32, 33, 700, 1, 4096, 95]
+    c = decode_case(lens, seed=21, block_size=32, extra_blocks=3)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    nb = kc.shape[0]
+    bt16 = torch.stack([2 * bt, 2 * bt + 1], dim=2).reshape(bt.shape[0], -1).contiguous()
+    kc16, vc16 = kc.view(2 * nb, 16, 4, 128), vc.view(2 * nb, 16, 4, 128)
+    for splits in (None, 1, 4):
+        a = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs, num_splits=splits)
+        b = int8kv.int8_paged_attention(q, kc16, vc16, bt16, sl, ks, vs, num_splits=splits)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"int8 splits={splits}"
+    k32, v32 = (x.to(cuda) for x in bf16_caches(c))
+    a = int8kv.bf16_paged_attention(q, k32, v32, bt, sl)
+    b = int8kv.bf16_paged_attention(q, k32.view(2 * nb, 16, 4, 128), v32.view(2 * nb, 16, 4, 128),
+                                    bt16, sl)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_unsupported_block_sizes_raise(cuda):
+    c = decode_case([40], seed=3)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    for bs in (8, 24, 48):
+        kx = torch.zeros(64, bs, 4, 128, dtype=torch.int8, device=cuda)
+        with pytest.raises(RuntimeError, match="E_SHAPE"):
+            int8kv.int8_paged_attention(q, kx, kx.clone(), bt, sl, ks, vs)
