@@ -159,7 +159,9 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *                 each; a sequence cut by range bounds is combined by the merge kernel.
  *                 0 = automatic (int8kv_decode_auto_ranges).  num_ranges = batch gives one
  *                 range per sequence when all lengths are equal (a single pass).
- *   min_tiles:    smallest range in tiles (0 = automatic, 4).
+ *   min_tiles:    smallest range in tiles (0 = automatic: 2, or 4 when 2-tile ranges could cut
+ *                 one sequence into more than 128 ranges; decided from batch, table width and
+ *                 block size only).
  *   flags:        INT8KV_DECODE_ALL normally; MAIN and MERGE separately let a caller time the
  *                 two kernels on their own (MERGE must follow MAIN with identical arguments).
  *                 OR INT8KV_DECODE_QUANTIZE_Q to quantise each (sequence, query head) row of q

@@ -45,6 +45,7 @@
 //   * A running max is only moved when a tile's max exceeds it by more than 8 (log2 units), so
 //     most tiles skip the accumulator rescale; probabilities are then <= 2^8 (fits fp16/bf16).
 
+#include <cmath>
 #include <type_traits>
 
 #include "int8kv_common.h"
@@ -148,9 +149,11 @@ struct Plan {
   int64_t P;
 };
 
-__device__ __forceinline__ Plan make_plan(const DecodeArgs& a, int lane) {
-  int64_t U = 0;
-  for (int64_t base = 0; base < a.batch; base += kWave)
+// L0: this lane's seq_len_of(a, lane), the first 64 sequences' lengths, which the caller keeps
+// in a register for its own walk over the batch (most batches have at most 64 sequences).
+__device__ __forceinline__ Plan make_plan(const DecodeArgs& a, int lane, int64_t L0) {
+  int64_t U = wave_sum(units_of(a, tiles_of(a, L0)));
+  for (int64_t base = kWave; base < a.batch; base += kWave)
     U += wave_sum(units_of(a, tiles_of(a, seq_len_of(a, base + lane))));
   int64_t P = (U + a.min_tiles - 1) / a.min_tiles;
   P = P < 1 ? 1 : (P > a.max_ranges ? a.max_ranges : P);
@@ -727,7 +730,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   const int kvh = blockIdx.y * (blockDim.x / kWave) + wave;
   const int64_t r = blockIdx.x;
 
-  const Plan plan = make_plan(a, lane);
+  const int64_t L0 = seq_len_of(a, lane);
+  const Plan plan = make_plan(a, lane, L0);
   if (r >= plan.P) return;
   const int64_t u0 = range_start(plan, r);
   const int64_t u1 = range_start(plan, r + 1);
@@ -735,7 +739,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
 
   int64_t cum = 0;  // units of the sequences before this 64-sequence chunk
   for (int64_t base = 0; base < a.batch; base += kWave) {
-    const int64_t L = seq_len_of(a, base + lane);
+    const int64_t L = base == 0 ? L0 : seq_len_of(a, base + lane);
     const int64_t n = tiles_of(a, L);
     const int64_t u = units_of(a, n);
     const int64_t incl = wave_inclusive_scan(u, lane) + cum;
@@ -825,13 +829,15 @@ __global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
   const int c4 = lane & 31;  // head_dim elements [4 c4, 4 c4 + 4)
   const int slot = 2 * wave + rs;  // 0 .. 2 MW - 1
 
-  const Plan plan = make_plan(a, lane);
+  const int64_t L0 = seq_len_of(a, lane);
+  const Plan plan = make_plan(a, lane, L0);
   int64_t S = 0;  // stream units before sequence b
   for (int64_t base = 0; base < b; base += kWave) {
     const int64_t bb = base + lane;
-    S += wave_sum(bb < b ? units_of(a, tiles_of(a, seq_len_of(a, bb))) : 0);
+    const int64_t Lb = base == 0 ? L0 : seq_len_of(a, bb);
+    S += wave_sum(bb < b ? units_of(a, tiles_of(a, Lb)) : 0);
   }
-  const int64_t n = tiles_of(a, seq_len_of(a, b));
+  const int64_t n = tiles_of(a, b < kWave ? readlane64(L0, (int)b) : seq_len_of(a, b));
   if (n == 0) return;  // zeros written by decode_kernel
   const int64_t first = S + a.seq_cost;  // unit of tile 0
   const int64_t r0 = range_of(plan, first);
@@ -888,9 +894,10 @@ namespace {
 
 constexpr int kMaxRangesLimit = 1 << 20;
 constexpr int kSeqStartCost = 2;  // stream units per sequence start (about one tile's time each)
-// Smallest automatic range: 4 tiles keep the partial records (3.6 KB per kv head and range)
-// under a quarter of a range's K/V bytes and bound the merge of one long sequence.
-constexpr int kAutoMinTiles = 4;
+// Smallest automatic range (see auto_min_tiles).
+constexpr int kMinTilesSmall = 2;
+constexpr int kMinTilesLarge = 4;
+constexpr int64_t kMaxMergeRanges = 128;  // ranges per sequence the merge takes in 4 rounds
 constexpr int kWavesPerCU = 8;  // resident decode waves per CU the automatic range count targets
 constexpr int64_t kInfinityCacheBytes = 256LL << 20;  // MI355X last-level (MALL) capacity
 
@@ -911,6 +918,19 @@ int cu_count() {
     n = 256;
   if (dev >= 0 && dev < 64) cached[dev] = n;
   return n;
+}
+
+// Smallest automatic range, from host-side bounds only.  A call whose units stay below the range
+// cap is latency-bound: 2-tile ranges need one K/V round trip instead of two (MI355X: 1.5-2 us
+// less per call for B <= 16 at 512-8192 tokens), unless that cuts a sequence into more than
+// kMaxMergeRanges ranges, whose merge then costs more (one 32k-token sequence cut 512 ways: +6 us).
+// 4 tiles also keep the partial records (3.6 KB per kv head and range) under a quarter of a
+// range's K/V bytes.
+int32_t auto_min_tiles(int64_t batch, int64_t table_width, int32_t block_size, int32_t ranges) {
+  const double tiles = std::ceil((double)table_width * block_size / 32.0);  // longest sequence
+  const double units = (double)batch * (tiles + kSeqStartCost);
+  const double p = std::fmin(std::ceil(units / kMinTilesSmall), (double)ranges);
+  return p <= (double)kMaxMergeRanges * (double)batch ? kMinTilesSmall : kMinTilesLarge;
 }
 
 int32_t auto_ranges(int32_t num_kv_heads) {
@@ -1041,7 +1061,7 @@ extern "C" int int8kv_paged_decode(
   }
 
   if (num_ranges == 0) num_ranges = auto_ranges(num_kv_heads);
-  if (min_tiles == 0) min_tiles = kAutoMinTiles;
+  if (min_tiles == 0) min_tiles = auto_min_tiles(batch, table_width, block_size, num_ranges);
   const size_t need = workspace_bytes(num_q_heads, num_ranges);
   if (workspace == nullptr || workspace_bytes_given < need || ((uintptr_t)workspace % 16) != 0)
     return INT8KV_E_WORKSPACE;
