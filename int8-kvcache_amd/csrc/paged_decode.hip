@@ -15,7 +15,7 @@
 //     distribution.  The unit counts and the range bounds are computed on the device from
 //     seq_lens; the host never reads them.
 //   * A workgroup owns one range for W kv heads, one wave per kv head.  The W waves read the
-//     same cache blocks (their head slices of the same 16-token rows) at the same time.  A wave
+//     same cache rows (their head slices of the same 16-token row groups) at the same time.  A wave
 //     handles all query heads of its GQA group on the matrix cores, so every K/V byte is read
 //     from HBM exactly once, and needs no barrier.
 //   * A sequence wholly inside one range is finished by that wave (output written directly).
@@ -173,10 +173,11 @@ __device__ __forceinline__ int64_t range_of(const Plan& p, int64_t x) {
 __device__ __forceinline__ int64_t cut_slot(int64_t first_tile) { return first_tile > 0 ? 0 : 1; }
 
 // ------------------------------------------------------------------------ tile registers
-// Registers holding the K or the V half of one tile (NB cache blocks) for one lane.
-//   K: lane (i = lane % 16, g = lane / 16) holds token i of block s, head_dim elements
+// Registers holding the K or the V half of one tile (NB 16-token row groups) for one lane.
+//   K: lane (i = lane % 16, g = lane / 16) holds token i of row group s, head_dim elements
 //      [32g, 32g + 32).
-//   V: lane (i, g) holds tokens 4g + r (r = 0..3) of block s, head_dim elements [8i, 8i + 8).
+//   V: lane (i, g) holds tokens 4g + r (r = 0..3) of row group s, head_dim elements
+//      [8i, 8i + 8).
 template <int CACHE>
 struct VRow {
   typedef u32x4 T;  // 8 16-bit elements
@@ -316,7 +317,7 @@ __device__ __forceinline__ void issue_v(VTile<CACHE, NB>& r, const char* vb,
   }
 }
 
-// Scores of one tile (NB cache blocks) and the online-softmax update: rescales acc/l_part when
+// Scores of one tile (NB row groups) and the online-softmax update: rescales acc/l_part when
 // the running max moves and returns the P^T operands (one per MFMA k-step of 32 tokens) as a
 // hi + lo pair of 16-bit values (p = hi + lo to about 2^-22 relative), so that P*V on the
 // 16-bit matrix cores keeps fp32 accuracy: the rounding of p would otherwise dominate the error
@@ -389,7 +390,7 @@ __device__ __forceinline__ void tile_scores(const KTile<CACHE, NB>& r,
 
 // out^T[dim][head] += V^T[dim][token] * P^T[token][head] for one tile.
 // MFMA row i of dim tile dt is head_dim element 8i + dt; k-slot e of lane group g in k-step
-// kst is token (block 2 kst + e / 4, row 4g + e % 4), matching the P^T operands.
+// kst is token (row group 2 kst + e / 4, row 4g + e % 4), matching the P^T operands.
 template <int CACHE, int NB>
 __device__ __forceinline__ void tile_pv(VTile<CACHE, NB>& r,
                                         const typename MfmaOp<CACHE>::T (&pop)[NB / 2][2],
