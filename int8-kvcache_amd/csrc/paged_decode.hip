@@ -220,6 +220,14 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Exact int8 x int8 -> int32 product of a 16x64 and a 64x16 tile (lane (i, g): row/column i,
+// 16 k-slots of group g).
+__device__ __forceinline__ i32x4 mfma_i8(u32x4 a, i32x4 b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Byte permute: result byte k = byte sel_k of the 8-byte value {hi, lo} (0-3 from lo).
@@ -323,18 +331,30 @@ __device__ __forceinline__ void issue_v(VTile<CACHE, NB>& r, const char* vb,
 // 16-bit matrix cores keeps fp32 accuracy: the rounding of p would otherwise dominate the error
 // (2^-12 relative for fp16, 2^-9 for bf16).
 //   valid: number of tokens of this tile inside the sequence (1..16 NB).
-template <int CACHE, int NB>
+//   QQ (INT8 cache with a quantised query): the scores are the exact integer products of the
+//   int8 K rows and q8 on the int8 matrix cores (2 k-steps of 64, no K conversion); otherwise
+//   K is converted to 16-bit operands (4 k-steps of 32).
+template <int CACHE, int NB, bool QQ>
 __device__ __forceinline__ void tile_scores(const KTile<CACHE, NB>& r,
                                             const typename MfmaOp<CACHE>::T (&qop)[4],
-                                            f32x4 (&acc)[8], float& m_run, float& l_part,
-                                            int valid, int lg, float s_scale,
+                                            const i32x4 (&q8op)[2], f32x4 (&acc)[8],
+                                            float& m_run, float& l_part, int valid, int lg,
+                                            float s_scale,
                                             typename MfmaOp<CACHE>::T (&pop)[NB / 2][2]) {
   typedef typename MfmaOp<CACHE>::T OpT;
   constexpr int kTileTokens = NB * kRows;
-  // ---- scores S^T[token][head] for each block of the tile ----
+  // ---- scores S^T[token][head] for each row group of the tile ----
   f32x4 S[NB];
 #pragma unroll
   for (int s = 0; s < NB; ++s) {
+    if constexpr (QQ) {
+      i32x4 si = (i32x4)(0);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) si = mfma_i8(r.k[s][ks], q8op[ks], si);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) S[s][rr] = (float)si[rr];
+      continue;
+    }
     S[s] = (f32x4)(0.0f);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -492,10 +512,13 @@ __device__ __forceinline__ float round_half_away(float x) {
 //     operands (exact for bf16 input, never overflows); bf16 operands take q as is;
 //   * quantize_q: per (sequence, head) q_scale = max(absmax / 127, 1e-6) and
 //     q8 = clamp(round_half_away(q / q_scale), -127, 127) (src/triton_ops/int8_paged_attention.py:
-//     137-146, :798-802); the operand is q8 and q_scale joins the score factor.
-template <int CACHE, int QT>
+//     137-146, :798-802); the operand is q8 and q_scale joins the score factor.  With QQ the
+//     q8 values are packed as int8 operands instead (q8op[ks] byte e of lane (li, lg) =
+//     q8[li][32 lg + 16 ks + e], matching the int8 K bytes the lane holds).
+template <int CACHE, int QT, bool QQ>
 __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRaw<QT>& raw,
-                                              int kvh, typename MfmaOp<CACHE>::T (&qop)[4]) {
+                                              int kvh, typename MfmaOp<CACHE>::T (&qop)[4],
+                                              i32x4 (&q8op)[2]) {
   float x[4][8];
   if constexpr (QT == kF32) {
 #pragma unroll
@@ -520,6 +543,22 @@ __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRa
     amax = fmaxf(amax, __shfl_xor(amax, 16));
     amax = fmaxf(amax, __shfl_xor(amax, 32));
     const float qs = fmaxf(amax / 127.0f, 1e-6f);
+    if constexpr (QQ) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          uint32_t word = 0;
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb) {
+            const int d = 16 * ks + 4 * w + bb;  // element of the lane's 32
+            const float v = fminf(fmaxf(round_half_away(x[d / 8][d % 8] / qs), -127.0f), 127.0f);
+            word |= ((uint32_t)(int32_t)v & 0xffu) << (8 * bb);
+          }
+          q8op[ks][w] = (int32_t)word;
+        }
+      return s_scale * qs;
+    }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -582,7 +621,7 @@ __device__ __forceinline__ void write_zero_rows(const DecodeArgs& a, int64_t b, 
 
 // Processes tiles [ta, tb) of sequence b (length L) for kv head kvh with one wave, then writes
 // either the final output (full == true) or a partial record.  ids: this wave's LDS slots.
-template <int CACHE, int QT, bool NT>
+template <int CACHE, int QT, bool NT, bool QQ>
 __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, int64_t b,
                                             int64_t L, int kvh, int64_t ta, int64_t tb,
                                             bool full, int64_t rec, int lane) {
@@ -646,12 +685,13 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   // the query operand is built once they are all in flight (otherwise three memory latencies
   // would line up at every segment start).
   OpT qop[4];
+  i32x4 q8op[2];
   float s_scale;
   {
     QueryRaw<QT> qraw;
     issue_query<QT>(a, b, kvh, li, lg, qraw);
     chunk_prologue();
-    s_scale = finish_query<CACHE, QT>(a, qraw, kvh, qop);
+    s_scale = finish_query<CACHE, QT, QQ>(a, qraw, kvh, qop, q8op);
   }
 
   while (true) {
@@ -661,7 +701,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     // compute that follows them (which would shorten the prefetch distance).
     for (; t + 1 < c1; t += 2) {
       int valid = valid_of(t);
-      tile_scores<CACHE, NB>(ka, qop, acc, m_run, l_part, valid, lg, s_scale, pop);
+      tile_scores<CACHE, NB, QQ>(ka, qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
       blocks_of(t + 2 < c1 ? t + 2 : last, pha);
       issue_k<CACHE, NB, NT>(ka, kb, pha, a, li, lg);
       __builtin_amdgcn_sched_barrier(0);
@@ -670,7 +710,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
       __builtin_amdgcn_sched_barrier(0);
 
       valid = valid_of(t + 1);
-      tile_scores<CACHE, NB>(kb2, qop, acc, m_run, l_part, valid, lg, s_scale, pop);
+      tile_scores<CACHE, NB, QQ>(kb2, qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
       blocks_of(t + 3 < c1 ? t + 3 : last, phb);
       issue_k<CACHE, NB, NT>(kb2, kb, phb, a, li, lg);
       __builtin_amdgcn_sched_barrier(0);
@@ -680,7 +720,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     }
     if (t < c1) {  // odd tile count: the last tile is in the A buffers
       const int valid = valid_of(t);
-      tile_scores<CACHE, NB>(ka, qop, acc, m_run, l_part, valid, lg, s_scale, pop);
+      tile_scores<CACHE, NB, QQ>(ka, qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
       tile_pv<CACHE, NB>(va, pop, acc, valid, lg);
     }
     if (c1 >= tb) break;
@@ -723,7 +763,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
 
 // grid (max_ranges, num_kv_heads / W), block W waves; wave w of workgroup (r, y) handles
 // kv head y * W + w over stream range r.
-template <int CACHE, int QT, bool NT>
+template <int CACHE, int QT, bool NT, bool QQ>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(DecodeArgs a) {
   __shared__ int32_t s_ids[kMaxWavesPerWG][kChunkTiles * tile_blocks<CACHE>()];
   const int lane = threadIdx.x % kWave;
@@ -739,8 +779,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
   const bool last_range = r == plan.P - 1;
 
   int64_t cum = 0;  // units of the sequences before this 64-sequence chunk
+  int64_t L = L0;
   for (int64_t base = 0; base < a.batch; base += kWave) {
-    const int64_t L = base == 0 ? L0 : seq_len_of(a, base + lane);
+    if (base > 0) L = seq_len_of(a, base + lane);
     const int64_t n = tiles_of(a, L);
     const int64_t u = units_of(a, n);
     const int64_t incl = wave_inclusive_scan(u, lane) + cum;
@@ -767,7 +808,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void d
         const int64_t te = (u1 < first + nb ? u1 : first + nb) - first;
         if (ta >= te) continue;
         const bool full = ta == 0 && te == nb;
-        run_segment<CACHE, QT, NT>(a, s_ids[wave], base + j, Lb, kvh, ta, te, full,
+        run_segment<CACHE, QT, NT, QQ>(a, s_ids[wave], base + j, Lb, kvh, ta, te, full,
                                2 * r + cut_slot(ta), lane);
       }
     }
@@ -965,10 +1006,19 @@ int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
   const int W = waves_per_wg(a.num_kv_heads);
   if (flags & INT8KV_DECODE_MAIN) {
     dim3 grid((unsigned)a.max_ranges, (unsigned)(a.num_kv_heads / W));
-    if (CACHE == kI8 && nt)
-      hipLaunchKernelGGL((decode_kernel<CACHE, QT, true>), grid, dim3(W * kWave), 0, s, a);
-    else
-      hipLaunchKernelGGL((decode_kernel<CACHE, QT, false>), grid, dim3(W * kWave), 0, s, a);
+    // INT8 caches: non-temporal loads for large pools, int8 scores for a quantised query.
+    if constexpr (CACHE == kI8) {
+      if (nt && a.quantize_q)
+        hipLaunchKernelGGL((decode_kernel<CACHE, QT, true, true>), grid, dim3(W * kWave), 0, s, a);
+      else if (nt)
+        hipLaunchKernelGGL((decode_kernel<CACHE, QT, true, false>), grid, dim3(W * kWave), 0, s, a);
+      else if (a.quantize_q)
+        hipLaunchKernelGGL((decode_kernel<CACHE, QT, false, true>), grid, dim3(W * kWave), 0, s, a);
+      else
+        hipLaunchKernelGGL((decode_kernel<CACHE, QT, false, false>), grid, dim3(W * kWave), 0, s, a);
+    } else {
+      hipLaunchKernelGGL((decode_kernel<CACHE, QT, false, false>), grid, dim3(W * kWave), 0, s, a);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }

@@ -278,6 +278,15 @@ def test_large_pool_streaming_path(cuda):
     torch.cuda.synchronize()
     _check(big, oracle_int8(c), "large pool")
     assert torch.equal(small, big)
+    # the int8-score kernel (quantize_q) on the streaming path as well
+    small_q = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs, quantize_q=True)
+    big_q = int8kv.int8_paged_attention(q, kb, vb, btw, sl, ks, vs, quantize_q=True)
+    torch.cuda.synchronize()
+    ref_q = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                  c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
+                                  quantize_q=True)
+    _check(big_q, ref_q, "large pool quantize_q")
+    assert torch.equal(small_q, big_q)
 
 
 @pytest.mark.parametrize("block_size", [32, 64, 256])
@@ -289,6 +298,10 @@ def test_block_sizes(cuda, block_size):
     ref = oracle_int8(c)
     for splits in (None, 1, 3, 7):
         _check(_int8(c, cuda, num_splits=splits), ref, f"int8 bs={block_size} splits={splits}")
+    ref_q = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                  c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
+                                  quantize_q=True)
+    _check(_int8(c, cuda, quantize_q=True), ref_q, f"int8 quantize_q bs={block_size}")
     kc, vc = bf16_caches(c)
     ref16 = O.paged_attention_ref(c.query.float().numpy(), kc.float().numpy(), vc.float().numpy(),
                                   c.block_tables.numpy(), c.seq_lens.numpy())
