@@ -107,7 +107,7 @@ def paged_decode(
     if B == 0:
         return out
     if not _aligned16(query, (0, 1)):
-        query = query.contiguous()
+        query = _lib.aligned_rows(query)
     if not seq_lens.is_contiguous():
         seq_lens = seq_lens.contiguous()
     lib = _lib.load()

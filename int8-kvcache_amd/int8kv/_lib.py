@@ -102,6 +102,13 @@ def strides(t: torch.Tensor):
     return arr
 
 
+def aligned_rows(t: torch.Tensor) -> torch.Tensor:
+    """A contiguous copy of ``t`` at a fresh (16-byte aligned) address: for inputs whose rows
+    the kernels could not read with 16-byte loads.  ``contiguous()`` alone keeps a misaligned
+    storage offset of an already contiguous view."""
+    return t.clone(memory_format=torch.contiguous_format)
+
+
 def check(status: int, what: str) -> None:
     if status != 0:
         msg = ERRORS.get(status, f"hipError_t {status}")

@@ -70,9 +70,9 @@ def reshape_and_cache_int8(
     if value.dtype != key.dtype:
         key, value = key.float(), value.float()
     if not _aligned16(key):
-        key = key.contiguous()
+        key = _lib.aligned_rows(key)
     if not _aligned16(value):
-        value = value.contiguous()
+        value = _lib.aligned_rows(value)
     slot_mapping = slot_mapping.contiguous()
     status = _lib.load().int8kv_dynamic_cache_write(
         key.data_ptr(), value.data_ptr(), _lib.DTYPE_CODE[key.dtype], num_tokens, num_kv_heads,

@@ -74,9 +74,9 @@ def int8_kv_cache_write(
         # One source type per launch; widening to fp32 is exact, so the quotients are unchanged.
         key, value = key.float(), value.float()
     if not _aligned16(key):
-        key = key.contiguous()
+        key = _lib.aligned_rows(key)
     if not _aligned16(value):
-        value = value.contiguous()
+        value = _lib.aligned_rows(value)
     if k_scale.dtype != torch.float32 or not k_scale.is_contiguous():
         k_scale = k_scale.to(torch.float32).contiguous()
     if v_scale.dtype != torch.float32 or not v_scale.is_contiguous():

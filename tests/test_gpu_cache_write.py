@@ -284,3 +284,34 @@ def test_debug_checks_reject_duplicate_slots(cuda, monkeypatch):
         cache_ops.reshape_and_cache_int8(k, k, kc, vc, ksc, ksc.clone(), slots)
     torch.cuda.synchronize()
     assert (kc == SENTINEL).all() and (vc == SENTINEL).all()
+
+
+def test_write_misaligned_sources_are_copied(cuda):
+    """Contiguous key/value at an odd storage offset (rows not 16-byte aligned) are read through
+    aligned copies; the caches are bit-exact to the oracle."""
+    g = torch.Generator().manual_seed(17)
+    T, hkv, d, nb = 45, 4, 128, 8
+    k = torch.randn(T, hkv, d, generator=g).to(torch.bfloat16).to(cuda)
+    v = torch.randn(T, hkv, d, generator=g).to(torch.bfloat16).to(cuda)
+    bufk = torch.empty(k.numel() + 1, dtype=k.dtype, device=cuda)
+    bufv = torch.empty(v.numel() + 3, dtype=v.dtype, device=cuda)
+    k_odd, v_odd = bufk[1:].view(k.shape), bufv[3:].view(v.shape)
+    k_odd.copy_(k)
+    v_odd.copy_(v)
+    assert k_odd.data_ptr() % 16 and v_odd.data_ptr() % 16
+    ks = (k.float().abs().amax(dim=(0, 2)) / 127).clamp_min(1e-6)
+    vs = (v.float().abs().amax(dim=(0, 2)) / 127).clamp_min(1e-6)
+    slots = torch.randperm(nb * 16, generator=g)[:T]
+    _assert_equal(*_run(k_odd, v_odd, slots, ks, vs, nb, cuda))
+    from int8kv import cache_ops
+    kc = torch.zeros(nb, 16, hkv, d, dtype=torch.int8, device=cuda)
+    vc = torch.zeros_like(kc)
+    ksc = torch.zeros(nb, 16, hkv, device=cuda)
+    vsc = torch.zeros_like(ksc)
+    cache_ops.reshape_and_cache_int8(k_odd, v_odd, kc, vc, ksc, vsc, slots.to(cuda))
+    kc2, vc2 = torch.zeros_like(kc), torch.zeros_like(vc)
+    ksc2, vsc2 = torch.zeros_like(ksc), torch.zeros_like(vsc)
+    cache_ops.reshape_and_cache_int8(k, v, kc2, vc2, ksc2, vsc2, slots.to(cuda))
+    torch.cuda.synchronize()
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    assert torch.equal(ksc, ksc2) and torch.equal(vsc, vsc2)

@@ -342,3 +342,18 @@ def test_unsupported_block_sizes_raise(cuda):
         kx = torch.zeros(64, bs, 4, 128, dtype=torch.int8, device=cuda)
         with pytest.raises(RuntimeError, match="E_SHAPE"):
             int8kv.int8_paged_attention(q, kx, kx.clone(), bt, sl, ks, vs)
+
+
+def test_misaligned_query_is_copied(cuda):
+    """A contiguous query at an odd storage offset (rows not 16-byte aligned) is read through an
+    aligned copy; the result equals the aligned call bit for bit."""
+    c = decode_case([77, 300], seed=12)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    buf = torch.empty(q.numel() + 1, dtype=q.dtype, device=cuda)
+    q_odd = buf[1:].view(q.shape)
+    q_odd.copy_(q)
+    assert q_odd.data_ptr() % 16 != 0 and q_odd.is_contiguous()
+    a = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs)
+    b = int8kv.int8_paged_attention(q_odd, kc, vc, bt, sl, ks, vs)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
