@@ -14,10 +14,12 @@
 //     range), so a ragged batch costs every workgroup the same whatever the length
 //     distribution.  The unit counts and the range bounds are computed on the device from
 //     seq_lens; the host never reads them.
-//   * A workgroup owns one range for W kv heads, one wave per kv head.  The W waves read the
-//     same cache rows (their head slices of the same 16-token row groups) at the same time.  A wave
+//   * A workgroup owns a pair of ranges for W kv heads: waves 0..W-1 the first range, waves
+//     W..2W-1 the second, one wave per (range, kv head).  The W waves of a range read the same
+//     cache rows (their head slices of the same 16-token row groups) at the same time.  A wave
 //     handles all query heads of its GQA group on the matrix cores, so every K/V byte is read
-//     from HBM exactly once, and needs no barrier.
+//     from HBM exactly once, and needs no barrier.  The first range of a pair is the longer
+//     one: of two waves sharing a SIMD the first streams faster (see kFirstShare).
 //   * A sequence wholly inside one range is finished by that wave (output written directly).
 //     A sequence cut by range bounds leaves (max, sum, accumulator) partials in the workspace,
 //     at most two per range and head; merge_kernel combines them.
@@ -98,6 +100,9 @@ struct DecodeArgs {
   int32_t bt_is64;
   int32_t sl_is64;
   float sm_scale_log2e;
+  int32_t first_share;  // of a range pair's units, the first range's share in 1/256
+  int32_t pair_min;     // ranges are paired when P >= pair_min (every CU gets a whole pair)
+  int32_t halves;       // ranges per workgroup (1, or 2 with the paired layout)
 };
 
 // ------------------------------------------------------------------------ wave utilities
@@ -127,8 +132,12 @@ __device__ __forceinline__ int64_t readlane64(int64_t x, int lane) {
 // n_b = ceil(L_b / tile_tokens).  The batch becomes a stream of units: a non-empty sequence
 // contributes seq_cost "start" units (the latency of its first block ids and tiles, which a
 // range pays again for every sequence it starts) followed by its n_b tiles.  With U units in
-// all, P = clamp(ceil(U / min_tiles), 1, max_ranges) and range r covers units
-// [r * U / P, (r + 1) * U / P), so every workgroup gets the same cost whatever the lengths.
+// all, P = clamp(ceil(U / min_tiles), 1, max_ranges) and the uniform bounds are b_r = r U / P,
+// so every range costs the same whatever the lengths.  When P >= pair_min (enough ranges for a
+// pair on every CU), ranges come in pairs (2k, 2k + 1), the two halves of one workgroup, and
+// the bound between them moves from b_{2k+1} to first_share / 256 of the pair's units (an
+// unpaired last range keeps its bounds): the first half, which streams faster on a shared
+// SIMD, gets the larger share.
 __device__ __forceinline__ int64_t seq_len_of(const DecodeArgs& a, int64_t b) {
   if (b >= a.batch) return 0;
   int64_t L = load_index(a.sl, b, a.sl_is64);
@@ -137,16 +146,30 @@ __device__ __forceinline__ int64_t seq_len_of(const DecodeArgs& a, int64_t b) {
 }
 
 __device__ __forceinline__ int64_t tiles_of(const DecodeArgs& a, int64_t L) {
-  return (L + a.tile_tokens - 1) / a.tile_tokens;
+  static_assert(tile_blocks<kI8>() == 2 && tile_blocks<kBF16>() == 2, "32-token tiles");
+  return (L + 2 * kRows - 1) / (2 * kRows);
 }
 
 __device__ __forceinline__ int64_t units_of(const DecodeArgs& a, int64_t n) {
   return n > 0 ? n + a.seq_cost : 0;
 }
 
+// a / b for a >= 0, b > 0, with a 32-bit divide when both fit (the plan's bounds always do in
+// practice; the 64-bit divide is a long instruction sequence on the GPU).
+__device__ __forceinline__ int64_t udiv(int64_t a, int64_t b) {
+  if ((((uint64_t)a | (uint64_t)b) >> 32) == 0) return (int64_t)((uint32_t)a / (uint32_t)b);
+  return a / b;
+}
+
+// Ranges are paired only when they average at least this many units: short ranges are
+// latency-bound, and shifting a unit or two between them costs more than the balance gains.
+constexpr int kPairMinUnits = 16;
+
 struct Plan {
   int64_t U;
   int64_t P;
+  int32_t share;  // first_share
+  bool paired;
 };
 
 // L0: this lane's seq_len_of(a, lane), the first 64 sequences' lengths, which the caller keeps
@@ -155,16 +178,32 @@ __device__ __forceinline__ Plan make_plan(const DecodeArgs& a, int lane, int64_t
   int64_t U = wave_sum(units_of(a, tiles_of(a, L0)));
   for (int64_t base = kWave; base < a.batch; base += kWave)
     U += wave_sum(units_of(a, tiles_of(a, seq_len_of(a, base + lane))));
-  int64_t P = (U + a.min_tiles - 1) / a.min_tiles;
+  int64_t P = udiv(U + a.min_tiles - 1, a.min_tiles);
   P = P < 1 ? 1 : (P > a.max_ranges ? a.max_ranges : P);
-  return {U, P};
+  return {U, P, a.first_share, P >= a.pair_min && U >= (int64_t)kPairMinUnits * P};
 }
 
-__device__ __forceinline__ int64_t range_start(const Plan& p, int64_t r) { return r * p.U / p.P; }
+// Bound between the ranges of pair k (2k + 1 < P): first_share of the pair's units, at least
+// one unit on each side (P <= U keeps every uniform range non-empty).
+__device__ __forceinline__ int64_t pair_split(const Plan& p, int64_t k) {
+  const int64_t ps = udiv(2 * k * p.U, p.P);
+  const int64_t pe = udiv((2 * k + 2) * p.U, p.P);
+  int64_t h = ((pe - ps) * p.share) >> 8;
+  h = h < 1 ? 1 : (h > pe - ps - 1 ? pe - ps - 1 : h);
+  return ps + h;
+}
+
+__device__ __forceinline__ int64_t range_start(const Plan& p, int64_t r) {
+  if (p.paired && (r & 1) && r < p.P) return pair_split(p, r >> 1);
+  return udiv(r * p.U, p.P);
+}
 
 // The range holding stream unit x (0 <= x < U): the largest r with range_start(r) <= x.
 __device__ __forceinline__ int64_t range_of(const Plan& p, int64_t x) {
-  return ((x + 1) * p.P - 1) / p.U;
+  const int64_t r0 = udiv((x + 1) * p.P - 1, p.U);  // uniform range
+  const int64_t k = r0 >> 1;
+  if (!p.paired || 2 * k + 1 >= p.P) return r0;  // uniform, or the unpaired last range
+  return 2 * k + (x >= pair_split(p, k) ? 1 : 0);
 }
 
 // Partial-record slot of a sequence cut by a range: 0 if it started in an earlier range, 1 if
@@ -761,18 +800,26 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   }
 }
 
-// grid (max_ranges, num_kv_heads / W), block W waves; wave w of workgroup (r, y) handles
-// kv head y * W + w over stream range r.
-template <int CACHE, int QT, bool NT, bool QQ>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(DecodeArgs a) {
-  __shared__ int32_t s_ids[kMaxWavesPerWG][kChunkTiles * tile_blocks<CACHE>()];
+// grid (ceil(max_ranges / 2), num_kv_heads / W), block 2W waves; wave w of workgroup (x, y)
+// handles kv head y * W + w % W over stream range 2x + w / W (paired ranges) or
+// x + (w / W) grid.x.
+template <int CACHE, int QT, bool NT, bool QQ, int HALVES>
+__global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(DecodeArgs a) {
+  __shared__ int32_t s_ids[HALVES * kMaxWavesPerWG][kChunkTiles * tile_blocks<CACHE>()];
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int kvh = blockIdx.y * (blockDim.x / kWave) + wave;
-  const int64_t r = blockIdx.x;
+  const int W = blockDim.x / (HALVES * kWave);  // kv heads per workgroup
+  const int kvh = blockIdx.y * W + (HALVES == 1 ? wave : wave % W);
+  const int half = HALVES == 1 ? 0 : wave / W;
 
   const int64_t L0 = seq_len_of(a, lane);
   const Plan plan = make_plan(a, lane, L0);
+  // One range per workgroup, or two: ranges 2x and 2x + 1 when paired, else x and x + grid.x
+  // (the second only when the batch needs more ranges than there are workgroups).
+  int64_t r = blockIdx.x;
+  if constexpr (HALVES == 2)
+    r = plan.paired ? 2 * (int64_t)blockIdx.x + half
+                    : (int64_t)blockIdx.x + half * (int64_t)gridDim.x;
   if (r >= plan.P) return;
   const int64_t u0 = range_start(plan, r);
   const int64_t u1 = range_start(plan, r + 1);
@@ -942,8 +989,14 @@ constexpr int kMinTilesLarge = 4;
 constexpr int64_t kMaxMergeRanges = 128;  // ranges per sequence the merge takes in 4 rounds
 constexpr int kWavesPerCU = 8;  // resident decode waves per CU the automatic range count targets
 constexpr int64_t kInfinityCacheBytes = 256LL << 20;  // MI355X last-level (MALL) capacity
+// Share (1/256) of a range pair's units given to the first half of the workgroup.  Two waves
+// share each SIMD, and the first (waves 0..W-1) streams ~30 % faster than the second on
+// MI355X; with equal halves the second then runs alone for the last quarter of the call.
+// 160 (62.5 %) measured best between cfg3 (~152) and B=32 x 8320 (~168): -2 us at both.
+constexpr int32_t kFirstShare = 160;
 
-// Waves per workgroup: the largest of 4, 3, 2, 1 dividing num_kv_heads.
+// kv heads per workgroup (two waves each, one per range of the pair): the largest of 4, 3, 2, 1
+// dividing num_kv_heads.
 int waves_per_wg(int32_t num_kv_heads) {
   for (int w = kMaxWavesPerWG; w > 1; --w)
     if (num_kv_heads % w == 0) return w;
@@ -1001,23 +1054,34 @@ bool shape_ok(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32
          block_size_ok(block_size);
 }
 
+template <int CACHE, int QT, bool NT, bool QQ>
+void launch_main(const DecodeArgs& a, dim3 grid, int W, hipStream_t s) {
+  if constexpr (CACHE == kI8) {
+    if (a.halves == 2) {
+      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 2>), grid, dim3(2 * W * kWave), 0, s, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1>), grid, dim3(W * kWave), 0, s, a);
+}
+
 template <int CACHE, int QT>
 int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
   const int W = waves_per_wg(a.num_kv_heads);
   if (flags & INT8KV_DECODE_MAIN) {
-    dim3 grid((unsigned)a.max_ranges, (unsigned)(a.num_kv_heads / W));
+    dim3 grid((unsigned)((a.max_ranges + a.halves - 1) / a.halves), (unsigned)(a.num_kv_heads / W));
     // INT8 caches: non-temporal loads for large pools, int8 scores for a quantised query.
     if constexpr (CACHE == kI8) {
       if (nt && a.quantize_q)
-        hipLaunchKernelGGL((decode_kernel<CACHE, QT, true, true>), grid, dim3(W * kWave), 0, s, a);
+        launch_main<CACHE, QT, true, true>(a, grid, W, s);
       else if (nt)
-        hipLaunchKernelGGL((decode_kernel<CACHE, QT, true, false>), grid, dim3(W * kWave), 0, s, a);
+        launch_main<CACHE, QT, true, false>(a, grid, W, s);
       else if (a.quantize_q)
-        hipLaunchKernelGGL((decode_kernel<CACHE, QT, false, true>), grid, dim3(W * kWave), 0, s, a);
+        launch_main<CACHE, QT, false, true>(a, grid, W, s);
       else
-        hipLaunchKernelGGL((decode_kernel<CACHE, QT, false, false>), grid, dim3(W * kWave), 0, s, a);
+        launch_main<CACHE, QT, false, false>(a, grid, W, s);
     } else {
-      hipLaunchKernelGGL((decode_kernel<CACHE, QT, false, false>), grid, dim3(W * kWave), 0, s, a);
+      launch_main<CACHE, QT, false, false>(a, grid, W, s);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
@@ -1158,6 +1222,24 @@ extern "C" int int8kv_paged_decode(
   a.bt_is64 = table_dtype == INT8KV_I64;
   a.sl_is64 = seq_lens_dtype == INT8KV_I64;
   a.sm_scale_log2e = sm_scale * kLog2e;
+  a.first_share = kFirstShare;
+  // Pairs only pay when every CU gets one (INT8 caches; the 16-bit kernel measured 1 % slower
+  // with them).
+  {
+    // Paired layout (two ranges per workgroup, the first one longer) for INT8 calls that can
+    // reach a pair per CU: P >= pair_min needs at least pair_min * min_tiles units, bounded
+    // here by batch x (longest possible sequence).  Smaller calls and 16-bit caches (1 %
+    // slower paired) keep one range per workgroup.
+    const int64_t wgs_y = num_kv_heads / waves_per_wg(num_kv_heads);  // workgroups per range
+    const int64_t pair_min = (2LL * cu_count() + wgs_y - 1) / wgs_y;
+    const double units_max =
+        (double)batch * (std::ceil((double)table_width * block_size / a.tile_tokens) + a.seq_cost);
+    const bool paired = cache_dtype == INT8KV_I8 && num_ranges >= pair_min &&
+                        units_max >= (double)pair_min * min_tiles &&
+                        units_max >= (double)pair_min * kPairMinUnits;
+    a.halves = paired ? 2 : 1;
+    a.pair_min = paired ? (int32_t)pair_min : 0x7fffffff;
+  }
 
   // Non-temporal K/V loads when the call may stream more than the Infinity Cache holds: the
   // most it can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).

@@ -357,3 +357,16 @@ def test_misaligned_query_is_copied(cuda):
     b = int8kv.int8_paged_attention(q_odd, kc, vc, bt, sl, ks, vs)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("hq,hkv,lens", [
+    (28, 4, [8192, 8000, 7777, 8192, 1, 8191, 6000, 8192]),
+    (32, 8, [4096] * 12 + [1, 333, 4095, 4097]),
+])
+def test_paired_ranges_regime(cuda, hq, hkv, lens):
+    """Batches large enough to give every CU a pair of ranges (the uneven first/second split of
+    each workgroup) against the oracle, and against one range per sequence."""
+    c = decode_case(lens, seed=hkv + len(lens), hq=hq, hkv=hkv)
+    ref = oracle_int8(c)
+    _check(_int8(c, cuda), ref, f"paired hq={hq} hkv={hkv}")
+    _check(_int8(c, cuda, num_splits=1), ref, f"single pass hq={hq} hkv={hkv}")
