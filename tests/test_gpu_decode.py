@@ -370,3 +370,24 @@ def test_paired_ranges_regime(cuda, hq, hkv, lens):
     ref = oracle_int8(c)
     _check(_int8(c, cuda), ref, f"paired hq={hq} hkv={hkv}")
     _check(_int8(c, cuda, num_splits=1), ref, f"single pass hq={hq} hkv={hkv}")
+
+
+@pytest.mark.parametrize("splits", [None, 1, 3])
+def test_batches_beyond_one_wave_of_sequences(cuda, splits):
+    """B = 200 (four 64-sequence chunks in the kernels' batch walk) with ragged lengths, some
+    empty sequences spread over the chunks, int64 lengths and tables."""
+    g = torch.Generator().manual_seed(77)
+    lens = torch.randint(1, 600, (200,), generator=g).tolist()
+    c = decode_case(lens, seed=77, extra_blocks=11)
+    sl = c.seq_lens.clone().to(torch.int64)
+    for b in (0, 63, 64, 130, 199):
+        sl[b] = 0
+    q, kc, vc, bt, _, ks, vs = to_dev(c, cuda)
+    out = int8kv.int8_paged_attention(q, kc, vc, bt.to(torch.int64), sl.to(cuda), ks, vs,
+                                      num_splits=splits)
+    torch.cuda.synchronize()
+    ref = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                sl.numpy(), c.k_scale.numpy(), c.v_scale.numpy())
+    for b in (0, 63, 64, 130, 199):
+        assert (out[b] == 0).all(), b
+    _check(out, ref, f"B=200 splits={splits}")
