@@ -169,7 +169,7 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *                 (src/triton_ops/int8_paged_attention.py:137-146): q_scale = max(absmax/127,
  *                 1e-6), q8 = clamp(round_half_away_from_zero(q / q_scale), -127, 127).
  *
- * Supported sizes: head_dim = 128, block_size a power of two in [16, 65536] (16 and 32 are
+ * Supported sizes: head_dim 64 or 128, block_size a power of two in [16, 65536] (16 and 32 are
  * vLLM's usual values), group = num_q_heads / num_kv_heads in [1, 16].  Other sizes return
  * INT8KV_E_SHAPE.
  */

@@ -54,7 +54,7 @@
 
 namespace int8kv {
 
-constexpr int kHeadDim = 128;
+// head_dim: 64 or 128 (template parameter HD of the kernels).
 constexpr int kRows = 16;           // tokens per MFMA row group (half a tile)
 constexpr int kMaxGroup = 16;       // query heads per kv head (MFMA column count)
 constexpr int kChunkTiles = 256;    // tiles whose block ids a wave stages in LDS at a time
@@ -82,7 +82,7 @@ struct DecodeArgs {
   const float* v_scale;
   char* out;
   int64_t o_sb, o_sh;  // element strides
-  float* ws_acc;       // [max_ranges * 2][num_q_heads][kHeadDim]
+  float* ws_acc;       // [max_ranges * 2][num_q_heads][head_dim]
   float* ws_m;         // [max_ranges * 2][num_q_heads]
   float* ws_l;         // [max_ranges * 2][num_q_heads]
   int64_t num_blocks;
@@ -103,6 +103,7 @@ struct DecodeArgs {
   int32_t first_share;  // of a range pair's units, the first range's share in 1/256
   int32_t pair_min;     // ranges are paired when P >= pair_min (every CU gets a whole pair)
   int32_t halves;       // ranges per workgroup (1, or 2 with the paired layout)
+  int32_t head_dim;     // 64 or 128
 };
 
 // ------------------------------------------------------------------------ wave utilities
@@ -212,26 +213,27 @@ __device__ __forceinline__ int64_t range_of(const Plan& p, int64_t x) {
 __device__ __forceinline__ int64_t cut_slot(int64_t first_tile) { return first_tile > 0 ? 0 : 1; }
 
 // ------------------------------------------------------------------------ tile registers
-// Registers holding the K or the V half of one tile (NB 16-token row groups) for one lane.
+// Registers holding the K or the V half of one tile (NB 16-token row groups) for one lane, for
+// head_dim HD (64 or 128).
 //   K: lane (i = lane % 16, g = lane / 16) holds token i of row group s, head_dim elements
-//      [32g, 32g + 32).
+//      [HD/4 g, HD/4 (g + 1)): HD/4 elements, HD E / 64 16-byte pieces.
 //   V: lane (i, g) holds tokens 4g + r (r = 0..3) of row group s, head_dim elements
-//      [8i, 8i + 8).
-template <int CACHE>
-struct VRow {
-  typedef u32x4 T;  // 8 16-bit elements
-};
-template <>
-struct VRow<kI8> {
-  typedef u32x2 T;  // 8 int8 elements
-};
-template <int CACHE, int NB>
+//      [HD/16 i, HD/16 (i + 1)): HD E / 64 dwords per token row.
+template <int CACHE, int HD>
+constexpr int k_pieces() {
+  return HD * (CACHE == kI8 ? 1 : 2) / 64;
+}
+template <int CACHE, int HD>
+constexpr int v_dwords() {
+  return HD * (CACHE == kI8 ? 1 : 2) / 64;
+}
+template <int CACHE, int NB, int HD>
 struct KTile {
-  u32x4 k[NB][CACHE == kI8 ? 2 : 4];
+  u32x4 k[NB][k_pieces<CACHE, HD>()];
 };
-template <int CACHE, int NB>
+template <int CACHE, int NB, int HD>
 struct VTile {
-  typename VRow<CACHE>::T v[NB][4];
+  uint32_t v[NB][4][v_dwords<CACHE, HD>()];
 };
 
 template <int CACHE>
@@ -314,6 +316,23 @@ __device__ __forceinline__ void store8(char* p, const float (&x)[8]) {
   }
 }
 
+// Stores N (4 or 8) consecutive fp32 values as DT (aligned to N elements).
+template <int DT, int N>
+__device__ __forceinline__ void store_n(char* p, const float (&x)[N]) {
+  static_assert(N == 4 || N == 8, "4 or 8 elements");
+  if constexpr (N == 8) {
+    store8<DT>(p, x);
+  } else if constexpr (DT == kF32) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
+  } else if constexpr (DT == kF16) {
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<f16x4*>(p) = f16x4{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
+  } else {
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<bf16x4*>(p) = bf16x4{(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]};
+  }
+}
+
 // Cache-stream load.  NT (chosen per call by the host, INT8 caches only): the non-temporal hint,
 // +10 % delivered bandwidth on MI355X when the call streams more K/V than the Infinity Cache
 // holds; a small pool that the cache keeps between calls is read faster without it.  16-bit
@@ -334,8 +353,8 @@ struct TileRows {
   int32_t row[NB];
 };
 
-template <int CACHE, int NB, bool NT>
-__device__ __forceinline__ void issue_k(KTile<CACHE, NB>& r, const char* kb,
+template <int CACHE, int NB, bool NT, int HD>
+__device__ __forceinline__ void issue_k(KTile<CACHE, NB, HD>& r, const char* kb,
                                         const TileRows<NB>& ph, const DecodeArgs& a, int li,
                                         int lg) {
   constexpr int E = esize<CACHE>();
@@ -343,24 +362,36 @@ __device__ __forceinline__ void issue_k(KTile<CACHE, NB>& r, const char* kb,
   for (int s = 0; s < NB; ++s) {
     const u32x4* k4 =
         reinterpret_cast<const u32x4*>(kb + ph.id[s] * a.kc_sb + (ph.row[s] + li) * a.kc_ss +
-                                       lg * (32 * E));
+                                       lg * (HD / 4 * E));
 #pragma unroll
-    for (int i = 0; i < 2 * E; ++i) r.k[s][i] = stream_load<CACHE, NT>(&k4[i]);
+    for (int i = 0; i < k_pieces<CACHE, HD>(); ++i) r.k[s][i] = stream_load<CACHE, NT>(&k4[i]);
   }
 }
 
-template <int CACHE, int NB, bool NT>
-__device__ __forceinline__ void issue_v(VTile<CACHE, NB>& r, const char* vb,
+template <int CACHE, int NB, bool NT, int HD>
+__device__ __forceinline__ void issue_v(VTile<CACHE, NB, HD>& r, const char* vb,
                                         const TileRows<NB>& ph, const DecodeArgs& a, int li,
                                         int lg) {
   constexpr int E = esize<CACHE>();
-  typedef typename VRow<CACHE>::T Row;
+  constexpr int DW = v_dwords<CACHE, HD>();
 #pragma unroll
   for (int s = 0; s < NB; ++s) {
-    const char* vp = vb + ph.id[s] * a.vc_sb + (ph.row[s] + 4 * lg) * a.vc_ss + li * (8 * E);
+    const char* vp = vb + ph.id[s] * a.vc_sb + (ph.row[s] + 4 * lg) * a.vc_ss + li * (HD / 16 * E);
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr)
-      r.v[s][rr] = stream_load<CACHE, NT>(reinterpret_cast<const Row*>(vp + rr * a.vc_ss));
+    for (int rr = 0; rr < 4; ++rr) {
+      const char* rp = vp + rr * a.vc_ss;
+      if constexpr (DW == 1) {
+        r.v[s][rr][0] = stream_load<CACHE, NT>(reinterpret_cast<const uint32_t*>(rp));
+      } else if constexpr (DW == 2) {
+        const u32x2 x = stream_load<CACHE, NT>(reinterpret_cast<const u32x2*>(rp));
+        r.v[s][rr][0] = x[0];
+        r.v[s][rr][1] = x[1];
+      } else {
+        const u32x4 x = stream_load<CACHE, NT>(reinterpret_cast<const u32x4*>(rp));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r.v[s][rr][k] = x[k];
+      }
+    }
   }
 }
 
@@ -373,10 +404,10 @@ __device__ __forceinline__ void issue_v(VTile<CACHE, NB>& r, const char* vb,
 //   QQ (INT8 cache with a quantised query): the scores are the exact integer products of the
 //   int8 K rows and q8 on the int8 matrix cores (2 k-steps of 64, no K conversion); otherwise
 //   K is converted to 16-bit operands (4 k-steps of 32).
-template <int CACHE, int NB, bool QQ>
-__device__ __forceinline__ void tile_scores(const KTile<CACHE, NB>& r,
-                                            const typename MfmaOp<CACHE>::T (&qop)[4],
-                                            const i32x4 (&q8op)[2], f32x4 (&acc)[8],
+template <int CACHE, int NB, bool QQ, int HD>
+__device__ __forceinline__ void tile_scores(const KTile<CACHE, NB, HD>& r,
+                                            const typename MfmaOp<CACHE>::T (&qop)[HD / 32],
+                                            const i32x4 (&q8op)[HD / 64], f32x4 (&acc)[HD / 16],
                                             float& m_run, float& l_part, int valid, int lg,
                                             float s_scale,
                                             typename MfmaOp<CACHE>::T (&pop)[NB / 2][2]) {
@@ -389,14 +420,14 @@ __device__ __forceinline__ void tile_scores(const KTile<CACHE, NB>& r,
     if constexpr (QQ) {
       i32x4 si = (i32x4)(0);
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) si = mfma_i8(r.k[s][ks], q8op[ks], si);
+      for (int ks = 0; ks < HD / 64; ++ks) si = mfma_i8(r.k[s][ks], q8op[ks], si);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) S[s][rr] = (float)si[rr];
       continue;
     }
     S[s] = (f32x4)(0.0f);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < HD / 32; ++ks) {
       OpT kop;
       if constexpr (CACHE == kI8) {
         const uint32_t d0 = r.k[s][ks >> 1][(ks & 1) * 2] ^ kSignFlip;
@@ -434,7 +465,7 @@ __device__ __forceinline__ void tile_scores(const KTile<CACHE, NB>& r,
     m_run = m_new;
     l_part *= alpha;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+    for (int dt = 0; dt < HD / 16; ++dt) acc[dt] *= alpha;
   }
   typedef typename MfmaOp<CACHE>::E E;
 #pragma unroll
@@ -448,13 +479,14 @@ __device__ __forceinline__ void tile_scores(const KTile<CACHE, NB>& r,
 }
 
 // out^T[dim][head] += V^T[dim][token] * P^T[token][head] for one tile.
-// MFMA row i of dim tile dt is head_dim element 8i + dt; k-slot e of lane group g in k-step
-// kst is token (row group 2 kst + e / 4, row 4g + e % 4), matching the P^T operands.
-template <int CACHE, int NB>
-__device__ __forceinline__ void tile_pv(VTile<CACHE, NB>& r,
+// MFMA row i of dim tile dt is head_dim element (HD/16) i + dt; k-slot e of lane group g in
+// k-step kst is token (row group 2 kst + e / 4, row 4g + e % 4), matching the P^T operands.
+template <int CACHE, int NB, int HD>
+__device__ __forceinline__ void tile_pv(VTile<CACHE, NB, HD>& r,
                                         const typename MfmaOp<CACHE>::T (&pop)[NB / 2][2],
-                                        f32x4 (&acc)[8], int valid, int lg) {
+                                        f32x4 (&acc)[HD / 16], int valid, int lg) {
   typedef typename MfmaOp<CACHE>::T OpT;
+  constexpr int DW = v_dwords<CACHE, HD>();
   if constexpr (CACHE != kI8) {
     // 16-bit rows past the sequence end may hold non-finite garbage; 0 * NaN would leak.
     if (valid < NB * kRows) {
@@ -462,27 +494,30 @@ __device__ __forceinline__ void tile_pv(VTile<CACHE, NB>& r,
       for (int s = 0; s < NB; ++s)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
-          if (16 * s + 4 * lg + rr >= valid) r.v[s][rr] = (u32x4)(0u);
+          if (16 * s + 4 * lg + rr >= valid) {
+#pragma unroll
+            for (int k = 0; k < DW; ++k) r.v[s][rr][k] = 0u;
+          }
     }
   }
 #pragma unroll
   for (int kst = 0; kst < NB / 2; ++kst) {
     const int s0 = 2 * kst;
     if constexpr (CACHE == kI8) {
-      uint32_t pk[2][2][2][2];  // [block][token pair][lo/hi dword][byte pair 01/23]
+      uint32_t pk[2][2][DW][2];  // [row group][token pair][row dword][byte pair 01/23]
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int rp = 0; rp < 2; ++rp)
 #pragma unroll
-          for (int hsel = 0; hsel < 2; ++hsel) {
+          for (int hsel = 0; hsel < DW; ++hsel) {
             const uint32_t a0 = r.v[s0 + s][2 * rp][hsel] ^ kSignFlip;
             const uint32_t b0 = r.v[s0 + s][2 * rp + 1][hsel] ^ kSignFlip;
             pk[s][rp][hsel][0] = perm(a0, b0, 0x01050004u);  // [a.b0, b.b0, a.b1, b.b1]
             pk[s][rp][hsel][1] = perm(a0, b0, 0x03070206u);  // [a.b2, b.b2, a.b3, b.b3]
           }
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
+      for (int dt = 0; dt < HD / 16; ++dt) {
         const int hsel = dt >> 2, bp = (dt >> 1) & 1;
         const uint32_t sel = (dt & 1) ? kSelHi : kSelLo;
         u32x4 w;
@@ -496,7 +531,7 @@ __device__ __forceinline__ void tile_pv(VTile<CACHE, NB>& r,
       }
     } else {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
+      for (int dt = 0; dt < HD / 16; ++dt) {
         const int wd = dt >> 1;
         const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
         u32x4 w;
@@ -512,27 +547,27 @@ __device__ __forceinline__ void tile_pv(VTile<CACHE, NB>& r,
   }
 }
 
-// Raw query row piece of one lane: head li, elements [32 lg, 32 lg + 32) as loaded.
-template <int QT>
+// Raw query row piece of one lane: head li, elements [HD/4 lg, HD/4 (lg + 1)) as loaded.
+template <int QT, int HD>
 struct QueryRaw {
-  u32x4 w[4];  // 32 16-bit elements
+  u32x4 w[HD / 32];  // HD/4 16-bit elements
 };
-template <>
-struct QueryRaw<kF32> {
-  f32x4 w[8];  // 32 fp32 elements
+template <int HD>
+struct QueryRaw<kF32, HD> {
+  f32x4 w[HD / 16];  // HD/4 fp32 elements
 };
 
 // Issues the query loads (no wait): lane (head li, group lg) fetches q[b, kvh * G + li,
-// 32 lg .. 32 lg + 31]; lanes of padding heads (li >= G) hold zeros.
-template <int QT>
+// HD/4 lg .. HD/4 (lg + 1) - 1]; lanes of padding heads (li >= G) hold zeros.
+template <int QT, int HD>
 __device__ __forceinline__ void issue_query(const DecodeArgs& a, int64_t b, int kvh, int li,
-                                            int lg, QueryRaw<QT>& raw) {
+                                            int lg, QueryRaw<QT, HD>& raw) {
   constexpr int QE = esize<QT>();
   typedef typename std::remove_reference<decltype(raw.w[0])>::type Vec;
   constexpr int N = sizeof(raw.w) / sizeof(raw.w[0]);
   if (li < a.group) {
     const Vec* qp = reinterpret_cast<const Vec*>(
-        a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh + 32 * lg) * QE);
+        a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh + HD / 4 * lg) * QE);
 #pragma unroll
     for (int i = 0; i < N; ++i) raw.w[i] = qp[i];
   } else {
@@ -545,7 +580,7 @@ __device__ __forceinline__ float round_half_away(float x) {
   return x >= 0.0f ? floorf(x + 0.5f) : -floorf(-x + 0.5f);
 }
 
-// Builds the Q^T operand (lane (li, lg) holds q[li][32 lg + 8 ks + e]) from the raw loads and
+// Builds the Q^T operand (lane (li, lg) holds q[li][HD/4 lg + 8 ks + e]) from the raw loads and
 // returns the lane's fp32 factor turning MFMA scores into log2-domain logits.
 //   * default: q is scaled by 2^e so the largest |q| of the wave lands in [2^14, 2^15) for fp16
 //     operands (exact for bf16 input, never overflows); bf16 operands take q as is;
@@ -553,26 +588,27 @@ __device__ __forceinline__ float round_half_away(float x) {
 //     q8 = clamp(round_half_away(q / q_scale), -127, 127) (src/triton_ops/int8_paged_attention.py:
 //     137-146, :798-802); the operand is q8 and q_scale joins the score factor.  With QQ the
 //     q8 values are packed as int8 operands instead (q8op[ks] byte e of lane (li, lg) =
-//     q8[li][32 lg + 16 ks + e], matching the int8 K bytes the lane holds).
-template <int CACHE, int QT, bool QQ>
-__device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRaw<QT>& raw,
-                                              int kvh, typename MfmaOp<CACHE>::T (&qop)[4],
-                                              i32x4 (&q8op)[2]) {
-  float x[4][8];
+//     q8[li][HD/4 lg + 16 ks + e], matching the int8 K bytes the lane holds).
+template <int CACHE, int QT, bool QQ, int HD>
+__device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRaw<QT, HD>& raw,
+                                              int kvh, typename MfmaOp<CACHE>::T (&qop)[HD / 32],
+                                              i32x4 (&q8op)[HD / 64]) {
+  constexpr int KS = HD / 32;  // 16-bit k-steps
+  float x[KS][8];
   if constexpr (QT == kF32) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[ks][e] = raw.w[2 * ks + e / 4][e % 4];
   } else {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int e = 0; e < 4; ++e) unpack2<QT>(raw.w[ks][e], x[ks][2 * e], x[ks][2 * e + 1]);
   }
   float amax = 0.0f;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
+  for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[ks][e]));
   float s_scale = a.sm_scale_log2e;
@@ -584,7 +620,7 @@ __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRa
     const float qs = fmaxf(amax / 127.0f, 1e-6f);
     if constexpr (QQ) {
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < HD / 64; ++ks)
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           uint32_t word = 0;
@@ -599,7 +635,7 @@ __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRa
       return s_scale * qs;
     }
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         qop[ks][e] = (typename MfmaOp<CACHE>::E)fminf(fmaxf(round_half_away(x[ks][e] / qs), -127.0f),
@@ -621,7 +657,7 @@ __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRa
     }
   }
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
+  for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
     for (int e = 0; e < 8; ++e) qop[ks][e] = (typename MfmaOp<CACHE>::E)(x[ks][e] * qmul);
   return s_scale;
@@ -647,20 +683,23 @@ __device__ __forceinline__ void stage_block_ids(const DecodeArgs& a, int32_t* id
 }
 
 // Output rows of an empty sequence: zeros for the kv head's query heads (one wave).
-template <int QT>
+template <int QT, int HD>
 __device__ __forceinline__ void write_zero_rows(const DecodeArgs& a, int64_t b, int kvh, int lane) {
   const int li = lane & 15;
   const int lg = lane >> 4;
   if (li >= a.group) return;
   char* op = a.out + (b * a.o_sb + (int64_t)(kvh * a.group + li) * a.o_sh) * esize<QT>();
-  const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float z[HD / 16];
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) store8<QT>(op + (32 * lg + 8 * rr) * esize<QT>(), z);
+  for (int i = 0; i < HD / 16; ++i) z[i] = 0.0f;
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr)
+    store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), z);
 }
 
 // Processes tiles [ta, tb) of sequence b (length L) for kv head kvh with one wave, then writes
 // either the final output (full == true) or a partial record.  ids: this wave's LDS slots.
-template <int CACHE, int QT, bool NT, bool QQ>
+template <int CACHE, int QT, bool NT, bool QQ, int HD>
 __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, int64_t b,
                                             int64_t L, int kvh, int64_t ta, int64_t tb,
                                             bool full, int64_t rec, int lane) {
@@ -669,9 +708,9 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   const int lg = lane >> 4;
   const int G = a.group;
 
-  f32x4 acc[8];
+  f32x4 acc[HD / 16];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) acc[dt] = (f32x4)(0.0f);
+  for (int dt = 0; dt < HD / 16; ++dt) acc[dt] = (f32x4)(0.0f);
   float m_run = -INFINITY;
   float l_part = 0.0f;
 
@@ -706,31 +745,31 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   // tiles as one straight-line block and every load in it is unconditional (a request past the
   // chunk repeats its last tile, which the caches still hold), so the compiler's wait counts
   // are exact and no wait drains the pipeline.
-  KTile<CACHE, NB> ka, kb2;
-  VTile<CACHE, NB> va, vb2;
+  KTile<CACHE, NB, HD> ka, kb2;
+  VTile<CACHE, NB, HD> va, vb2;
   TileRows<NB> pha, phb;
   OpT pop[NB / 2][2];
   auto chunk_prologue = [&]() {
     stage_block_ids<NB>(a, ids, b, c0, c1, nblk, lane);
     blocks_of(c0, pha);
-    issue_k<CACHE, NB, NT>(ka, kb, pha, a, li, lg);
-    issue_v<CACHE, NB, NT>(va, vb, pha, a, li, lg);
+    issue_k<CACHE, NB, NT, HD>(ka, kb, pha, a, li, lg);
+    issue_v<CACHE, NB, NT, HD>(va, vb, pha, a, li, lg);
     blocks_of(c0 + 1 < c1 ? c0 + 1 : c1 - 1, phb);
-    issue_k<CACHE, NB, NT>(kb2, kb, phb, a, li, lg);
-    issue_v<CACHE, NB, NT>(vb2, vb, phb, a, li, lg);
+    issue_k<CACHE, NB, NT, HD>(kb2, kb, phb, a, li, lg);
+    issue_v<CACHE, NB, NT, HD>(vb2, vb, phb, a, li, lg);
   };
 
   // The query, the first chunk's block ids and its first two tiles are requested back to back;
   // the query operand is built once they are all in flight (otherwise three memory latencies
   // would line up at every segment start).
-  OpT qop[4];
-  i32x4 q8op[2];
+  OpT qop[HD / 32];
+  i32x4 q8op[HD / 64];
   float s_scale;
   {
-    QueryRaw<QT> qraw;
-    issue_query<QT>(a, b, kvh, li, lg, qraw);
+    QueryRaw<QT, HD> qraw;
+    issue_query<QT, HD>(a, b, kvh, li, lg, qraw);
     chunk_prologue();
-    s_scale = finish_query<CACHE, QT, QQ>(a, qraw, kvh, qop, q8op);
+    s_scale = finish_query<CACHE, QT, QQ, HD>(a, qraw, kvh, qop, q8op);
   }
 
   while (true) {
@@ -740,27 +779,27 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     // compute that follows them (which would shorten the prefetch distance).
     for (; t + 1 < c1; t += 2) {
       int valid = valid_of(t);
-      tile_scores<CACHE, NB, QQ>(ka, qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
+      tile_scores<CACHE, NB, QQ, HD>(ka, qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
       blocks_of(t + 2 < c1 ? t + 2 : last, pha);
-      issue_k<CACHE, NB, NT>(ka, kb, pha, a, li, lg);
+      issue_k<CACHE, NB, NT, HD>(ka, kb, pha, a, li, lg);
       __builtin_amdgcn_sched_barrier(0);
-      tile_pv<CACHE, NB>(va, pop, acc, valid, lg);
-      issue_v<CACHE, NB, NT>(va, vb, pha, a, li, lg);
+      tile_pv<CACHE, NB, HD>(va, pop, acc, valid, lg);
+      issue_v<CACHE, NB, NT, HD>(va, vb, pha, a, li, lg);
       __builtin_amdgcn_sched_barrier(0);
 
       valid = valid_of(t + 1);
-      tile_scores<CACHE, NB, QQ>(kb2, qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
+      tile_scores<CACHE, NB, QQ, HD>(kb2, qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
       blocks_of(t + 3 < c1 ? t + 3 : last, phb);
-      issue_k<CACHE, NB, NT>(kb2, kb, phb, a, li, lg);
+      issue_k<CACHE, NB, NT, HD>(kb2, kb, phb, a, li, lg);
       __builtin_amdgcn_sched_barrier(0);
-      tile_pv<CACHE, NB>(vb2, pop, acc, valid, lg);
-      issue_v<CACHE, NB, NT>(vb2, vb, phb, a, li, lg);
+      tile_pv<CACHE, NB, HD>(vb2, pop, acc, valid, lg);
+      issue_v<CACHE, NB, NT, HD>(vb2, vb, phb, a, li, lg);
       __builtin_amdgcn_sched_barrier(0);
     }
     if (t < c1) {  // odd tile count: the last tile is in the A buffers
       const int valid = valid_of(t);
-      tile_scores<CACHE, NB, QQ>(ka, qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
-      tile_pv<CACHE, NB>(va, pop, acc, valid, lg);
+      tile_scores<CACHE, NB, QQ, HD>(ka, qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
+      tile_pv<CACHE, NB, HD>(va, pop, acc, valid, lg);
     }
     if (c1 >= tb) break;
     c0 = c1;
@@ -778,20 +817,20 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     char* op = a.out + (b * a.o_sb + (int64_t)h * a.o_sh) * esize<QT>();
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      float o[8];
+      float o[HD / 16];
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o[dt] = acc[dt][rr] * inv;
-      store8<QT>(op + (32 * lg + 8 * rr) * esize<QT>(), o);
+      for (int dt = 0; dt < HD / 16; ++dt) o[dt] = acc[dt][rr] * inv;
+      store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), o);
     }
   } else {
     const int64_t row = rec * a.num_q_heads + h;
-    char* pp = reinterpret_cast<char*>(a.ws_acc + row * kHeadDim);
+    char* pp = reinterpret_cast<char*>(a.ws_acc + row * HD);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      float o[8];
+      float o[HD / 16];
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) o[dt] = acc[dt][rr];
-      store8<kF32>(pp + (32 * lg + 8 * rr) * 4, o);
+      for (int dt = 0; dt < HD / 16; ++dt) o[dt] = acc[dt][rr];
+      store_n<kF32, HD / 16>(pp + (HD / 4 * lg + HD / 16 * rr) * 4, o);
     }
     if (lg == 0) {
       a.ws_m[row] = m_run;
@@ -803,7 +842,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
 // grid (ceil(max_ranges / 2), num_kv_heads / W), block 2W waves; wave w of workgroup (x, y)
 // handles kv head y * W + w % W over stream range 2x + w / W (paired ranges) or
 // x + (w / W) grid.x.
-template <int CACHE, int QT, bool NT, bool QQ, int HALVES>
+template <int CACHE, int QT, bool NT, bool QQ, int HALVES, int HD>
 __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(DecodeArgs a) {
   __shared__ int32_t s_ids[HALVES * kMaxWavesPerWG][kChunkTiles * tile_blocks<CACHE>()];
   const int lane = threadIdx.x % kWave;
@@ -841,7 +880,7 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(2)
       while (zmask) {
         const int j = __builtin_ctzll(zmask);
         zmask &= zmask - 1;
-        write_zero_rows<QT>(a, base + j, kvh, lane);
+        write_zero_rows<QT, HD>(a, base + j, kvh, lane);
       }
       // Sequences whose tiles (units past the start cost) meet [u0, u1).
       uint64_t mask = __ballot(n > 0 && incl > u0 && excl + a.seq_cost < u1);
@@ -855,7 +894,7 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(2)
         const int64_t te = (u1 < first + nb ? u1 : first + nb) - first;
         if (ta >= te) continue;
         const bool full = ta == 0 && te == nb;
-        run_segment<CACHE, QT, NT, QQ>(a, s_ids[wave], base + j, Lb, kvh, ta, te, full,
+        run_segment<CACHE, QT, NT, QQ, HD>(a, s_ids[wave], base + j, Lb, kvh, ta, te, full,
                                2 * r + cut_slot(ta), lane);
       }
     }
@@ -898,25 +937,28 @@ __device__ __forceinline__ void merge_in(float& M, float& L, f32x4& O, float m, 
 }
 
 // Combines the partials of every sequence cut by range bounds.  grid (batch, num_q_heads), MW
-// waves per query head.  Lane (range parity, column) of wave w owns 4 head_dim elements of ranges
-// 2w + parity, 2w + parity + 2 MW, ... and folds them in with one online-softmax pass, four
-// ranges' loads in flight at a time (8 MW ranges per round for the workgroup); the 2 MW running
+// waves per query head.  A wave's lanes are RS = 256 / HD range slots of HD / 4 columns: lane
+// (slot rs, column c4) of wave w owns head_dim elements [4 c4, 4 c4 + 4) of ranges
+// RS w + rs, RS w + rs + RS MW, ... and folds them in with one online-softmax pass, four ranges'
+// loads in flight at a time (4 RS MW ranges per round for the workgroup); the RS MW running
 // states per column are then merged through LDS.  A sequence's merge costs about
-// 1 + nr / (8 MW) dependent memory latencies; the host picks MW from the average number of
+// 1 + nr / (4 RS MW) dependent memory latencies; the host picks MW from the average number of
 // ranges per sequence (one wave when a round covers them, up to four for a few long sequences).
-template <int CACHE, int QT, int MW>
+template <int CACHE, int QT, int MW, int HD>
 __global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
-  __shared__ float s_m[2 * MW][32];
-  __shared__ float s_l[2 * MW][32];
-  __shared__ f32x4 s_o[2 * MW][32];
+  constexpr int C4 = HD / 4;      // float4 columns of a head
+  constexpr int RS = kWave / C4;  // range slots per wave
+  __shared__ float s_m[RS * MW][C4];
+  __shared__ float s_l[RS * MW][C4];
+  __shared__ f32x4 s_o[RS * MW][C4];
   const int64_t b = blockIdx.x;
   const int h = blockIdx.y;
   const int kvh = h / a.group;
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int rs = lane >> 5;  // range parity handled by this lane
-  const int c4 = lane & 31;  // head_dim elements [4 c4, 4 c4 + 4)
-  const int slot = 2 * wave + rs;  // 0 .. 2 MW - 1
+  const int rs = lane / C4;  // range slot of this lane within the wave
+  const int c4 = lane % C4;  // head_dim elements [4 c4, 4 c4 + 4)
+  const int slot = RS * wave + rs;  // 0 .. RS MW - 1
 
   const int64_t L0 = seq_len_of(a, lane);
   const Plan plan = make_plan(a, lane, L0);
@@ -937,7 +979,7 @@ __global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
     return (2 * (r0 + c) + cut_slot(c)) * a.num_q_heads + h;  // tile 0 lies in range r0
   };
 
-  constexpr int kStride = 2 * MW;
+  constexpr int kStride = RS * MW;
   float M = -INFINITY, L = 0.0f;
   f32x4 O = (f32x4)(0.0f);
   for (int64_t cb = slot; cb < nr; cb += 4 * kStride) {
@@ -950,7 +992,7 @@ __global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
         const int64_t row = row_of(c);
         m[u] = a.ws_m[row];
         l[u] = a.ws_l[row];
-        v[u] = *reinterpret_cast<const f32x4*>(a.ws_acc + row * kHeadDim + 4 * c4);
+        v[u] = *reinterpret_cast<const f32x4*>(a.ws_acc + row * HD + 4 * c4);
       } else {
         m[u] = -INFINITY;
         l[u] = 0.0f;
@@ -964,7 +1006,7 @@ __global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
   s_l[slot][c4] = L;
   s_o[slot][c4] = O;
   __syncthreads();
-  if (threadIdx.x >= 32) return;
+  if (threadIdx.x >= C4) return;
   M = -INFINITY;
   L = 0.0f;
   O = (f32x4)(0.0f);
@@ -1033,8 +1075,8 @@ int32_t auto_ranges(int32_t num_kv_heads) {
   return (int32_t)(p < 1 ? 1 : (p > kMaxRangesLimit ? kMaxRangesLimit : p));
 }
 
-size_t workspace_bytes(int32_t num_q_heads, int32_t ranges) {
-  return (size_t)ranges * 2 * num_q_heads * (kHeadDim + 2) * sizeof(float);
+size_t workspace_bytes(int32_t num_q_heads, int32_t ranges, int32_t head_dim) {
+  return (size_t)ranges * 2 * num_q_heads * (head_dim + 2) * sizeof(float);
 }
 
 bool aligned16(const void* p, int64_t stride_bytes) {
@@ -1050,22 +1092,23 @@ bool block_size_ok(int32_t block_size) {
 
 bool shape_ok(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size) {
   return num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0 &&
-         num_q_heads / num_kv_heads <= kMaxGroup && head_dim == kHeadDim &&
+         num_q_heads / num_kv_heads <= kMaxGroup && (head_dim == 64 || head_dim == 128) &&
          block_size_ok(block_size);
 }
 
-template <int CACHE, int QT, bool NT, bool QQ>
+template <int CACHE, int QT, bool NT, bool QQ, int HD>
 void launch_main(const DecodeArgs& a, dim3 grid, int W, hipStream_t s) {
   if constexpr (CACHE == kI8) {
     if (a.halves == 2) {
-      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 2>), grid, dim3(2 * W * kWave), 0, s, a);
+      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 2, HD>), grid, dim3(2 * W * kWave), 0, s,
+                         a);
       return;
     }
   }
-  hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1>), grid, dim3(W * kWave), 0, s, a);
+  hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD>), grid, dim3(W * kWave), 0, s, a);
 }
 
-template <int CACHE, int QT>
+template <int CACHE, int QT, int HD>
 int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
   const int W = waves_per_wg(a.num_kv_heads);
   if (flags & INT8KV_DECODE_MAIN) {
@@ -1073,15 +1116,15 @@ int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
     // INT8 caches: non-temporal loads for large pools, int8 scores for a quantised query.
     if constexpr (CACHE == kI8) {
       if (nt && a.quantize_q)
-        launch_main<CACHE, QT, true, true>(a, grid, W, s);
+        launch_main<CACHE, QT, true, true, HD>(a, grid, W, s);
       else if (nt)
-        launch_main<CACHE, QT, true, false>(a, grid, W, s);
+        launch_main<CACHE, QT, true, false, HD>(a, grid, W, s);
       else if (a.quantize_q)
-        launch_main<CACHE, QT, false, true>(a, grid, W, s);
+        launch_main<CACHE, QT, false, true, HD>(a, grid, W, s);
       else
-        launch_main<CACHE, QT, false, false>(a, grid, W, s);
+        launch_main<CACHE, QT, false, false, HD>(a, grid, W, s);
     } else {
-      launch_main<CACHE, QT, false, false>(a, grid, W, s);
+      launch_main<CACHE, QT, false, false, HD>(a, grid, W, s);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
@@ -1092,11 +1135,11 @@ int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
     const int64_t per_seq = ((int64_t)a.max_ranges + a.batch - 1) / a.batch;
     const int64_t mw = (per_seq + 7) / 8;
     if (mw <= 1)
-      hipLaunchKernelGGL((merge_kernel<CACHE, QT, 1>), grid, dim3(kWave), 0, s, a);
+      hipLaunchKernelGGL((merge_kernel<CACHE, QT, 1, HD>), grid, dim3(kWave), 0, s, a);
     else if (mw == 2)
-      hipLaunchKernelGGL((merge_kernel<CACHE, QT, 2>), grid, dim3(2 * kWave), 0, s, a);
+      hipLaunchKernelGGL((merge_kernel<CACHE, QT, 2, HD>), grid, dim3(2 * kWave), 0, s, a);
     else
-      hipLaunchKernelGGL((merge_kernel<CACHE, QT, 4>), grid, dim3(4 * kWave), 0, s, a);
+      hipLaunchKernelGGL((merge_kernel<CACHE, QT, 4, HD>), grid, dim3(4 * kWave), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }
@@ -1107,11 +1150,14 @@ template <int CACHE>
 int launch_q(const DecodeArgs& a, int query_dtype, uint32_t flags, bool nt, hipStream_t s) {
   switch (query_dtype) {
     case INT8KV_F32:
-      return launch<CACHE, kF32>(a, flags, nt, s);
+      return a.head_dim == 64 ? launch<CACHE, kF32, 64>(a, flags, nt, s)
+                              : launch<CACHE, kF32, 128>(a, flags, nt, s);
     case INT8KV_F16:
-      return launch<CACHE, kF16>(a, flags, nt, s);
+      return a.head_dim == 64 ? launch<CACHE, kF16, 64>(a, flags, nt, s)
+                              : launch<CACHE, kF16, 128>(a, flags, nt, s);
     default:
-      return launch<CACHE, kBF16>(a, flags, nt, s);
+      return a.head_dim == 64 ? launch<CACHE, kBF16, 64>(a, flags, nt, s)
+                              : launch<CACHE, kBF16, 128>(a, flags, nt, s);
   }
 }
 
@@ -1129,7 +1175,7 @@ extern "C" size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num
       num_ranges > kMaxRangesLimit)
     return 0;
   if (num_ranges == 0) num_ranges = auto_ranges(num_kv_heads);
-  return workspace_bytes(num_q_heads, num_ranges);
+  return workspace_bytes(num_q_heads, num_ranges, head_dim);
 }
 
 extern "C" int int8kv_paged_decode(
@@ -1177,7 +1223,7 @@ extern "C" int int8kv_paged_decode(
 
   if (num_ranges == 0) num_ranges = auto_ranges(num_kv_heads);
   if (min_tiles == 0) min_tiles = auto_min_tiles(batch, table_width, block_size, num_ranges);
-  const size_t need = workspace_bytes(num_q_heads, num_ranges);
+  const size_t need = workspace_bytes(num_q_heads, num_ranges, head_dim);
   if (workspace == nullptr || workspace_bytes_given < need || ((uintptr_t)workspace % 16) != 0)
     return INT8KV_E_WORKSPACE;
 
@@ -1205,8 +1251,9 @@ extern "C" int int8kv_paged_decode(
   const int64_t recs = (int64_t)num_ranges * 2 * num_q_heads;
   float* ws = static_cast<float*>(workspace);
   a.ws_acc = ws;
-  a.ws_m = ws + recs * kHeadDim;
-  a.ws_l = ws + recs * (kHeadDim + 1);
+  a.ws_m = ws + recs * head_dim;
+  a.ws_l = ws + recs * (head_dim + 1);
+  a.head_dim = head_dim;
   a.num_blocks = num_blocks;
   a.batch = batch;
   a.num_kv_heads = num_kv_heads;

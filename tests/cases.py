@@ -28,7 +28,7 @@ class DecodeCase:
 
 
 def decode_case(lens, seed=0, hq=28, hkv=4, extra_blocks=17, width=None, randn_kv=False,
-                fill=None, block_size=16) -> DecodeCase:
+                fill=None, block_size=16, head_dim=128) -> DecodeCase:
     """Sequences of the given lengths written into a shuffled block pool.
 
     randn_kv=True uses the reference tests' inputs (K, V ~ N(0, 1), scales = absmax/127 of the
@@ -39,15 +39,15 @@ def decode_case(lens, seed=0, hq=28, hkv=4, extra_blocks=17, width=None, randn_k
     lens = [int(n) for n in lens]
     total = sum(lens)
     if randn_kv:
-        k = torch.randn(total, hkv, 128, generator=g).to(torch.bfloat16)
-        v = torch.randn(total, hkv, 128, generator=g).to(torch.bfloat16)
+        k = torch.randn(total, hkv, head_dim, generator=g).to(torch.bfloat16)
+        v = torch.randn(total, hkv, head_dim, generator=g).to(torch.bfloat16)
         ks = (k.float().abs().amax(dim=(0, 2)) / 127.0).clamp_min(1e-6)
         vs = (v.float().abs().amax(dim=(0, 2)) / 127.0).clamp_min(1e-6)
     else:
-        dist = syn.make_distribution(seed, hkv=hkv)
+        dist = syn.make_distribution(seed, hkv=hkv, d=head_dim)
         ks, vs = syn.calibrate_scales(dist, seed=seed + 1)
         k, v = syn.sample_kv(total, dist, g)
-    q = torch.randn(len(lens), hq, 128, generator=g).to(torch.bfloat16)
+    q = torch.randn(len(lens), hq, head_dim, generator=g).to(torch.bfloat16)
     bs = block_size
     nblk = sum((n + bs - 1) // bs for n in lens)
     nb = nblk + extra_blocks
@@ -55,7 +55,7 @@ def decode_case(lens, seed=0, hq=28, hkv=4, extra_blocks=17, width=None, randn_k
         fill = nb - 1
     bt = syn.random_block_tables(lens, nb, g, width=width, block_size=bs, fill=fill)
     slots = syn.slot_mapping_for(bt, lens, block_size=bs)
-    kc = np.zeros((nb, bs, hkv, 128), np.int8)
+    kc = np.zeros((nb, bs, hkv, head_dim), np.int8)
     vc = np.zeros_like(kc)
     # Unwritten slots hold random bytes: the kernels must never read them into a result.
     rng = np.random.default_rng(seed + 7)
@@ -79,11 +79,12 @@ def bf16_caches(c: DecodeCase, dtype=torch.bfloat16):
     hkv = c.key.shape[1]
     g = torch.Generator().manual_seed(123)
     bs = c.block_size
-    kc = torch.randn(nb * bs, hkv, 128, generator=g).to(dtype)
-    vc = torch.randn(nb * bs, hkv, 128, generator=g).to(dtype)
+    d = c.key.shape[2]
+    kc = torch.randn(nb * bs, hkv, d, generator=g).to(dtype)
+    vc = torch.randn(nb * bs, hkv, d, generator=g).to(dtype)
     kc[c.slots] = c.key.to(dtype)
     vc[c.slots] = c.value.to(dtype)
-    return kc.view(nb, bs, hkv, 128), vc.view(nb, bs, hkv, 128)
+    return kc.view(nb, bs, hkv, d), vc.view(nb, bs, hkv, d)
 
 
 def to_dev(c: DecodeCase, dev):

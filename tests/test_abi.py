@@ -56,7 +56,9 @@ def test_workspace_bytes(lib):
     assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 512) == 512 * 2 * 28 * 130 * 4
     assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 1) == 2 * 28 * 130 * 4
     # unsupported sizes -> 0
-    assert lib.int8kv_decode_workspace_bytes(28, 4, 64, 16, 0) == 0  # head_dim
+    for d in (32, 96, 256):  # head_dim: 64 or 128
+        assert lib.int8kv_decode_workspace_bytes(28, 4, d, 16, 0) == 0
+    assert lib.int8kv_decode_workspace_bytes(28, 4, 64, 16, 3) == 3 * 2 * 28 * 66 * 4
     for bs in (8, 24, 48, 1 << 17):  # block size: a power of two in [16, 65536]
         assert lib.int8kv_decode_workspace_bytes(28, 4, 128, bs, 0) == 0
     for bs in (16, 32, 64, 1 << 16):  # the partials do not depend on the block size
@@ -90,7 +92,7 @@ def test_decode_rejects_bad_arguments_without_launching(lib):
     assert _decode_call(lib, query_dtype=3) == -2
     assert _decode_call(lib, cache_dtype=4) == -2
     assert _decode_call(lib, table_dtype=2) == -2
-    assert _decode_call(lib, head_dim=64) == -3
+    assert _decode_call(lib, head_dim=96) == -3
     assert _decode_call(lib, block_size=8) == -3
     assert _decode_call(lib, block_size=48) == -3
     assert _decode_call(lib, num_q_heads=30) == -3

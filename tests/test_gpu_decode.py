@@ -391,3 +391,53 @@ def test_batches_beyond_one_wave_of_sequences(cuda, splits):
     for b in (0, 63, 64, 130, 199):
         assert (out[b] == 0).all(), b
     _check(out, ref, f"B=200 splits={splits}")
+
+
+HD64_SHAPES = [(32, 8), (14, 2), (8, 8)]  # Llama-3.2-1B, Qwen2.5-0.5B, multi-head
+
+
+@pytest.mark.parametrize("hq,hkv", HD64_SHAPES)
+def test_head_dim_64(cuda, hq, hkv):
+    """head_dim 64 (GQA models with 64-wide heads): INT8 and BF16 parity at tile, block and split
+    boundaries, quantize_q, and an fp32 query."""
+    lens = [1, 15, 16, 17, 31, 32, 33, 300, 1025, 2048]
+    c = decode_case(lens, seed=hq + hkv, hq=hq, hkv=hkv, head_dim=64, extra_blocks=7)
+    ref = oracle_int8(c)
+    for splits in (None, 1, 3):
+        _check(_int8(c, cuda, num_splits=splits), ref, f"d64 {hq}/{hkv} splits={splits}")
+    ref_q = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                  c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
+                                  quantize_q=True)
+    _check(_int8(c, cuda, quantize_q=True), ref_q, f"d64 {hq}/{hkv} quantize_q")
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    out32 = int8kv.int8_paged_attention(q.float(), kc, vc, bt, sl, ks, vs)
+    torch.cuda.synchronize()
+    err, _, _ = metrics(out32.cpu().numpy(), ref)
+    assert err <= 1e-3, err
+    k16, v16 = bf16_caches(c)
+    ref16 = O.paged_attention_ref(c.query.float().numpy(), k16.float().numpy(), v16.float().numpy(),
+                                  c.block_tables.numpy(), c.seq_lens.numpy())
+    out16 = int8kv.bf16_paged_attention(q, k16.to(cuda), v16.to(cuda), bt, sl)
+    torch.cuda.synchronize()
+    _check(out16, ref16, f"d64 {hq}/{hkv} bf16")
+
+
+def test_head_dim_64_paired_regime(cuda):
+    """head_dim 64 in batches large enough for the two-range workgroups: 16 x 8192 tokens pair
+    the ranges (32 q / 8 kv heads); 15 x 8192 + 77 tokens take the same grid with unpaired
+    ranges (the device-side check on the actual units)."""
+    for lens in ([8192] * 16, [8192] * 15 + [77]):
+        c = decode_case(lens, seed=64 + len(lens), hq=32, hkv=8, head_dim=64, extra_blocks=3)
+        ref = oracle_int8(c)
+        _check(_int8(c, cuda), ref, f"d64 large {lens[-1]}")
+        _check(_int8(c, cuda, num_splits=1), ref, f"d64 single pass {lens[-1]}")
+
+
+def test_unsupported_head_dims_raise(cuda):
+    c = decode_case([40], seed=3)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    for d in (32, 96, 256):
+        kx = torch.zeros(kc.shape[0], 16, 4, d, dtype=torch.int8, device=cuda)
+        qx = torch.zeros(q.shape[0], q.shape[1], d, dtype=q.dtype, device=cuda)
+        with pytest.raises(RuntimeError, match="E_SHAPE"):
+            int8kv.int8_paged_attention(qx, kx, kx.clone(), bt, sl, ks, vs)
