@@ -34,7 +34,7 @@ def metrics(out: np.ndarray, ref: np.ndarray):
     return float(diff), cos, rel
 
 
-# Parity bar for attention outputs against the fp32 oracle.
+# Parity bar for attention outputs against the fp32 oracle (the project's acceptance bar).
 MAX_ABS = 2e-2
 MIN_COS = 0.9999
 

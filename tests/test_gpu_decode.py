@@ -1,6 +1,6 @@
 """GPU parity of INT8 / BF16 PagedAttention decode against the fp32 oracle.
 
-Bar (BASELINE north star): max |out - oracle| <= 2e-2 and cosine >= 0.9999, where the oracle is
+Bar: max |out - oracle| <= 2e-2 and cosine >= 0.9999, where the oracle is
 the reference's INT8 path run in fp32 (src/triton_ops/int8_paged_attention.py:776-814) on the
 same int8 cache bytes.  Cases mirror the reference's tests (tests/test_int8_paged_attention.py:
 108-323, tests/test_runtime_write_and_attention.py) plus the benchmark configurations, ragged
