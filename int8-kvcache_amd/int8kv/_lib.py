@@ -81,6 +81,13 @@ def load() -> ctypes.CDLL:
     lib.int8kv_rotary_inplace.argtypes = [_vp, i64, i64, i32, i32, _vp, _vp, _vp, i64, _vp]
     lib.int8kv_silu_mul.restype = ctypes.c_int
     lib.int8kv_silu_mul.argtypes = [_vp, _vp, i64, i32, i64, i64, _vp]
+    lib.int8kv_rotary_cache_write.restype = ctypes.c_int
+    lib.int8kv_rotary_cache_write.argtypes = [
+        _vp, i64, i64, i32, i32, i32, _vp, _vp, _vp, i64, _vp, i64, i64, i64, i32, ctypes.c_int,
+        _vp, _vp, _c_i64p, _c_i64p, _vp, _vp, _vp,
+    ]
+    lib.int8kv_argmax_rows.restype = ctypes.c_int
+    lib.int8kv_argmax_rows.argtypes = [_vp, i64, i64, i64, _vp, _vp]
     lib.int8kv_version.restype = ctypes.c_char_p
     lib.int8kv_version.argtypes = []
     _lib = lib

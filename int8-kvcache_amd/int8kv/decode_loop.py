@@ -58,6 +58,9 @@ class QwenShape:
 
 QWEN25_7B = QwenShape()
 BLOCK_SIZE = 16
+# Decode step with the fused kernels (rotary + cache write in one launch, the HIP argmax); False
+# runs the unfused sequence (rotary, slot arithmetic, cache write, torch argmax) for comparison.
+FUSED_STEP = True
 MODES = ("int8", "bf16")
 
 # hipBLASLt solutions chosen by torch's TunableOp for the decode step's GEMMs (M = batch rows)
@@ -175,6 +178,45 @@ def hip_rotary_(qkv: torch.Tensor, num_heads: int, head_dim: int, positions: tor
         cos.data_ptr(), sin.data_ptr(), cos.shape[0], _lib.stream_handle(qkv.device))
     _lib.check(status, "int8kv_rotary_inplace")
     return qkv
+
+
+def hip_rotary_cache_write_(qkv: torch.Tensor, shape: QwenShape, positions: torch.Tensor,
+                            cos: torch.Tensor, sin: torch.Tensor, block_tables: torch.Tensor,
+                            key_cache: torch.Tensor, value_cache: torch.Tensor,
+                            k_scale: torch.Tensor | None, v_scale: torch.Tensor | None) -> torch.Tensor:
+    """Rotates the q and k heads of every qkv row in place and writes the row's k and v to the
+    paged caches at its position's slot (one decode token per row; the fused form of
+    ``hip_rotary_`` followed by the cache write, with the same results)."""
+    _bf16_rows(qkv, "qkv")
+    assert positions.dtype == torch.int64 and positions.is_contiguous()
+    assert positions.numel() == qkv.shape[0] == block_tables.shape[0]
+    assert block_tables.dtype == torch.int32 and block_tables.stride(1) == 1
+    assert cos.dtype == sin.dtype == torch.float32 and cos.is_contiguous() and sin.is_contiguous()
+    assert cos.shape == sin.shape and cos.shape[1] == shape.head_dim
+    int8 = key_cache.dtype == torch.int8
+    assert key_cache.dtype == value_cache.dtype and (int8 or key_cache.dtype == torch.bfloat16)
+    num_blocks, block_size = key_cache.shape[0], key_cache.shape[1]
+    status = _lib.load().int8kv_rotary_cache_write(
+        qkv.data_ptr(), qkv.shape[0], qkv.stride(0), shape.q_heads, shape.kv_heads, shape.head_dim,
+        positions.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0], block_tables.data_ptr(),
+        block_tables.shape[1], block_tables.stride(0), num_blocks, block_size,
+        _lib.I8 if int8 else _lib.BF16, key_cache.data_ptr(), value_cache.data_ptr(),
+        _lib.strides(key_cache), _lib.strides(value_cache),
+        k_scale.data_ptr() if int8 else None, v_scale.data_ptr() if int8 else None,
+        _lib.stream_handle(qkv.device))
+    _lib.check(status, "int8kv_rotary_cache_write")
+    return qkv
+
+
+def hip_argmax_rows(logits: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out[r] = argmax(logits[r]) (int64, first maximum; bf16 logits [rows, vocab])."""
+    assert logits.dtype == torch.bfloat16 and logits.stride(1) == 1
+    assert out.dtype == torch.int64 and out.is_contiguous() and out.numel() == logits.shape[0]
+    status = _lib.load().int8kv_argmax_rows(logits.data_ptr(), logits.shape[0], logits.shape[1],
+                                            logits.stride(0), out.data_ptr(),
+                                            _lib.stream_handle(logits.device))
+    _lib.check(status, "int8kv_argmax_rows")
+    return out
 
 
 def hip_silu_mul(gate_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
@@ -301,6 +343,15 @@ class PagedKVCache:
             Hkv, D = self.shape.kv_heads, self.shape.head_dim
             self.key[layer].view(-1, Hkv, D).index_copy_(0, slots, k.to(torch.bfloat16))
             self.value[layer].view(-1, Hkv, D).index_copy_(0, slots, v.to(torch.bfloat16))
+
+    def rotary_write(self, layer: int, qkv: torch.Tensor, positions: torch.Tensor, cos, sin,
+                     block_tables: torch.Tensor) -> None:
+        """Rotary on the q/k heads of the decode rows of qkv (in place) fused with the cache write
+        of their k (rotated) and v at each row's position."""
+        ks = self.k_scale[layer] if self.mode == "int8" else None
+        vs = self.v_scale[layer] if self.mode == "int8" else None
+        hip_rotary_cache_write_(qkv, self.shape, positions, cos, sin, block_tables, self.key[layer],
+                                self.value[layer], ks, vs)
 
     def attend(self, layer: int, q: torch.Tensor, block_tables: torch.Tensor, seq_lens: torch.Tensor,
                out: torch.Tensor, workspace: torch.Tensor) -> torch.Tensor:
@@ -441,28 +492,35 @@ class DecodeLoop:
     def _step(self) -> None:
         """One greedy step for every sequence: reads/writes only the device state buffers."""
         shape, B = self.shape, self.batch
-        Hq, Hkv, D, L = shape.q_heads, shape.kv_heads, shape.head_dim, shape.layers
+        Hq, D, L = shape.q_heads, shape.head_dim, shape.layers
         pos = self.positions
-        slots = self.block_tables.gather(1, (pos // BLOCK_SIZE).view(B, 1)).view(B).to(torch.int64)
-        slots = slots * BLOCK_SIZE + pos % BLOCK_SIZE
+        if not FUSED_STEP:
+            slots = self.block_tables.gather(1, (pos // BLOCK_SIZE).view(B, 1)).view(B).to(torch.int64)
+            slots = slots * BLOCK_SIZE + pos % BLOCK_SIZE
         x, h = self.resid, self.normed
         torch.index_select(self.w.embed, 0, self.tokens, out=x)
         hip_add_rms_norm(x, None, self.w.layers[0].ln1, h, shape.rms_eps)
         for l, lw in enumerate(self.w.layers):
             qkv = F.linear(h, lw.wqkv, lw.bqkv)
-            hip_rotary_(qkv, Hq + Hkv, D, pos, self.cos, self.sin)
-            q, k, v = _split_qkv(qkv, shape)
-            self.cache.write(l, k, v, slots)
+            if FUSED_STEP:
+                self.cache.rotary_write(l, qkv, pos, self.cos, self.sin, self.block_tables)
+                q, _, _ = _split_qkv(qkv, shape)
+            else:
+                hip_rotary_(qkv, Hq + shape.kv_heads, D, pos, self.cos, self.sin)
+                q, k, v = _split_qkv(qkv, shape)
+                self.cache.write(l, k, v, slots)
             self.cache.attend(l, q, self.block_tables, self.seq_lens, self.attn_out, self.workspace)
             hip_add_rms_norm(x, F.linear(self.attn_out.view(B, Hq * D), lw.wo), lw.ln2, h, shape.rms_eps)
             hip_silu_mul(F.linear(h, lw.w_gate_up), self.act)
             nxt = self.w.layers[l + 1].ln1 if l + 1 < L else self.w.ln_f
             hip_add_rms_norm(x, F.linear(self.act, lw.w_down), nxt, h, shape.rms_eps)
         torch.mm(h, self.w.lm_head.t(), out=self.logits)
-        nxt_tok = self.logits.argmax(-1)
-        self.tokens.copy_(nxt_tok)
+        if FUSED_STEP:
+            hip_argmax_rows(self.logits, self.tokens)
+        else:
+            self.tokens.copy_(self.logits.argmax(-1))
         col = self.step_idx.clamp(max=self.new_tokens - 1).view(1, 1).expand(B, 1)
-        self.generated.scatter_(1, col, nxt_tok.view(B, 1))
+        self.generated.scatter_(1, col, self.tokens.view(B, 1))
         self.positions.add_(1)
         self.seq_lens.add_(1)
         self.step_idx.add_(1)

@@ -34,11 +34,13 @@ def test_header_declares_expected_entry_points():
     assert [h.name for h in HEADERS] == ["int8kv.h", "int8kv_decode_loop.h"]
     assert _declared_functions() == [
         "int8kv_add_rms_norm",
+        "int8kv_argmax_rows",
         "int8kv_cache_write",
         "int8kv_decode_auto_ranges",
         "int8kv_decode_workspace_bytes",
         "int8kv_dynamic_cache_write",
         "int8kv_paged_decode",
+        "int8kv_rotary_cache_write",
         "int8kv_rotary_inplace",
         "int8kv_silu_mul",
         "int8kv_version",
@@ -184,3 +186,27 @@ def test_loop_ops_reject_bad_arguments_without_launching(lib):
     assert lib.int8kv_silu_mul(P, P, 4, 60, 120, 60, None) == E_SHAPE
     assert lib.int8kv_silu_mul(P, P, 4, 64, 64, 64, None) == E_STRIDE
     assert lib.int8kv_silu_mul(P, P, 0, 64, 128, 64, None) == 0
+    # rotary_cache_write(qkv, rows, rs, hq, hkv, d, pos, cos, sin, maxp, bt, width, bts, nb, bs,
+    #                    dtype, kc, vc, kcs, vcs, ks, vs, stream)
+    st4 = (ctypes.c_int64 * 4)(16 * 4 * 128, 4 * 128, 128, 1)
+    bad4 = (ctypes.c_int64 * 4)(16 * 4 * 128, 4 * 128, 128, 2)
+    rw = dict(q=P, rows=4, rs=4608, hq=28, hkv=4, d=128, pos=P, c=P, s=P, maxp=10, bt=P, width=8,
+              bts=8, nb=64, bs=16, dt=3, kc=P, vc=P, kcs=st4, vcs=st4, ks=P, vs=P, st=None)
+
+    def rope_write(**kw):
+        a = dict(rw, **kw)
+        return lib.int8kv_rotary_cache_write(*a.values())
+
+    assert rope_write(bt=None) == E_NULL and rope_write(ks=None) == E_NULL
+    assert rope_write(dt=0) == -2  # fp32 caches are not a decode-loop format
+    assert rope_write(ks=None, vs=None, dt=2, rows=0) == 0  # bf16 caches need no scales
+    assert rope_write(d=120) == E_SHAPE and rope_write(nb=0) == E_SHAPE and rope_write(bs=0) == E_SHAPE
+    assert rope_write(rs=4000) == E_STRIDE and rope_write(kcs=bad4) == E_STRIDE
+    assert rope_write(kc=P + 4) == E_STRIDE
+    assert rope_write(rows=0) == 0
+    # argmax_rows(logits, rows, vocab, row_stride, out, stream)
+    assert lib.int8kv_argmax_rows(None, 4, 100, 100, P, None) == E_NULL
+    assert lib.int8kv_argmax_rows(P, 4, 0, 100, P, None) == E_SHAPE
+    assert lib.int8kv_argmax_rows(P, 4, 1 << 31, 1 << 31, P, None) == E_SHAPE
+    assert lib.int8kv_argmax_rows(P, 4, 100, 99, P, None) == E_STRIDE
+    assert lib.int8kv_argmax_rows(P, 0, 100, 100, P, None) == 0

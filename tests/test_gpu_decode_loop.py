@@ -44,21 +44,31 @@ class _Recorder:
     def __init__(self, loop):
         self.loop, self.writes, self.attends = loop, [], []
         cache = loop.cache
-        self._write, self._attend = cache.write, cache.attend
+        self._write, self._attend, self._rw = cache.write, cache.attend, cache.rotary_write
 
         def write(layer, k, v, slots):
             self.writes.append((layer, k.detach().clone(), v.detach().clone(), slots.detach().clone()))
             self._write(layer, k, v, slots)
+
+        def rotary_write(layer, qkv, positions, cos, sin, bt):
+            # The decode step's fused rotary + write: record the rotated k (left in qkv) and v
+            # with the slots of the rows' positions, as an unfused write would have received.
+            self._rw(layer, qkv, positions, cos, sin, bt)
+            _, k, v = DL._split_qkv(qkv, SHAPE)
+            pos = positions.long()
+            slots = bt.long().gather(1, (pos // 16).view(-1, 1)).view(-1) * 16 + pos % 16
+            self.writes.append((layer, k.detach().clone(), v.detach().clone(), slots.detach().clone()))
 
         def attend(layer, q, bt, sl, out, ws):
             r = self._attend(layer, q, bt, sl, out, ws)
             self.attends.append((layer, q.detach().clone(), sl.detach().clone(), r.detach().clone()))
             return r
 
-        cache.write, cache.attend = write, attend
+        cache.write, cache.attend, cache.rotary_write = write, attend, rotary_write
 
     def detach(self):
-        self.loop.cache.write, self.loop.cache.attend = self._write, self._attend
+        c = self.loop.cache
+        c.write, c.attend, c.rotary_write = self._write, self._attend, self._rw
 
 
 def _make(model, mode):

@@ -127,3 +127,75 @@ def test_strided_rows(cuda):
     assert torch.equal(big[:, 512:], before[:, 512:])
     assert torch.equal(out_big[:, 512:], torch.zeros(6, 8, dtype=torch.bfloat16, device=cuda))
     assert torch.equal(res, (before[:, :512].float() + d.float()).to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("mode", ["int8", "bf16"])
+def test_rotary_cache_write_matches_unfused(cuda, mode):
+    """The fused rotary + cache write equals the rotary kernel followed by the cache write
+    (int8_kv_cache_write, or a bf16 scatter) bit for bit: the qkv rows and both caches.  Rows
+    with a position outside the rotary table, or a negative block id, write nothing."""
+    from int8kv import int8_kv_cache_write
+
+    shape = DL.QwenShape(hidden=64, layers=1, q_heads=8, kv_heads=2, head_dim=128, ffn=64, vocab=16)
+    B, width, nb = 9, 6, 60
+    g = torch.Generator().manual_seed(5 if mode == "int8" else 6)
+    qkv = (torch.randn(B, shape.qkv_width, generator=g) * 2).to(torch.bfloat16).to(cuda)
+    pos = torch.randint(0, width * 16, (B,), generator=g)
+    pos[3] = 10_000  # beyond the rotary table: untouched, nothing written
+    bt = torch.randperm(nb, generator=g)[: B * width].view(B, width).to(torch.int32)
+    bt[5, pos[5] // 16] = -1  # a negative block id: the row is rotated, its cache write skipped
+    cos, sin = DL.rope_tables(shape, width * 16, cuda)
+    dtype = torch.int8 if mode == "int8" else torch.bfloat16
+    kc = torch.randint(-100, 100, (nb, 16, 2, 128), generator=g).to(dtype).to(cuda)
+    vc = torch.randint(-100, 100, (nb, 16, 2, 128), generator=g).to(dtype).to(cuda)
+    ks = torch.tensor([0.02, 0.05], device=cuda)
+    vs = torch.tensor([0.03, 0.01], device=cuda)
+    pos_d, bt_d = pos.to(cuda), bt.to(cuda)
+
+    ref_qkv, ref_k, ref_v = qkv.clone(), kc.clone(), vc.clone()
+    DL.hip_rotary_(ref_qkv, shape.q_heads + shape.kv_heads, 128, pos_d, cos, sin)
+    q, k, v = DL._split_qkv(ref_qkv, shape)
+    ok = (pos < width * 16) & (bt[torch.arange(B), (pos // 16).clamp(max=width - 1)] >= 0)
+    rows = torch.nonzero(ok).view(-1)
+    slots = (bt[rows, pos[rows] // 16].long() * 16 + pos[rows] % 16).to(cuda)
+    if mode == "int8":
+        int8_kv_cache_write(k[rows.to(cuda)], v[rows.to(cuda)], ref_k, ref_v, slots, ks, vs)
+    else:
+        ref_k.view(-1, 2, 128).index_copy_(0, slots, k[rows.to(cuda)].contiguous())
+        ref_v.view(-1, 2, 128).index_copy_(0, slots, v[rows.to(cuda)].contiguous())
+
+    DL.hip_rotary_cache_write_(qkv, shape, pos_d, cos, sin, bt_d, kc, vc,
+                               ks if mode == "int8" else None, vs if mode == "int8" else None)
+    torch.cuda.synchronize()
+    assert torch.equal(qkv, ref_qkv)
+    assert torch.equal(kc, ref_k) and torch.equal(vc, ref_v)
+
+
+def test_argmax_rows_matches_torch(cuda):
+    """First maximum per row, as torch.argmax on the same device: ties, -inf rows, a NaN."""
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(12, 152064, generator=g).to(torch.bfloat16)
+    x[1, 1000] = x[1, 99_000] = 50.0  # tie: the lower index wins
+    x[2, :] = -float("inf")
+    x[3, 77] = float("inf")
+    x[4, 5] = x[4, 6] = float("inf")
+    x[5, 123_456] = float("nan")
+    x[6, :] = 1.0  # all equal
+    x[7, 152_058] = 70.0  # the maximum in the last, partial 8-element piece of a shortened row
+    x[8, 3] = x[8, 152_059] = 80.0  # a tie between a 16-byte piece and that partial piece
+    x[9, 500] = x[9, 20] = float("nan")  # two NaNs: the first one
+    xd = x.to(cuda)
+    out = torch.empty(12, dtype=torch.int64, device=cuda)
+    DL.hip_argmax_rows(xd, out)
+    view = xd[:, 1:-3]  # misaligned rows, row stride above the row length: 2-byte loads
+    out2 = torch.empty(12, dtype=torch.int64, device=cuda)
+    DL.hip_argmax_rows(view, out2)
+    short = xd[:, :152_061]  # aligned rows with a 5-element remainder after the 16-byte loads
+    out3 = torch.empty(12, dtype=torch.int64, device=cuda)
+    DL.hip_argmax_rows(short, out3)
+    torch.cuda.synchronize()
+    assert torch.equal(out, xd.argmax(-1))
+    assert torch.equal(out2, view.argmax(-1))
+    assert torch.equal(out3, short.argmax(-1))
+    assert out[1].item() == 1000 and out[6].item() == 0 and out[4].item() == 5
+    assert out3[7].item() == 152_058 and out3[8].item() == 3 and out[9].item() == 20
