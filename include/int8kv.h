@@ -115,8 +115,8 @@ int int8kv_dynamic_cache_write(const void* key, const void* value, int src_dtype
 
 /*
  * Automatic range count of int8kv_paged_decode (num_ranges = 0) on the current device: the
- * token stream of a decode call is cut into this many equal ranges per kv head, a few
- * workgroups per compute unit.
+ * token stream of a decode call is cut into at most this many equal ranges, one wave per SIMD
+ * (4 x compute units / num_kv_heads: 256 for 4 kv heads on MI355X).
  */
 int32_t int8kv_decode_auto_ranges(int32_t num_kv_heads);
 
@@ -158,7 +158,9 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *                 P = min(num_ranges, ceil(units / min_tiles)) equal ranges, one workgroup
  *                 each; a sequence cut by range bounds is combined by the merge kernel.
  *                 0 = automatic (int8kv_decode_auto_ranges).  num_ranges = batch gives one
- *                 range per sequence when all lengths are equal (a single pass).
+ *                 range per sequence when all lengths are equal (a single pass).  With an
+ *                 INT8 cache, twice the automatic count (two waves per SIMD) puts two ranges
+ *                 in each workgroup once every range holds 16 units or more.
  *   min_tiles:    smallest range in tiles (0 = automatic: 2, or 4 when 2-tile ranges could cut
  *                 one sequence into more than 128 ranges; decided from batch, table width and
  *                 block size only).

@@ -10,16 +10,17 @@
 //   * Every sequence is cut into 32-token tiles.  The batch, in order, becomes one stream of
 //     units per kv head: a non-empty sequence is a few "start" units (the cost of reaching its
 //     first tile) followed by its tiles.  The stream is divided into P equal contiguous ranges
-//     (P = a few workgroups per CU, fewer for short batches: at least min_tiles units per
+//     (P = one wave per SIMD by default, fewer for short batches: at least min_tiles units per
 //     range), so a ragged batch costs every workgroup the same whatever the length
 //     distribution.  The unit counts and the range bounds are computed on the device from
 //     seq_lens; the host never reads them.
-//   * A workgroup owns a pair of ranges for W kv heads: waves 0..W-1 the first range, waves
-//     W..2W-1 the second, one wave per (range, kv head).  The W waves of a range read the same
-//     cache rows (their head slices of the same 16-token row groups) at the same time.  A wave
-//     handles all query heads of its GQA group on the matrix cores, so every K/V byte is read
-//     from HBM exactly once, and needs no barrier.  The first range of a pair is the longer
-//     one: of two waves sharing a SIMD the first streams faster (see kFirstShare).
+//   * A workgroup owns a range for W kv heads, one wave per (range, kv head).  The W waves of a
+//     range read the same cache rows (their head slices of the same 16-token row groups) at the
+//     same time.  A wave handles all query heads of its GQA group on the matrix cores, so every
+//     K/V byte is read from HBM exactly once, and needs no barrier.  With a range count of two
+//     waves per SIMD (a caller's choice) INT8 workgroups own a pair of ranges instead, waves
+//     0..W-1 the first and W..2W-1 the second; the first range of a pair is the longer one: of
+//     two waves sharing a SIMD the first streams faster (see kFirstShare).
 //   * A sequence wholly inside one range is finished by that wave (output written directly).
 //     A sequence cut by range bounds leaves (max, sum, accumulator) partials in the workspace,
 //     at most two per range and head; merge_kernel combines them.
@@ -32,11 +33,13 @@
 //     Infinity Cache raises the delivered bandwidth by ~10 % on MI355X (large ragged batch,
 //     5.4 -> 6.1 TB/s).  Smaller pools, which the cache keeps between calls, and 16-bit caches use
 //     plain loads (see stream_load).
-//   * Two tiles are in flight per wave: K(t+2) is requested as soon as the scores of tile t are
-//     formed and V(t+2) as soon as its P*V is done.  The block ids of up to 256 tiles are staged
+//   * DEPTH tiles are in flight per wave: K(t+DEPTH) is requested as soon as the scores of tile
+//     t are formed and V(t+DEPTH) as soon as its P*V is done.  DEPTH is 2 (a 16 KB BF16 tile
+//     keeps 32 KB in flight per wave), or 4 for INT8 waves with long ranges, so that one wave
+//     per SIMD has the bytes in flight of two.  The block ids of up to 256 tiles are staged
 //     in LDS per wave ahead of use, every load in the tile loop is unconditional (requests past
 //     the end of a range repeat its last tile), and the loop body is straight-line code per
-//     tile pair, so no wait for a table read or a branch drains the pipeline.
+//     DEPTH tiles, so no wait for a table read or a branch drains the pipeline.
 //   * INT8 K/V are dequantised in registers to fp16 with the exact magic-number conversion
 //     (0x6400 | (x ^ 0x80)) - 1152 = x, two elements per v_pk_add_f16.  Q is scaled by a power
 //     of two into the upper fp16 range (exact for bf16 input); k_scale * sm_scale * log2(e) and
@@ -103,6 +106,7 @@ struct DecodeArgs {
   int32_t first_share;  // of a range pair's units, the first range's share in 1/256
   int32_t pair_min;     // ranges are paired when P >= pair_min (every CU gets a whole pair)
   int32_t halves;       // ranges per workgroup (1, or 2 with the paired layout)
+  int32_t depth;        // tiles of K/V loads in flight per wave (2, or 4: INT8, one range per WG)
   int32_t head_dim;     // 64 or 128
 };
 
@@ -699,7 +703,8 @@ __device__ __forceinline__ void write_zero_rows(const DecodeArgs& a, int64_t b, 
 
 // Processes tiles [ta, tb) of sequence b (length L) for kv head kvh with one wave, then writes
 // either the final output (full == true) or a partial record.  ids: this wave's LDS slots.
-template <int CACHE, int QT, bool NT, bool QQ, int HD>
+// DEPTH: tiles of K/V loads kept in flight (register buffers).
+template <int CACHE, int QT, bool NT, bool QQ, int HD, int DEPTH>
 __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, int64_t b,
                                             int64_t L, int kvh, int64_t ta, int64_t tb,
                                             bool full, int64_t rec, int lane) {
@@ -739,29 +744,29 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     }
   };
 
-  // Two K and two V register buffers, refilled as soon as they are consumed: K(t + 2) is
-  // requested right after the scores of tile t, V(t + 2) right after its P*V, so up to two
-  // tiles of loads are in flight while a tile is computed.  The loop body handles a pair of
+  // DEPTH K and DEPTH V register buffers, refilled as soon as they are consumed: K(t + DEPTH)
+  // is requested right after the scores of tile t, V(t + DEPTH) right after its P*V, so up to
+  // DEPTH tiles of loads are in flight while a tile is computed.  The loop body handles DEPTH
   // tiles as one straight-line block and every load in it is unconditional (a request past the
   // chunk repeats its last tile, which the caches still hold), so the compiler's wait counts
   // are exact and no wait drains the pipeline.
-  KTile<CACHE, NB, HD> ka, kb2;
-  VTile<CACHE, NB, HD> va, vb2;
-  TileRows<NB> pha, phb;
+  KTile<CACHE, NB, HD> kt[DEPTH];
+  VTile<CACHE, NB, HD> vt[DEPTH];
+  TileRows<NB> ph[DEPTH];
   OpT pop[NB / 2][2];
   auto chunk_prologue = [&]() {
     stage_block_ids<NB>(a, ids, b, c0, c1, nblk, lane);
-    blocks_of(c0, pha);
-    issue_k<CACHE, NB, NT, HD>(ka, kb, pha, a, li, lg);
-    issue_v<CACHE, NB, NT, HD>(va, vb, pha, a, li, lg);
-    blocks_of(c0 + 1 < c1 ? c0 + 1 : c1 - 1, phb);
-    issue_k<CACHE, NB, NT, HD>(kb2, kb, phb, a, li, lg);
-    issue_v<CACHE, NB, NT, HD>(vb2, vb, phb, a, li, lg);
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      blocks_of(c0 + d < c1 ? c0 + d : c1 - 1, ph[d]);
+      issue_k<CACHE, NB, NT, HD>(kt[d], kb, ph[d], a, li, lg);
+      issue_v<CACHE, NB, NT, HD>(vt[d], vb, ph[d], a, li, lg);
+    }
   };
 
-  // The query, the first chunk's block ids and its first two tiles are requested back to back;
-  // the query operand is built once they are all in flight (otherwise three memory latencies
-  // would line up at every segment start).
+  // The query, the first chunk's block ids and its first DEPTH tiles are requested back to
+  // back; the query operand is built once they are all in flight (otherwise three memory
+  // latencies would line up at every segment start).
   OpT qop[HD / 32];
   i32x4 q8op[HD / 64];
   float s_scale;
@@ -777,29 +782,29 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     int64_t t = c0;
     // sched_barrier(0) keeps the compiler's scheduler from sinking the refills past the
     // compute that follows them (which would shorten the prefetch distance).
-    for (; t + 1 < c1; t += 2) {
-      int valid = valid_of(t);
-      tile_scores<CACHE, NB, QQ, HD>(ka, qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
-      blocks_of(t + 2 < c1 ? t + 2 : last, pha);
-      issue_k<CACHE, NB, NT, HD>(ka, kb, pha, a, li, lg);
-      __builtin_amdgcn_sched_barrier(0);
-      tile_pv<CACHE, NB, HD>(va, pop, acc, valid, lg);
-      issue_v<CACHE, NB, NT, HD>(va, vb, pha, a, li, lg);
-      __builtin_amdgcn_sched_barrier(0);
-
-      valid = valid_of(t + 1);
-      tile_scores<CACHE, NB, QQ, HD>(kb2, qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
-      blocks_of(t + 3 < c1 ? t + 3 : last, phb);
-      issue_k<CACHE, NB, NT, HD>(kb2, kb, phb, a, li, lg);
-      __builtin_amdgcn_sched_barrier(0);
-      tile_pv<CACHE, NB, HD>(vb2, pop, acc, valid, lg);
-      issue_v<CACHE, NB, NT, HD>(vb2, vb, phb, a, li, lg);
-      __builtin_amdgcn_sched_barrier(0);
+    for (; t + DEPTH - 1 < c1; t += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        const int valid = valid_of(t + d);
+        tile_scores<CACHE, NB, QQ, HD>(kt[d], qop, q8op, acc, m_run, l_part, valid, lg, s_scale,
+                                       pop);
+        blocks_of(t + d + DEPTH < c1 ? t + d + DEPTH : last, ph[d]);
+        issue_k<CACHE, NB, NT, HD>(kt[d], kb, ph[d], a, li, lg);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_pv<CACHE, NB, HD>(vt[d], pop, acc, valid, lg);
+        issue_v<CACHE, NB, NT, HD>(vt[d], vb, ph[d], a, li, lg);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    if (t < c1) {  // odd tile count: the last tile is in the A buffers
-      const int valid = valid_of(t);
-      tile_scores<CACHE, NB, QQ, HD>(ka, qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
-      tile_pv<CACHE, NB, HD>(va, pop, acc, valid, lg);
+    // The last c1 - t < DEPTH tiles of the chunk are in buffers 0, 1, ...
+#pragma unroll
+    for (int d = 0; d + 1 < DEPTH; ++d) {
+      if (t + d < c1) {
+        const int valid = valid_of(t + d);
+        tile_scores<CACHE, NB, QQ, HD>(kt[d], qop, q8op, acc, m_run, l_part, valid, lg, s_scale,
+                                       pop);
+        tile_pv<CACHE, NB, HD>(vt[d], pop, acc, valid, lg);
+      }
     }
     if (c1 >= tb) break;
     c0 = c1;
@@ -842,8 +847,8 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
 // grid (ceil(max_ranges / 2), num_kv_heads / W), block 2W waves; wave w of workgroup (x, y)
 // handles kv head y * W + w % W over stream range 2x + w / W (paired ranges) or
 // x + (w / W) grid.x.
-template <int CACHE, int QT, bool NT, bool QQ, int HALVES, int HD>
-__global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(DecodeArgs a) {
+template <int CACHE, int QT, bool NT, bool QQ, int HALVES, int HD, int DEPTH>
+__global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(DEPTH > 2 ? 1 : 2))) void decode_kernel(DecodeArgs a) {
   __shared__ int32_t s_ids[HALVES * kMaxWavesPerWG][kChunkTiles * tile_blocks<CACHE>()];
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -894,7 +899,7 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(2)
         const int64_t te = (u1 < first + nb ? u1 : first + nb) - first;
         if (ta >= te) continue;
         const bool full = ta == 0 && te == nb;
-        run_segment<CACHE, QT, NT, QQ, HD>(a, s_ids[wave], base + j, Lb, kvh, ta, te, full,
+        run_segment<CACHE, QT, NT, QQ, HD, DEPTH>(a, s_ids[wave], base + j, Lb, kvh, ta, te, full,
                                2 * r + cut_slot(ta), lane);
       }
     }
@@ -1029,7 +1034,14 @@ constexpr int kSeqStartCost = 2;  // stream units per sequence start (about one 
 constexpr int kMinTilesSmall = 2;
 constexpr int kMinTilesLarge = 4;
 constexpr int64_t kMaxMergeRanges = 128;  // ranges per sequence the merge takes in 4 rounds
-constexpr int kWavesPerCU = 8;  // resident decode waves per CU the automatic range count targets
+// Resident decode waves per CU the automatic range count targets: one per SIMD.  Against two
+// per SIMD (the second of which streams ~30 % slower) it measured 3-11 % faster on every
+// shape tried on MI355X from B=1 x 32k to B=128 x 2048 tokens and on cfg3's BF16 call, and
+// equal on cfg3's INT8 call with four tiles in flight.
+constexpr int kWavesPerCU = 4;
+// INT8 ranges of at least this many units (host-side bound) keep four tiles in flight per wave;
+// shorter ones two (the deeper prologue and its unused refills cost 2-3 us on short ranges).
+constexpr int64_t kDeepMinUnits = 32;
 constexpr int64_t kInfinityCacheBytes = 256LL << 20;  // MI355X last-level (MALL) capacity
 // Share (1/256) of a range pair's units given to the first half of the workgroup.  Two waves
 // share each SIMD, and the first (waves 0..W-1) streams ~30 % faster than the second on
@@ -1100,12 +1112,17 @@ template <int CACHE, int QT, bool NT, bool QQ, int HD>
 void launch_main(const DecodeArgs& a, dim3 grid, int W, hipStream_t s) {
   if constexpr (CACHE == kI8) {
     if (a.halves == 2) {
-      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 2, HD>), grid, dim3(2 * W * kWave), 0, s,
+      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 2, HD, 2>), grid, dim3(2 * W * kWave), 0,
+                         s, a);
+      return;
+    }
+    if (a.depth == 4) {
+      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 4>), grid, dim3(W * kWave), 0, s,
                          a);
       return;
     }
   }
-  hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD>), grid, dim3(W * kWave), 0, s, a);
+  hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 2>), grid, dim3(W * kWave), 0, s, a);
 }
 
 template <int CACHE, int QT, int HD>
@@ -1270,13 +1287,12 @@ extern "C" int int8kv_paged_decode(
   a.sl_is64 = seq_lens_dtype == INT8KV_I64;
   a.sm_scale_log2e = sm_scale * kLog2e;
   a.first_share = kFirstShare;
-  // Pairs only pay when every CU gets one (INT8 caches; the 16-bit kernel measured 1 % slower
-  // with them).
   {
-    // Paired layout (two ranges per workgroup, the first one longer) for INT8 calls that can
-    // reach a pair per CU: P >= pair_min needs at least pair_min * min_tiles units, bounded
-    // here by batch x (longest possible sequence).  Smaller calls and 16-bit caches (1 %
-    // slower paired) keep one range per workgroup.
+    // Paired layout (two ranges per workgroup, the first one longer) for INT8 calls whose
+    // range count reaches a pair per CU (two waves per SIMD: only an explicit num_ranges does)
+    // and that can fill it: P >= pair_min needs at least pair_min * min_tiles units, bounded
+    // here by batch x (longest possible sequence).  16-bit caches (1 % slower paired) keep one
+    // range per workgroup.
     const int64_t wgs_y = num_kv_heads / waves_per_wg(num_kv_heads);  // workgroups per range
     const int64_t pair_min = (2LL * cu_count() + wgs_y - 1) / wgs_y;
     const double units_max =
@@ -1286,6 +1302,13 @@ extern "C" int int8kv_paged_decode(
                         units_max >= (double)pair_min * kPairMinUnits;
     a.halves = paired ? 2 : 1;
     a.pair_min = paired ? (int32_t)pair_min : 0x7fffffff;
+    // One wave per SIMD at most (every range's waves resident at once) and long ranges: INT8
+    // waves keep four tiles in flight instead of two, the bytes in flight of two waves.
+    a.depth = cache_dtype == INT8KV_I8 && !paired &&
+                      (int64_t)num_ranges * num_kv_heads <= 4LL * cu_count() &&
+                      units_max >= (double)kDeepMinUnits * num_ranges
+                  ? 4
+                  : 2;
   }
 
   // Non-temporal K/V loads when the call may stream more than the Infinity Cache holds: the

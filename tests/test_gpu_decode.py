@@ -359,17 +359,49 @@ def test_misaligned_query_is_copied(cuda):
     assert torch.equal(a, b)
 
 
+def _pair_splits(hkv: int, batch: int) -> int:
+    """Splits per sequence giving the range count of two waves per SIMD (twice the automatic
+    count), the count at which INT8 workgroups take a pair of ranges."""
+    from int8kv import _lib
+
+    ranges = 2 * _lib.load().int8kv_decode_auto_ranges(hkv)
+    assert ranges % batch == 0
+    return ranges // batch
+
+
 @pytest.mark.parametrize("hq,hkv,lens", [
-    (28, 4, [8192, 8000, 7777, 8192, 1, 8191, 6000, 8192]),
-    (32, 8, [4096] * 12 + [1, 333, 4095, 4097]),
+    # 8485 stream units >= 16 x 512 ranges: paired workgroups for 4 kv heads
+    (28, 4, [33000, 32768, 33001, 40000, 1, 33333, 32769, 34000]),
+    # 4128 units >= 16 x 256 ranges (8 kv heads: two workgroups per range)
+    (32, 8, [8192] * 15 + [8191]),
 ])
 def test_paired_ranges_regime(cuda, hq, hkv, lens):
-    """Batches large enough to give every CU a pair of ranges (the uneven first/second split of
-    each workgroup) against the oracle, and against one range per sequence."""
+    """Two ranges per workgroup (the uneven first/second split) at the explicit range count of
+    two waves per SIMD, against the oracle; the same inputs at the automatic count and with one
+    range per sequence."""
     c = decode_case(lens, seed=hkv + len(lens), hq=hq, hkv=hkv)
     ref = oracle_int8(c)
-    _check(_int8(c, cuda), ref, f"paired hq={hq} hkv={hkv}")
+    splits = _pair_splits(hkv, len(lens))
+    _check(_int8(c, cuda, num_splits=splits), ref, f"paired hq={hq} hkv={hkv}")
+    _check(_int8(c, cuda), ref, f"automatic hq={hq} hkv={hkv}")
     _check(_int8(c, cuda, num_splits=1), ref, f"single pass hq={hq} hkv={hkv}")
+
+
+@pytest.mark.parametrize("splits", [1, 2, None])
+def test_four_tiles_in_flight(cuda, splits):
+    """INT8 ranges of at least 32 stream units with at most one wave per SIMD keep four tiles of
+    K/V loads in flight per wave (one or two ranges per sequence here; the automatic count cuts
+    these short batches into short ranges, which keep two).  Tile counts leave 0-3 tiles after
+    the last group of four (129, 258 = 256 + 2, 3, 4, 2, 1, 515 = 2 x 256 + 3 tiles); two
+    sequences are longer than one 256-tile chunk of staged block ids; quantize_q as well."""
+    lens = [4097, 8229, 65, 97, 33, 1, 16384 + 95, 640]
+    c = decode_case(lens, seed=40 + (splits or 0), extra_blocks=5)
+    ref = oracle_int8(c)
+    _check(_int8(c, cuda, num_splits=splits), ref, f"splits={splits}")
+    ref_q = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                  c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
+                                  quantize_q=True)
+    _check(_int8(c, cuda, num_splits=splits, quantize_q=True), ref_q, f"splits={splits} qq")
 
 
 @pytest.mark.parametrize("splits", [None, 1, 3])
@@ -423,13 +455,15 @@ def test_head_dim_64(cuda, hq, hkv):
 
 
 def test_head_dim_64_paired_regime(cuda):
-    """head_dim 64 in batches large enough for the two-range workgroups: 16 x 8192 tokens pair
-    the ranges (32 q / 8 kv heads); 15 x 8192 + 77 tokens take the same grid with unpaired
-    ranges (the device-side check on the actual units)."""
+    """head_dim 64 at the range count of two waves per SIMD: 16 x 8192 tokens pair the ranges
+    (32 q / 8 kv heads); 15 x 8192 + 77 tokens take the same grid with unpaired ranges (the
+    device-side check on the actual units).  The automatic count and one range per sequence
+    (four tiles in flight) as well."""
     for lens in ([8192] * 16, [8192] * 15 + [77]):
         c = decode_case(lens, seed=64 + len(lens), hq=32, hkv=8, head_dim=64, extra_blocks=3)
         ref = oracle_int8(c)
-        _check(_int8(c, cuda), ref, f"d64 large {lens[-1]}")
+        _check(_int8(c, cuda, num_splits=_pair_splits(8, len(lens))), ref, f"d64 large {lens[-1]}")
+        _check(_int8(c, cuda), ref, f"d64 automatic {lens[-1]}")
         _check(_int8(c, cuda, num_splits=1), ref, f"d64 single pass {lens[-1]}")
 
 
