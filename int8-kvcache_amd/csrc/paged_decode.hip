@@ -844,9 +844,10 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   }
 }
 
-// grid (ceil(max_ranges / 2), num_kv_heads / W), block 2W waves; wave w of workgroup (x, y)
-// handles kv head y * W + w % W over stream range 2x + w / W (paired ranges) or
-// x + (w / W) grid.x.
+// grid (ceil(max_ranges / HALVES), num_kv_heads / W), block HALVES * W waves; wave w of
+// workgroup (x, y) handles kv head y * W + w % W over stream range x (HALVES = 1), or, with two
+// ranges per workgroup, 2x + w / W (paired ranges) or x + (w / W) grid.x.  DEPTH: tiles in flight
+// per wave (4 only in the one-wave-per-SIMD layout, whose register budget allows it).
 template <int CACHE, int QT, bool NT, bool QQ, int HALVES, int HD, int DEPTH>
 __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(DEPTH > 2 ? 1 : 2))) void decode_kernel(DecodeArgs a) {
   __shared__ int32_t s_ids[HALVES * kMaxWavesPerWG][kChunkTiles * tile_blocks<CACHE>()];
@@ -1049,8 +1050,8 @@ constexpr int64_t kInfinityCacheBytes = 256LL << 20;  // MI355X last-level (MALL
 // 160 (62.5 %) measured best between cfg3 (~152) and B=32 x 8320 (~168): -2 us at both.
 constexpr int32_t kFirstShare = 160;
 
-// kv heads per workgroup (two waves each, one per range of the pair): the largest of 4, 3, 2, 1
-// dividing num_kv_heads.
+// kv heads per workgroup (one wave each per range it owns): the largest of 4, 3, 2, 1 dividing
+// num_kv_heads.
 int waves_per_wg(int32_t num_kv_heads) {
   for (int w = kMaxWavesPerWG; w > 1; --w)
     if (num_kv_heads % w == 0) return w;
