@@ -255,3 +255,29 @@ def test_int8_and_bf16_modes_agree(model):
         deq = ki.astype(np.float32) * a.cache.k_scale[l].cpu().numpy()[None, :, None]
         step = a.cache.k_scale[l].cpu().numpy()[None, :, None]
         assert (np.abs(deq - np.clip(kb, -127 * step, 127 * step)) <= 0.5 * step * 1.0001).all()
+
+
+@pytest.mark.parametrize("mode", DL.MODES)
+def test_fused_step_matches_unfused(model, mode, monkeypatch):
+    """The decode step with the fused kernels (rotary + cache write in one launch, the library
+    argmax) equals the unfused sequence (rotary kernel, slot arithmetic, cache write, torch
+    argmax) bit for bit: logits, greedy tokens and every layer's K/V cache over three steps."""
+    loops = {}
+    for fused in (True, False):
+        monkeypatch.setattr(DL, "FUSED_STEP", fused)
+        loop = _make(model, mode)
+        loop.prefill(model[2])
+        steps = []
+        for _ in range(3):
+            loop.step_eager()
+            steps.append((loop.logits.clone(), loop.tokens.clone()))
+        torch.cuda.synchronize()
+        loops[fused] = (loop, steps)
+    (a, sa), (b, sb) = loops[True], loops[False]
+    for i, ((la, ta), (lb, tb)) in enumerate(zip(sa, sb)):
+        assert torch.equal(la, lb), f"step {i}: logits differ"
+        assert torch.equal(ta, tb), f"step {i}: tokens differ"
+    for l in range(SHAPE.layers):
+        assert torch.equal(a.cache.key[l], b.cache.key[l]), f"layer {l}: key cache differs"
+        assert torch.equal(a.cache.value[l], b.cache.value[l]), f"layer {l}: value cache differs"
+    assert torch.equal(a.generated, b.generated)
