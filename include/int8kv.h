@@ -60,6 +60,7 @@ enum int8kv_dtype {
 #define INT8KV_DECODE_MERGE 2u  /* run the split merge kernel */
 #define INT8KV_DECODE_ALL 3u
 #define INT8KV_DECODE_QUANTIZE_Q 4u  /* quantise q to int8 per (sequence, head) first */
+#define INT8KV_DECODE_PER_SEQUENCE 8u  /* one workgroup per (sequence, kv head), no merge */
 
 /*
  * Static per-head INT8 quantisation of K and V plus the slot_mapping scatter into the paged
@@ -164,12 +165,22 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *   min_tiles:    smallest range in tiles (0 = automatic: 2, or 4 when 2-tile ranges could cut
  *                 one sequence into more than 128 ranges; decided from batch, table width and
  *                 block size only).
+ *                 With num_ranges = 0 and min_tiles = 0, short calls take the per-sequence layout
+ *                 below instead (decided from batch, num_kv_heads, table width and block size
+ *                 only: at most one workgroup per compute unit, and sequences of at most 512
+ *                 tokens, or of at most 2048 (1024 for a 16-bit cache) when the workgroups fill
+ *                 half the compute units).
  *   flags:        INT8KV_DECODE_ALL normally; MAIN and MERGE separately let a caller time the
  *                 two kernels on their own (MERGE must follow MAIN with identical arguments).
  *                 OR INT8KV_DECODE_QUANTIZE_Q to quantise each (sequence, query head) row of q
  *                 to int8 first, as the reference's quantize_q=True
  *                 (src/triton_ops/int8_paged_attention.py:137-146): q_scale = max(absmax/127,
  *                 1e-6), q8 = clamp(round_half_away_from_zero(q / q_scale), -127, 127).
+ *                 OR INT8KV_DECODE_PER_SEQUENCE for the per-sequence layout: one workgroup per
+ *                 (sequence, kv head), whose waves split the sequence and combine their partial
+ *                 softmax states on chip; one kernel, the workspace is not touched and MERGE
+ *                 does nothing.  Suited to short sequences (each workgroup streams its whole
+ *                 sequence on one compute unit).
  *
  * Supported sizes: head_dim 64 or 128, block_size a power of two in [16, 65536] (16 and 32 are
  * vLLM's usual values), group = num_q_heads / num_kv_heads in [1, 16].  Other sizes return

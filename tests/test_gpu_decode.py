@@ -475,3 +475,43 @@ def test_unsupported_head_dims_raise(cuda):
         qx = torch.zeros(q.shape[0], q.shape[1], d, dtype=q.dtype, device=cuda)
         with pytest.raises(RuntimeError, match="E_SHAPE"):
             int8kv.int8_paged_attention(qx, kx, kx.clone(), bt, sl, ks, vs)
+
+
+def _group(q, kc, vc, bt, sl, ks, vs, extra_flags=0):
+    from int8kv import _decode, _lib
+
+    out = torch.empty_like(q)
+    _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, out, 0,
+                         _lib.DECODE_ALL | _lib.DECODE_PER_SEQUENCE | extra_flags)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(28, 4, 128), (14, 2, 64), (8, 8, 128)])
+def test_per_sequence_mode(cuda, hq, hkv, d):
+    """One workgroup per (sequence, kv head) whose waves merge their states in LDS
+    (INT8KV_DECODE_PER_SEQUENCE): against the oracle for INT8 (fp32 query too) and quantize_q,
+    and for a BF16 cache; empty and one-token sequences, fewer tiles than waves (waves with no
+    tiles), tile counts that do not divide evenly, a sequence longer than one 256-tile chunk."""
+    from int8kv import _lib
+
+    lens = [0, 1, 17, 33, 95, 257, 511, 4096, 8229, 300]
+    c = decode_case(lens, seed=hq + d, hq=hq, hkv=hkv, head_dim=d, extra_blocks=9)
+    ref = oracle_int8(c)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    out = _group(q, kc, vc, bt, sl, ks, vs)
+    assert (out[0] == 0).all()
+    _check(out, ref, f"per-sequence int8 {hq}/{hkv}/{d}")
+    out32 = _group(q.float(), kc, vc, bt, sl, ks, vs)
+    err, _, _ = metrics(out32.cpu().numpy(), ref)
+    assert err <= 1e-3, err
+    ref_q = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                  c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
+                                  quantize_q=True)
+    _check(_group(q, kc, vc, bt, sl, ks, vs, _lib.DECODE_QUANTIZE_Q), ref_q,
+           f"per-sequence quantize_q {hq}/{hkv}/{d}")
+    k16, v16 = bf16_caches(c)
+    ref16 = O.paged_attention_ref(c.query.float().numpy(), k16.float().numpy(), v16.float().numpy(),
+                                  c.block_tables.numpy(), c.seq_lens.numpy())
+    _check(_group(q, k16.to(cuda), v16.to(cuda), bt, sl, None, None), ref16,
+           f"per-sequence bf16 {hq}/{hkv}/{d}")
