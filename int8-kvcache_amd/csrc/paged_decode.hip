@@ -1126,7 +1126,19 @@ using namespace int8kv;
 namespace {
 
 constexpr int kMaxRangesLimit = 1 << 20;
-constexpr int kSeqStartCost = 2;  // stream units per sequence start (about one tile's time each)
+// Stream units charged per sequence start (make_plan).  A wave that moves on to another
+// sequence inside its range lets its pipeline run dry and refills it after two dependent loads
+// (block ids, then the first tiles), which costs about 2 x DEPTH tile times for 8 KB INT8 tiles
+// and half as many tile times for 16 KB 16-bit tiles.  Measured on MI355X (per-wave exit stamps
+// and sweeps of the charge): with 2 units the INT8 ranges that start a second sequence
+// finished ~2.3 us after the others and set the end of the call; 6 (four tiles in flight) and
+// 4 (two) gave B=128 x U[1,4096] 58.0 -> 54.1 us, B=256 x U[1,2048] 64.1 -> 58.4 us,
+// B=64 x U[1,8192] 51.9 -> 49.9 us, B=32 x U[1,4096] 17.8 -> 16.9 us and the large ragged
+// batch 190.5 -> 188.8 us, and were neutral on uniform lengths; larger charges lose again.
+// 16-bit caches measured best at 2-3.
+constexpr int kSeqStartCost = 2;        // host-side bounds, and 16-bit caches
+constexpr int kSeqStartCostI8 = 4;      // INT8, two tiles in flight
+constexpr int kSeqStartCostI8Deep = 6;  // INT8, four tiles in flight
 // Smallest automatic range (see auto_min_tiles).
 constexpr int kMinTilesSmall = 2;
 constexpr int kMinTilesLarge = 4;
@@ -1444,6 +1456,10 @@ extern "C" int int8kv_paged_decode(
                   ? 4
                   : 2;
   }
+  // The layout above was chosen with the base charge; the plan itself charges what a sequence
+  // start costs at the chosen depth (kSeqStartCost*).  decode_kernel and merge_kernel read the
+  // same value, so their range bounds agree.
+  if (cache_dtype == INT8KV_I8) a.seq_cost = a.depth == 4 ? kSeqStartCostI8Deep : kSeqStartCostI8;
 
   // Non-temporal K/V loads when the call may stream more than the Infinity Cache holds: the
   // most it can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).
