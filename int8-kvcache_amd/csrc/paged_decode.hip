@@ -751,10 +751,10 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
 
   // DEPTH K and DEPTH V register buffers, refilled as soon as they are consumed: K(t + DEPTH)
   // is requested right after the scores of tile t, V(t + DEPTH) right after its P*V, so up to
-  // DEPTH tiles of loads are in flight while a tile is computed.  The loop body handles DEPTH
-  // tiles as one straight-line block and every load in it is unconditional (a request past the
-  // chunk repeats its last tile, which the caches still hold), so the compiler's wait counts
-  // are exact and no wait drains the pipeline.
+  // DEPTH tiles of loads are in flight while a tile is computed.  The main loop body handles
+  // DEPTH tiles as one straight-line block and every load in it is unconditional, so the
+  // compiler's wait counts are exact and no wait drains the pipeline; only the chunk's last
+  // full block refills conditionally (its waits may be coarser: the pipeline is ending there).
   KTile<CACHE, NB, HD> kt[DEPTH];
   VTile<CACHE, NB, HD> vt[DEPTH];
   TileRows<NB> ph[DEPTH];
@@ -782,24 +782,37 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     s_scale = finish_query<CACHE, QT, QQ, HD>(a, qraw, kvh, qop, q8op);
   }
 
+  // Tile t + d (buffer d): scores, refill K with tile t + d + DEPTH, P*V, refill V.  refill is a
+  // compile-time true inside the main loop; in the chunk's last full block it stops the refills
+  // at the chunk's end, so no request repeats a tile there (with non-temporal loads a repeated
+  // tile is read from HBM again: 1-4 tiles per segment, ~2 % of a large call's bytes).
+  // sched_barrier(0) keeps the compiler's scheduler from sinking the refills past the compute
+  // that follows them (which would shorten the prefetch distance).
+  auto tile_step = [&](int64_t t, int d, bool refill) {
+    const int valid = valid_of(t + d);
+    tile_scores<CACHE, NB, QQ, HD>(kt[d], qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
+    if (refill) {
+      blocks_of(t + d + DEPTH, ph[d]);
+      issue_k<CACHE, NB, NT, HD>(kt[d], kb, ph[d], a, li, lg);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    tile_pv<CACHE, NB, HD>(vt[d], pop, acc, valid, lg);
+    if (refill) issue_v<CACHE, NB, NT, HD>(vt[d], vb, ph[d], a, li, lg);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
   while (true) {
-    const int64_t last = c1 - 1;
     int64_t t = c0;
-    // sched_barrier(0) keeps the compiler's scheduler from sinking the refills past the
-    // compute that follows them (which would shorten the prefetch distance).
-    for (; t + DEPTH - 1 < c1; t += DEPTH) {
+    // Every refill of these blocks lies inside the chunk.
+    for (; t + 2 * DEPTH - 1 < c1; t += DEPTH) {
 #pragma unroll
-      for (int d = 0; d < DEPTH; ++d) {
-        const int valid = valid_of(t + d);
-        tile_scores<CACHE, NB, QQ, HD>(kt[d], qop, q8op, acc, m_run, l_part, valid, lg, s_scale,
-                                       pop);
-        blocks_of(t + d + DEPTH < c1 ? t + d + DEPTH : last, ph[d]);
-        issue_k<CACHE, NB, NT, HD>(kt[d], kb, ph[d], a, li, lg);
-        __builtin_amdgcn_sched_barrier(0);
-        tile_pv<CACHE, NB, HD>(vt[d], pop, acc, valid, lg);
-        issue_v<CACHE, NB, NT, HD>(vt[d], vb, ph[d], a, li, lg);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      for (int d = 0; d < DEPTH; ++d) tile_step(t, d, true);
+    }
+    // The chunk's last full block refills only the tiles the chunk still has.
+    if (t + DEPTH - 1 < c1) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) tile_step(t, d, t + d + DEPTH < c1);
+      t += DEPTH;
     }
     // The last c1 - t < DEPTH tiles of the chunk are in buffers 0, 1, ...
 #pragma unroll
