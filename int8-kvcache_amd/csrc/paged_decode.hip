@@ -109,6 +109,7 @@ struct DecodeArgs {
   int32_t depth;        // tiles of K/V loads in flight per wave (2, or 4: INT8, one range per WG)
   int32_t group_mode;   // one workgroup per (sequence, kv head), states merged in LDS
   int32_t head_dim;     // 64 or 128
+  int32_t scan32;       // a 64-sequence chunk's units fit 32 bits (see units_scan)
 };
 
 // ------------------------------------------------------------------------ wave utilities
@@ -125,6 +126,22 @@ __device__ __forceinline__ int64_t wave_inclusive_scan(int64_t x, int lane) {
     if (lane >= o) x += y;
   }
   return x;
+}
+
+// Inclusive prefix sum of a 32-bit value over the wave (all 64 lanes active): DPP row shifts
+// by 1, 2, 4, 8 inside each 16-lane row, then the totals of the rows below (lanes 15, 31, 47,
+// read before they change) added to each row.  A few dozen VALU cycles, against six
+// dependent LDS permutes per 32-bit word for a __shfl_up / __shfl_xor ladder.
+__device__ __forceinline__ int32_t wave_scan32(int32_t x, int lane) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  const int32_t r0 = __builtin_amdgcn_readlane(x, 15);
+  const int32_t r1 = __builtin_amdgcn_readlane(x, 31);
+  const int32_t r2 = __builtin_amdgcn_readlane(x, 47);
+  const int row = lane >> 4;
+  return x + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
 }
 
 __device__ __forceinline__ int64_t readlane64(int64_t x, int lane) {
@@ -160,6 +177,19 @@ __device__ __forceinline__ int64_t units_of(const DecodeArgs& a, int64_t n) {
   return n > 0 ? n + a.seq_cost : 0;
 }
 
+// Inclusive scan / total of the lanes' unit counts over one 64-sequence chunk.  32-bit DPP
+// scan when the host has bounded a chunk's units below 2^31 (scan32: no sequence can exceed
+// 2^25 tiles), else the 64-bit permute ladder.
+__device__ __forceinline__ int64_t units_scan(const DecodeArgs& a, int64_t u, int lane) {
+  if (a.scan32) return (int64_t)wave_scan32((int32_t)u, lane);
+  return wave_inclusive_scan(u, lane);
+}
+
+__device__ __forceinline__ int64_t units_sum(const DecodeArgs& a, int64_t u, int lane) {
+  if (a.scan32) return (int64_t)__builtin_amdgcn_readlane(wave_scan32((int32_t)u, lane), kWave - 1);
+  return wave_sum(u);
+}
+
 // a / b for a >= 0, b > 0, with a 32-bit divide when both fit (the plan's bounds always do in
 // practice; the 64-bit divide is a long instruction sequence on the GPU).
 __device__ __forceinline__ int64_t udiv(int64_t a, int64_t b) {
@@ -181,9 +211,9 @@ struct Plan {
 // L0: this lane's seq_len_of(a, lane), the first 64 sequences' lengths, which the caller keeps
 // in a register for its own walk over the batch (most batches have at most 64 sequences).
 __device__ __forceinline__ Plan make_plan(const DecodeArgs& a, int lane, int64_t L0) {
-  int64_t U = wave_sum(units_of(a, tiles_of(a, L0)));
+  int64_t U = units_sum(a, units_of(a, tiles_of(a, L0)), lane);
   for (int64_t base = kWave; base < a.batch; base += kWave)
-    U += wave_sum(units_of(a, tiles_of(a, seq_len_of(a, base + lane))));
+    U += units_sum(a, units_of(a, tiles_of(a, seq_len_of(a, base + lane))), lane);
   int64_t P = udiv(U + a.min_tiles - 1, a.min_tiles);
   P = P < 1 ? 1 : (P > a.max_ranges ? a.max_ranges : P);
   return {U, P, a.first_share, P >= a.pair_min && U >= (int64_t)kPairMinUnits * P};
@@ -905,7 +935,7 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(DE
     if (base > 0) L = seq_len_of(a, base + lane);
     const int64_t n = tiles_of(a, L);
     const int64_t u = units_of(a, n);
-    const int64_t incl = wave_inclusive_scan(u, lane) + cum;
+    const int64_t incl = units_scan(a, u, lane) + cum;
     const int64_t excl = incl - u;
     const int64_t chunk_end = readlane64(incl, kWave - 1);
     if (chunk_end >= u0) {
@@ -1081,7 +1111,7 @@ __global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
   for (int64_t base = 0; base < b; base += kWave) {
     const int64_t bb = base + lane;
     const int64_t Lb = base == 0 ? L0 : seq_len_of(a, bb);
-    S += wave_sum(bb < b ? units_of(a, tiles_of(a, Lb)) : 0);
+    S += units_sum(a, bb < b ? units_of(a, tiles_of(a, Lb)) : 0, lane);
   }
   const int64_t n = tiles_of(a, b < kWave ? readlane64(L0, (int)b) : seq_len_of(a, b));
   if (n == 0) return;  // zeros written by decode_kernel
@@ -1473,6 +1503,11 @@ extern "C" int int8kv_paged_decode(
   // start costs at the chosen depth (kSeqStartCost*).  decode_kernel and merge_kernel read the
   // same value, so their range bounds agree.
   if (cache_dtype == INT8KV_I8) a.seq_cost = a.depth == 4 ? kSeqStartCostI8Deep : kSeqStartCostI8;
+  // Units of one sequence are at most ceil(table_width x block_size / 32) + seq_cost (lengths are
+  // clamped to the table); 64 of them fit the 32-bit wave scans unless one sequence could hold
+  // more than 2^25 tiles.
+  a.scan32 = (double)kWave * (std::ceil((double)table_width * block_size / a.tile_tokens) +
+                              a.seq_cost) < 2147483647.0;
 
   // Non-temporal K/V loads when the call may stream more than the Infinity Cache holds: the
   // most it can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).

@@ -425,6 +425,27 @@ def test_batches_beyond_one_wave_of_sequences(cuda, splits):
     _check(out, ref, f"B=200 splits={splits}")
 
 
+@pytest.mark.parametrize("splits", [None, 3])
+def test_wide_tables_take_the_64bit_unit_scan(cuda, splits):
+    """A table wide enough that one sequence could hold 2^25 tiles (4096-token blocks, 2^18
+    table entries per row) makes the kernels count stream units with 64-bit wave scans instead
+    of the 32-bit DPP scan: oracle parity over B = 70 (two 64-sequence chunks), one empty
+    sequence in each chunk."""
+    g = torch.Generator().manual_seed(5)
+    lens = torch.randint(1, 600, (70,), generator=g).tolist()
+    lens[3], lens[66] = 9000, 4097
+    c = decode_case(lens, seed=5, block_size=4096, width=1 << 18, extra_blocks=3)
+    sl = c.seq_lens.clone()
+    sl[10] = sl[65] = 0
+    q, kc, vc, bt, _, ks, vs = to_dev(c, cuda)
+    out = int8kv.int8_paged_attention(q, kc, vc, bt, sl.to(cuda), ks, vs, num_splits=splits)
+    torch.cuda.synchronize()
+    ref = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                sl.numpy(), c.k_scale.numpy(), c.v_scale.numpy())
+    assert (out[10] == 0).all() and (out[65] == 0).all()
+    _check(out, ref, f"64-bit unit scan splits={splits}")
+
+
 HD64_SHAPES = [(32, 8), (14, 2), (8, 8)]  # Llama-3.2-1B, Qwen2.5-0.5B, multi-head
 
 
