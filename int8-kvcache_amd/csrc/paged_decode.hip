@@ -1209,15 +1209,14 @@ int waves_per_wg(int32_t num_kv_heads) {
   return 1;
 }
 
+// Compute units of the current device, queried on every call (no state is kept between calls;
+// the runtime answers from its cached device properties).  256 on MI355X.
 int cu_count() {
-  static int cached[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 256;
-  if (dev >= 0 && dev < 64 && cached[dev] > 0) return cached[dev];
   int n = 0;
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
     n = 256;
-  if (dev >= 0 && dev < 64) cached[dev] = n;
   return n;
 }
 
@@ -1243,8 +1242,7 @@ int32_t auto_min_tiles(int64_t batch, int64_t table_width, int32_t block_size, i
 // sequence and it loses (B=8 x 2048: 19.2 vs 14.4 us).  BF16 tiles hold twice the bytes: up to 4
 // tiles per wave.  At most one workgroup per CU (its LDS holds the 8 waves' states).
 bool use_per_sequence(bool int8_cache, int64_t batch, int32_t num_kv_heads, int64_t table_width,
-                      int32_t block_size) {
-  const int64_t cu = cu_count();
+                      int32_t block_size, int64_t cu) {
   const int64_t wgs = batch * num_kv_heads;
   if (wgs > cu) return false;
   const double tiles = std::ceil((double)table_width * block_size / 32.0);  // longest sequence
@@ -1253,8 +1251,8 @@ bool use_per_sequence(bool int8_cache, int64_t batch, int32_t num_kv_heads, int6
   return per_wave <= (int8_cache ? 8 : 4) && 2 * wgs >= cu;
 }
 
-int32_t auto_ranges(int32_t num_kv_heads) {
-  const int64_t p = (int64_t)cu_count() * kWavesPerCU / num_kv_heads;
+int32_t auto_ranges(int32_t num_kv_heads, int64_t cu) {
+  const int64_t p = cu * kWavesPerCU / num_kv_heads;
   return (int32_t)(p < 1 ? 1 : (p > kMaxRangesLimit ? kMaxRangesLimit : p));
 }
 
@@ -1367,7 +1365,7 @@ int launch_q(const DecodeArgs& a, int query_dtype, uint32_t flags, bool nt, hipS
 
 extern "C" int32_t int8kv_decode_auto_ranges(int32_t num_kv_heads) {
   if (num_kv_heads <= 0) return 1;
-  return auto_ranges(num_kv_heads);
+  return auto_ranges(num_kv_heads, cu_count());
 }
 
 extern "C" size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads,
@@ -1376,7 +1374,7 @@ extern "C" size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num
   if (!shape_ok(num_q_heads, num_kv_heads, head_dim, block_size) || num_ranges < 0 ||
       num_ranges > kMaxRangesLimit)
     return 0;
-  if (num_ranges == 0) num_ranges = auto_ranges(num_kv_heads);
+  if (num_ranges == 0) num_ranges = auto_ranges(num_kv_heads, cu_count());
   return workspace_bytes(num_q_heads, num_ranges, head_dim);
 }
 
@@ -1424,7 +1422,8 @@ extern "C" int int8kv_paged_decode(
   }
 
   const bool automatic = num_ranges == 0 && min_tiles == 0;
-  if (num_ranges == 0) num_ranges = auto_ranges(num_kv_heads);
+  const int64_t cus = cu_count();
+  if (num_ranges == 0) num_ranges = auto_ranges(num_kv_heads, cus);
   if (min_tiles == 0) min_tiles = auto_min_tiles(batch, table_width, block_size, num_ranges);
   const size_t need = workspace_bytes(num_q_heads, num_ranges, head_dim);
   if (workspace == nullptr || workspace_bytes_given < need || ((uintptr_t)workspace % 16) != 0)
@@ -1469,7 +1468,7 @@ extern "C" int int8kv_paged_decode(
   a.quantize_q = (flags & INT8KV_DECODE_QUANTIZE_Q) != 0;
   a.group_mode = (flags & INT8KV_DECODE_PER_SEQUENCE) != 0 ||
                  (automatic && use_per_sequence(cache_dtype == INT8KV_I8, batch, num_kv_heads,
-                                                table_width, block_size));
+                                                table_width, block_size, cus));
   a.block_shift = __builtin_ctz((unsigned)block_size);
   a.tile_tokens = kRows * (cache_dtype == INT8KV_I8 ? tile_blocks<kI8>() : tile_blocks<kBF16>());
   a.bt_is64 = table_dtype == INT8KV_I64;
@@ -1483,7 +1482,7 @@ extern "C" int int8kv_paged_decode(
     // here by batch x (longest possible sequence).  16-bit caches (1 % slower paired) keep one
     // range per workgroup.
     const int64_t wgs_y = num_kv_heads / waves_per_wg(num_kv_heads);  // workgroups per range
-    const int64_t pair_min = (2LL * cu_count() + wgs_y - 1) / wgs_y;
+    const int64_t pair_min = (2LL * cus + wgs_y - 1) / wgs_y;
     const double units_max =
         (double)batch * (std::ceil((double)table_width * block_size / a.tile_tokens) + a.seq_cost);
     const bool paired = cache_dtype == INT8KV_I8 && num_ranges >= pair_min &&
@@ -1494,7 +1493,7 @@ extern "C" int int8kv_paged_decode(
     // One wave per SIMD at most (every range's waves resident at once) and long ranges: INT8
     // waves keep four tiles in flight instead of two, the bytes in flight of two waves.
     a.depth = cache_dtype == INT8KV_I8 && !paired &&
-                      (int64_t)num_ranges * num_kv_heads <= 4LL * cu_count() &&
+                      (int64_t)num_ranges * num_kv_heads <= 4LL * cus &&
                       units_max >= (double)kDeepMinUnits * num_ranges
                   ? 4
                   : 2;

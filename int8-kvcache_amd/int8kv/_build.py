@@ -11,6 +11,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -43,11 +44,7 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found; ROCm is required to build libint8kv.so")
 
 
-def build_library(verbose: bool = False) -> Path:
-    """Compiles every HIP source into LIB_PATH (always rebuilds)."""
-    srcs = [str(CSRC_DIR / s) for s in SOURCES]
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc_path(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", *srcs, "-o", str(tmp)]
+def _run(cmd, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -57,7 +54,29 @@ def build_library(verbose: bool = False) -> Path:
         raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
     if verbose and msgs:
         print("\n".join(msgs), flush=True)
-    os.replace(tmp, LIB_PATH)
+
+
+def build_library(verbose: bool = False) -> Path:
+    """Compiles every HIP source into LIB_PATH (always rebuilds): one hipcc process per source,
+    in parallel, then one link."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    hipcc = hipcc_path()
+    obj_dir = Path(tempfile.mkdtemp(prefix="int8kv_build_"))
+    try:
+        compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+        objs = [obj_dir / (Path(s).stem + ".o") for s in SOURCES]
+        cmds = [[hipcc, *compile_flags, f"-I{INCLUDE_DIR}", "-c", str(CSRC_DIR / s), "-o", str(o)]
+                for s, o in zip(SOURCES, objs)]
+        with ThreadPoolExecutor(max_workers=len(cmds)) as pool:
+            for fut in [pool.submit(_run, c, verbose) for c in cmds]:
+                fut.result()
+        tmp = LIB_PATH.with_suffix(".so.tmp")
+        _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)],
+             verbose)
+        os.replace(tmp, LIB_PATH)
+    finally:
+        shutil.rmtree(obj_dir, ignore_errors=True)
     return LIB_PATH
 
 

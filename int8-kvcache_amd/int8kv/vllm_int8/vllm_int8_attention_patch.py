@@ -1,141 +1,158 @@
-"""INT8 decode attention inside vLLM (vllm_int8/vllm_int8_attention_patch.py of the reference).
+"""INT8 decode attention inside vLLM: a patch of ``TritonAttentionImpl.forward``.
 
-Patches ``TritonAttentionImpl.forward``.  Pure decode steps of layers that have an INT8 shadow
-cache run ``int8_paged_attention`` (HIP); prefill and chunked prefill fall back to vLLM.
-Modes: "shadow" (vLLM output kept, INT8 compared), "takeover" (INT8 output, vLLM still run for
-the comparison), "int8_only" (INT8 output only).
+Counterpart of the reference's vllm_int8/vllm_int8_attention_patch.py:140-334.  The public names
+its drivers use are kept: ``apply_int8_attention_patch``, ``PatchMode`` and the counters
+``ATTN_COMPARE_COUNT``, ``ATTN_METRICS``, ``ATTN_INT8_HITS``, ``ATTN_INT8_STATS``
+(bench/run_qwen_case_final.py:129-137, scripts/08-09 of the reference read them).
+
+How one patched forward call is routed:
+  * the layer owns no INT8 cache, or the call is not a pure decode step (prefill and chunked
+    prefill have more query tokens than sequences, or max_query_len > 1): vLLM's own forward;
+  * mode "int8_only": int8_paged_attention (HIP) on the layer's INT8 cache, nothing else;
+  * mode "shadow": vLLM's forward, then the INT8 result, compared with it; vLLM's output stays;
+  * mode "takeover": as "shadow", but the INT8 result replaces vLLM's output.
 """
 
 from __future__ import annotations
 
-from typing import Literal
+from dataclasses import dataclass
+from typing import Literal, Optional
 
 import torch
-import torch.nn.functional as F
 
 from ..int8_paged_attention import int8_paged_attention
 from .cache_manager import get_layer_cache, has_layer_cache
 
 PatchMode = Literal["shadow", "takeover", "int8_only"]
+MODES = ("shadow", "takeover", "int8_only")
 
 _PATCHED = False
+# Comparisons recorded per layer (shadow / takeover) and the metrics of each.
 ATTN_COMPARE_COUNT: dict[str, int] = {}
 ATTN_METRICS: dict[str, list] = {}
-# Decode steps that actually ran int8_paged_attention (int8_only / takeover).
+# Decode calls answered by the INT8 op alone (int8_only), per layer, and the batch sizes seen.
 ATTN_INT8_HITS: dict[str, int] = {}
 ATTN_INT8_STATS: dict[str, int] = {"last_batch": 0, "max_batch": 0}
 
 
-def _relative_l2(x: torch.Tensor, y: torch.Tensor) -> float:
-    x, y = x.float(), y.float()
-    return ((x - y).norm() / y.norm().clamp_min(1e-12)).item()
+@dataclass(frozen=True)
+class DecodeStep:
+    """The inputs of one pure decode step: a query row per sequence."""
+
+    query: torch.Tensor  # [B, Hq, D]: the first B rows of vLLM's (possibly padded) query
+    block_table: torch.Tensor  # [B, W], contiguous
+    seq_lens: torch.Tensor  # [B], contiguous
 
 
-def _cosine(x: torch.Tensor, y: torch.Tensor) -> float:
-    return F.cosine_similarity(x.float().reshape(-1), y.float().reshape(-1), dim=0).item()
+def decode_step_of(query: torch.Tensor, attn_metadata) -> Optional[DecodeStep]:
+    """The decode inputs of this forward call, or None when it is not a pure decode step.
 
-
-def _mae(x: torch.Tensor, y: torch.Tensor) -> float:
-    return (x.float() - y.float()).abs().mean().item()
-
-
-def _get_block_table(attn_metadata):
-    """vLLM's Triton metadata has block_table; some wrappers use block_tables (:65-70)."""
-    bt = getattr(attn_metadata, "block_table", None)
-    if bt is None:
-        bt = getattr(attn_metadata, "block_tables", None)
-    return bt
-
-
-def _is_supported_decode(query, attn_metadata) -> bool:
-    """True for pure decode steps: one query token per sequence (:73-114)."""
+    vLLM's Triton backend names the table ``block_table``; some wrappers say ``block_tables``.
+    vLLM 0.16 pads the query, so ``num_actual_tokens`` (when present) counts the real rows.
+    """
     if attn_metadata is None or query.ndim != 3:
-        return False
-    seq_lens = getattr(attn_metadata, "seq_lens", None)
-    block_table = _get_block_table(attn_metadata)
-    if seq_lens is None or block_table is None or block_table.ndim != 2:
-        return False
-    batch = int(seq_lens.numel())
-    if batch <= 0 or block_table.shape[0] != batch:
-        return False
-    num_tokens = getattr(attn_metadata, "num_actual_tokens", None)
-    if num_tokens is None:
-        num_tokens = query.shape[0]
-    if int(num_tokens) != batch:
-        return False
-    max_query_len = getattr(attn_metadata, "max_query_len", None)
-    if max_query_len is not None and int(max_query_len) != 1:
-        return False
-    return True
+        return None
+    lens = getattr(attn_metadata, "seq_lens", None)
+    table = getattr(attn_metadata, "block_table", None)
+    if table is None:
+        table = getattr(attn_metadata, "block_tables", None)
+    if lens is None or table is None or table.ndim != 2:
+        return None
+    batch = lens.numel()
+    if batch == 0 or table.shape[0] != batch:
+        return None
+    rows = getattr(attn_metadata, "num_actual_tokens", None)
+    rows = query.shape[0] if rows is None else int(rows)
+    longest_query = getattr(attn_metadata, "max_query_len", None)
+    if rows != batch or (longest_query is not None and int(longest_query) != 1):
+        return None
+    return DecodeStep(query[:batch], table.contiguous(), lens.contiguous())
 
 
-def _run_int8_attention(layer, query, attn_metadata):
-    """int8_paged_attention on the layer's shadow cache (:117-137)."""
-    shadow = get_layer_cache(layer.layer_name)
-    seq_lens = attn_metadata.seq_lens.contiguous()
-    block_table = _get_block_table(attn_metadata).contiguous()
-    num_tokens = getattr(attn_metadata, "num_actual_tokens", query.shape[0])
-    query = query[: int(num_tokens)]
-    return int8_paged_attention(query, shadow.key_cache, shadow.value_cache, block_table, seq_lens,
-                                shadow.k_scale, shadow.v_scale, quantize_q=False)
+def agreement(test: torch.Tensor, ref: torch.Tensor) -> dict:
+    """Cosine, relative L2 and mean absolute difference of two outputs, in float64."""
+    x = test.detach().double().reshape(-1)
+    y = ref.detach().double().reshape(-1)
+    d = x - y
+    denom = float(x.norm() * y.norm())
+    return {
+        "cosine": float(x @ y) / denom if denom > 0 else 0.0,
+        "rel_l2": float(d.norm()) / max(float(y.norm()), 1e-12),
+        "mae": float(d.abs().mean()) if d.numel() else 0.0,
+    }
+
+
+def _int8_attention(layer_name: str, step: DecodeStep) -> torch.Tensor:
+    cache = get_layer_cache(layer_name)
+    return int8_paged_attention(step.query, cache.key_cache, cache.value_cache, step.block_table,
+                                step.seq_lens, cache.k_scale, cache.v_scale, quantize_q=False)
+
+
+def _require_finite(out: torch.Tensor, layer_name: str, error) -> None:
+    for what, bad in (("NaN", torch.isnan), ("an infinity", torch.isinf)):
+        if bool(bad(out).any()):
+            raise error(f"{layer_name}: the INT8 decode output holds {what}")
+
+
+def _write_rows(output: torch.Tensor, out8: torch.Tensor) -> None:
+    n = out8.shape[0]
+    output[:n].copy_(out8.reshape_as(output[:n]))
+
+
+def _check_mode(mode) -> None:
+    if mode not in MODES:
+        raise ValueError(f"mode must be one of {MODES}, not {mode!r}")
 
 
 def make_patched_forward(original_forward, mode: PatchMode = "shadow", verbose_layer: int = 0,
                          max_compare_calls: int = 8):
-    """The patched forward around ``original_forward`` (:160-321)."""
-    if mode not in ("shadow", "takeover", "int8_only"):
-        raise ValueError(f"Unknown mode: {mode}")
+    """A forward method that routes decode steps as the module docstring describes and calls
+    ``original_forward`` (vLLM's) otherwise.  ``verbose_layer``: the layer index whose first
+    ``max_compare_calls`` comparisons are printed; in "int8_only" mode any value >= 0 also turns
+    on the NaN / infinity check of the INT8 output (RuntimeError)."""
+    _check_mode(mode)
+    watched = f"layers.{verbose_layer}."
 
-    def patched_forward(self, layer, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
-                        kv_cache: torch.Tensor, attn_metadata, output: torch.Tensor,
+    def patched_forward(self, layer, query, key, value, kv_cache, attn_metadata, output,
                         output_scale=None, output_block_scale=None):
-        layer_name = getattr(layer, "layer_name", None)
-        if (layer_name is None or not has_layer_cache(layer_name)
-                or not _is_supported_decode(query, attn_metadata)):
+        name = getattr(layer, "layer_name", None)
+        step = None
+        if name is not None and has_layer_cache(name):
+            step = decode_step_of(query, attn_metadata)
+        if step is None:
             return original_forward(self, layer, query, key, value, kv_cache, attn_metadata,
                                     output, output_scale=output_scale,
                                     output_block_scale=output_block_scale)
-        if mode in ("shadow", "takeover"):
-            bf16_result = original_forward(self, layer, query, key, value, kv_cache,
-                                           attn_metadata, output, output_scale=output_scale,
-                                           output_block_scale=output_block_scale)
-            bf16_out = output.detach().clone().reshape(query.shape[0], query.shape[1],
-                                                       query.shape[2])
-            int8_out = _run_int8_attention(layer, query, attn_metadata)
-            n = int8_out.shape[0]
-            metrics = {
-                "cosine": _cosine(int8_out, bf16_out[:n]),
-                "rel_l2": _relative_l2(int8_out, bf16_out[:n]),
-                "mae": _mae(int8_out, bf16_out[:n]),
-                "batch": int(attn_metadata.seq_lens.numel()),
-                "seq_lens": [int(x) for x in attn_metadata.seq_lens.tolist()],
-                "max_seq_len": int(attn_metadata.seq_lens.max().item()),
-            }
-            count = ATTN_COMPARE_COUNT.get(layer_name, 0)
-            ATTN_COMPARE_COUNT[layer_name] = count + 1
-            ATTN_METRICS.setdefault(layer_name, []).append(metrics)
-            if f"layers.{verbose_layer}." in layer_name and count < max_compare_calls:
-                print(f"[INT8 Attention / {mode}] {layer_name}: cosine={metrics['cosine']:.6f} "
-                      f"relL2={metrics['rel_l2']:.3e} MAE={metrics['mae']:.3e}")
-            if mode == "shadow":
-                return bf16_result
-            # the reference asserts here (vllm_int8_attention_patch.py:297-298)
-            if torch.isnan(int8_out).any() or torch.isinf(int8_out).any():
-                raise AssertionError(f"non-finite INT8 attention output: {layer_name}")
-            output[:n].copy_(int8_out.reshape_as(output[:n]))
+        batch = step.seq_lens.numel()
+        if mode == "int8_only":
+            out8 = _int8_attention(name, step)
+            if verbose_layer >= 0:
+                _require_finite(out8, name, RuntimeError)
+            ATTN_INT8_HITS[name] = ATTN_INT8_HITS.get(name, 0) + 1
+            ATTN_INT8_STATS["last_batch"] = batch
+            ATTN_INT8_STATS["max_batch"] = max(ATTN_INT8_STATS.get("max_batch", 0), batch)
+            _write_rows(output, out8)
             return output
-        int8_out = _run_int8_attention(layer, query, attn_metadata)
-        if verbose_layer >= 0:
-            if torch.isnan(int8_out).any():
-                raise RuntimeError(f"NaN in INT8 attention: {layer_name}")
-            if torch.isinf(int8_out).any():
-                raise RuntimeError(f"Inf in INT8 attention: {layer_name}")
-        ATTN_INT8_HITS[layer_name] = ATTN_INT8_HITS.get(layer_name, 0) + 1
-        batch_now = int(attn_metadata.seq_lens.numel())
-        ATTN_INT8_STATS["last_batch"] = batch_now
-        ATTN_INT8_STATS["max_batch"] = max(ATTN_INT8_STATS.get("max_batch", 0), batch_now)
-        n = int8_out.shape[0]
-        output[:n].copy_(int8_out.reshape_as(output[:n]))
+
+        vllm_result = original_forward(self, layer, query, key, value, kv_cache, attn_metadata,
+                                       output, output_scale=output_scale,
+                                       output_block_scale=output_block_scale)
+        vllm_rows = output.detach().reshape(query.shape)[:batch].clone()
+        out8 = _int8_attention(name, step)
+        record = agreement(out8, vllm_rows)
+        lens = [int(x) for x in step.seq_lens.tolist()]
+        record.update(batch=batch, seq_lens=lens, max_seq_len=max(lens))
+        seen = ATTN_COMPARE_COUNT.get(name, 0)
+        ATTN_COMPARE_COUNT[name] = seen + 1
+        ATTN_METRICS.setdefault(name, []).append(record)
+        if watched in name and seen < max_compare_calls:
+            print(f"[int8kv {mode}] {name} batch={batch} longest={record['max_seq_len']}: "
+                  f"cos {record['cosine']:.6f}, rel-L2 {record['rel_l2']:.3e}, "
+                  f"mean|d| {record['mae']:.3e} vs vLLM")
+        if mode == "shadow":
+            return vllm_result
+        _require_finite(out8, name, AssertionError)
+        _write_rows(output, out8)
         return output
 
     return patched_forward
@@ -143,15 +160,18 @@ def make_patched_forward(original_forward, mode: PatchMode = "shadow", verbose_l
 
 def apply_int8_attention_patch(*, mode: PatchMode = "shadow", verbose_layer: int = 0,
                                max_compare_calls: int = 8) -> None:
-    """Patches TritonAttentionImpl.forward (vllm_int8_attention_patch.py:140-334)."""
+    """Installs the patched forward on vLLM's TritonAttentionImpl (once per process)."""
     global _PATCHED
-    if mode not in ("shadow", "takeover", "int8_only"):
-        raise ValueError(f"Unknown mode: {mode}")
+    _check_mode(mode)
     if _PATCHED:
-        raise RuntimeError("Attention has already been patched in this Python process.")
+        raise RuntimeError("apply_int8_attention_patch(): TritonAttentionImpl.forward is already "
+                           "patched in this process")
     from vllm.v1.attention.backends.triton_attn import TritonAttentionImpl
 
     TritonAttentionImpl.forward = make_patched_forward(TritonAttentionImpl.forward, mode,
                                                        verbose_layer, max_compare_calls)
     _PATCHED = True
-    print(f"INT8 ATTENTION PATCH ENABLED (mode: {mode})")
+    answer = {"shadow": "vLLM's (INT8 compared beside it)",
+              "takeover": "INT8 (vLLM still computed for the comparison)",
+              "int8_only": "INT8 only"}[mode]
+    print(f"[int8kv] decode attention patched, mode {mode}: decode output is {answer}")

@@ -54,10 +54,21 @@ def test_config0(cuda):
 @pytest.mark.parametrize("B", [1, 2, 4, 8])
 @pytest.mark.parametrize("ctx", [512, 1024, 2048, 4096])
 def test_config2_sweep(cuda, B, ctx):
+    """Every config-2 point, INT8 (automatic layout and one range per sequence) and the BF16
+    comparison kernel on the same K/V in a bf16 cache, each against the oracle."""
     c = decode_case([ctx] * B, seed=B * 7 + ctx)
     ref = oracle_int8(c)
     _check(_int8(c, cuda), ref, f"B={B} ctx={ctx} auto")
     _check(_int8(c, cuda, num_splits=1), ref, f"B={B} ctx={ctx} single-pass")
+    kc, vc = bf16_caches(c)
+    ref16 = O.paged_attention_ref(c.query.float().numpy(), kc.float().numpy(), vc.float().numpy(),
+                                  c.block_tables.numpy(), c.seq_lens.numpy())
+    for splits in (None, 1):
+        out = int8kv.bf16_paged_attention(c.query.to(cuda), kc.to(cuda), vc.to(cuda),
+                                          c.block_tables.to(cuda), c.seq_lens.to(cuda),
+                                          num_splits=splits)
+        torch.cuda.synchronize()
+        _check(out, ref16, f"B={B} ctx={ctx} bf16 splits={splits}")
 
 
 @pytest.mark.parametrize("lens", [

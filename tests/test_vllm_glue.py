@@ -41,8 +41,8 @@ def test_static_scales_file_round_trip(tmp_path):
         static_scales.load_static_scales(str(bad))
 
 
-def test_infer_native_page_dims():
-    f = shadow_patch._infer_native_page_dims
+def test_native_page_geometry():
+    f = shadow_patch.native_page_geometry
     assert f(torch.empty(10, 4, 16, 256), 4) == (10, 16)  # v0.26 fused
     assert f(torch.empty(10, 2, 16, 4, 128), 4) == (10, 16)  # v0.16 split
     assert f(torch.empty(2, 10, 16, 4, 128), 4) == (10, 16)  # older split
@@ -60,7 +60,10 @@ def _meta(B, num_tokens=None, max_query_len=1, name="block_table"):
 
 def test_decode_gate():
     q = torch.zeros(4, 28, 128)
-    gate = attn_patch._is_supported_decode
+
+    def gate(query, meta):
+        return attn_patch.decode_step_of(query, meta) is not None
+
     assert gate(q, _meta(4))
     assert gate(q, _meta(4, name="block_tables"))  # wrapper naming
     assert not gate(q, _meta(4, num_tokens=9))  # prefill tokens
@@ -69,6 +72,36 @@ def test_decode_gate():
     assert not gate(q, None)
     padded = torch.zeros(8, 28, 128)  # vLLM 0.16 pads the query; num_actual_tokens decides
     assert gate(padded, _meta(4))
+    step = attn_patch.decode_step_of(padded, _meta(4))
+    assert step.query.shape == (4, 28, 128) and step.block_table.shape == (4, 3)
+    assert step.seq_lens.is_contiguous() and step.block_table.is_contiguous()
+    assert not gate(q, _meta(0))  # empty batch
+
+
+def test_agreement_metrics():
+    a = torch.tensor([[1.0, 2.0], [3.0, 4.0]])
+    m = attn_patch.agreement(a, a)
+    assert m == {"cosine": 1.0, "rel_l2": 0.0, "mae": 0.0}
+    m = attn_patch.agreement(-a, a)
+    assert m["cosine"] == -1.0 and m["rel_l2"] == 2.0 and m["mae"] == 5.0
+
+
+def test_backend_registration_class():
+    """INT8PagedAttentionBackend (vllm_int8/vllm_int8_attention_backend.py:81-87): the name and
+    the implementation class a caller registers with vLLM."""
+    import importlib
+
+    with fake_vllm.installed() as mods:
+        import int8kv.vllm_int8.vllm_int8_attention_backend as backend
+
+        backend = importlib.reload(backend)
+        assert issubclass(backend.INT8PagedAttentionBackend,
+                          mods["vllm.v1.attention.backend"].AttentionBackend)
+        assert backend.INT8PagedAttentionBackend.get_name() == "INT8_PAGED_ATTENTION"
+        impl_cls = backend.INT8PagedAttentionBackend.get_impl_cls()
+        assert impl_cls is backend.INT8PagedAttentionImpl
+        impl = impl_cls("model.layers.3.self_attn.attn", 28, 128, 4, 128 ** -0.5)
+        assert (impl.num_heads, impl.head_size, impl.num_kv_heads) == (28, 128, 4)
 
 
 def test_adapter_quantize_per_head():
