@@ -54,6 +54,7 @@ enum int8kv_dtype {
 #define INT8KV_E_SHAPE (-3)     /* unsupported or inconsistent size */
 #define INT8KV_E_STRIDE (-4)    /* innermost stride != 1 or rows not 16-byte aligned */
 #define INT8KV_E_WORKSPACE (-5) /* workspace missing or smaller than required */
+#define INT8KV_E_SCRATCH (-6)   /* needed scratch exceeds INT8KV_DECODE_SCRATCH_BYTES */
 
 /* Flags of int8kv_paged_decode. */
 #define INT8KV_DECODE_MAIN 1u   /* run the range decode kernel */
@@ -196,6 +197,38 @@ int int8kv_paged_decode(const void* query, int query_dtype, int64_t batch, int32
                         const float* k_scale, const float* v_scale, float sm_scale, void* out,
                         const int64_t out_strides[3], void* workspace, size_t workspace_bytes,
                         int32_t num_ranges, int32_t min_tiles, uint32_t flags, void* stream);
+
+/*
+ * int8kv_paged_decode without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP-graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference: it is the same operation as int8kv_paged_decode (same
+ * arguments, kernels and results) with the split partials kept in a fixed array of
+ * INT8KV_DECODE_SCRATCH_BYTES per GPU inside the library (held from the GPU's first call until
+ * the process ends) instead of a caller's workspace.  It calls no allocator.
+ *
+ *   - The array belongs to the current device (hipGetDevice); `stream` must be on it.
+ *   - A call whose partials need more than INT8KV_DECODE_SCRATCH_BYTES
+ *     (int8kv_decode_workspace_bytes(...) > INT8KV_DECODE_SCRATCH_BYTES) returns
+ *     INT8KV_E_SCRATCH and launches nothing.  16 MiB holds the automatic range count for up to
+ *     60 query heads at head_dim 128.
+ *   - Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams,
+ *     two threads) race and must be serialised by the caller.  The array keeps the last call's
+ *     contents; the kernels need no clearing between calls.
+ */
+#define INT8KV_DECODE_SCRATCH_BYTES ((size_t)16 << 20)
+int int8kv_paged_decode_noalloc(const void* query, int query_dtype, int64_t batch,
+                                int32_t num_q_heads, int32_t head_dim,
+                                const int64_t query_strides[3], const void* key_cache,
+                                const void* value_cache, int cache_dtype, int64_t num_blocks,
+                                int32_t block_size, int32_t num_kv_heads,
+                                const int64_t key_cache_strides[4],
+                                const int64_t value_cache_strides[4], const void* block_tables,
+                                int table_dtype, int64_t table_width,
+                                const int64_t table_strides[2], const void* seq_lens,
+                                int seq_lens_dtype, const float* k_scale, const float* v_scale,
+                                float sm_scale, void* out, const int64_t out_strides[3],
+                                int32_t num_ranges, int32_t min_tiles, uint32_t flags,
+                                void* stream);
 
 /* Library version string, e.g. "int8kv 0.1.0 gfx950". */
 const char* int8kv_version(void);

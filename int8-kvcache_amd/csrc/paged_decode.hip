@@ -50,7 +50,9 @@
 //   * A running max is only moved when a tile's max exceeds it by more than 8 (log2 units), so
 //     most tiles skip the accumulator rescale; probabilities are then <= 2^8 (fits fp16/bf16).
 
+#include <atomic>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 #include "int8kv_common.h"
@@ -1378,7 +1380,48 @@ extern "C" size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num
   return workspace_bytes(num_q_heads, num_ranges, head_dim);
 }
 
-extern "C" int int8kv_paged_decode(
+// ------------------------------------------------------------------ no-allocation scratch
+// Split partials of int8kv_paged_decode_noalloc: a fixed array in the code object, so a call
+// allocates nothing.  Each GPU the library runs on holds its own copy (kScratchBytes) until the
+// process ends.  In host code `scratch` names a host-side stand-in, not device memory: its
+// device address is looked up once per device with hipGetSymbolAddress and only that address is
+// ever passed to a kernel.  Every call on a GPU shares that GPU's array (calls that overlap on one
+// GPU race); the decode kernel writes every partial record the merge kernel reads, so nothing
+// needs clearing between calls.
+constexpr size_t kScratchBytes = INT8KV_DECODE_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxScratchDevices];
+std::mutex g_scratch_lookup;
+
+// Device address of the current device's scratch array (looked up on its first use there).
+int current_scratch(void** addr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return INT8KV_E_SCRATCH;
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_lookup);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return (int)e;
+      if (p == nullptr) return INT8KV_E_SCRATCH;
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *addr = p;
+  return INT8KV_OK;
+}
+
+// Shared body of int8kv_paged_decode and int8kv_paged_decode_noalloc.  from_scratch: take the
+// current device's scratch array as the workspace (after every argument check, so a rejected
+// call touches no device).
+int decode_entry(
     const void* query, int query_dtype, int64_t batch, int32_t num_q_heads, int32_t head_dim,
     const int64_t query_strides[3], const void* key_cache, const void* value_cache,
     int cache_dtype, int64_t num_blocks, int32_t block_size, int32_t num_kv_heads,
@@ -1387,7 +1430,7 @@ extern "C" int int8kv_paged_decode(
     const void* seq_lens, int seq_lens_dtype, const float* k_scale, const float* v_scale,
     float sm_scale, void* out, const int64_t out_strides[3], void* workspace,
     size_t workspace_bytes_given, int32_t num_ranges, int32_t min_tiles, uint32_t flags,
-    void* stream) {
+    void* stream, bool from_scratch) {
   if (!query_strides || !key_cache_strides || !value_cache_strides || !table_strides ||
       !out_strides)
     return INT8KV_E_NULL;
@@ -1426,6 +1469,12 @@ extern "C" int int8kv_paged_decode(
   if (num_ranges == 0) num_ranges = auto_ranges(num_kv_heads, cus);
   if (min_tiles == 0) min_tiles = auto_min_tiles(batch, table_width, block_size, num_ranges);
   const size_t need = workspace_bytes(num_q_heads, num_ranges, head_dim);
+  if (from_scratch) {
+    if (need > kScratchBytes) return INT8KV_E_SCRATCH;
+    const int st = current_scratch(&workspace);
+    if (st != INT8KV_OK) return st;
+    workspace_bytes_given = kScratchBytes;
+  }
   if (workspace == nullptr || workspace_bytes_given < need || ((uintptr_t)workspace % 16) != 0)
     return INT8KV_E_WORKSPACE;
 
@@ -1522,4 +1571,41 @@ extern "C" int int8kv_paged_decode(
     default:
       return launch_q<kF16>(a, query_dtype, flags, nt, s);
   }
+}
+
+}  // namespace
+
+extern "C" int int8kv_paged_decode(
+    const void* query, int query_dtype, int64_t batch, int32_t num_q_heads, int32_t head_dim,
+    const int64_t query_strides[3], const void* key_cache, const void* value_cache,
+    int cache_dtype, int64_t num_blocks, int32_t block_size, int32_t num_kv_heads,
+    const int64_t key_cache_strides[4], const int64_t value_cache_strides[4],
+    const void* block_tables, int table_dtype, int64_t table_width, const int64_t table_strides[2],
+    const void* seq_lens, int seq_lens_dtype, const float* k_scale, const float* v_scale,
+    float sm_scale, void* out, const int64_t out_strides[3], void* workspace,
+    size_t workspace_bytes_given, int32_t num_ranges, int32_t min_tiles, uint32_t flags,
+    void* stream) {
+  return decode_entry(query, query_dtype, batch, num_q_heads, head_dim, query_strides, key_cache,
+                      value_cache, cache_dtype, num_blocks, block_size, num_kv_heads,
+                      key_cache_strides, value_cache_strides, block_tables, table_dtype,
+                      table_width, table_strides, seq_lens, seq_lens_dtype, k_scale, v_scale,
+                      sm_scale, out, out_strides, workspace, workspace_bytes_given, num_ranges,
+                      min_tiles, flags, stream, false);
+}
+
+extern "C" int int8kv_paged_decode_noalloc(
+    const void* query, int query_dtype, int64_t batch, int32_t num_q_heads, int32_t head_dim,
+    const int64_t query_strides[3], const void* key_cache, const void* value_cache,
+    int cache_dtype, int64_t num_blocks, int32_t block_size, int32_t num_kv_heads,
+    const int64_t key_cache_strides[4], const int64_t value_cache_strides[4],
+    const void* block_tables, int table_dtype, int64_t table_width, const int64_t table_strides[2],
+    const void* seq_lens, int seq_lens_dtype, const float* k_scale, const float* v_scale,
+    float sm_scale, void* out, const int64_t out_strides[3], int32_t num_ranges,
+    int32_t min_tiles, uint32_t flags, void* stream) {
+  return decode_entry(query, query_dtype, batch, num_q_heads, head_dim, query_strides, key_cache,
+                      value_cache, cache_dtype, num_blocks, block_size, num_kv_heads,
+                      key_cache_strides, value_cache_strides, block_tables, table_dtype,
+                      table_width, table_strides, seq_lens, seq_lens_dtype, k_scale, v_scale,
+                      sm_scale, out, out_strides, nullptr, 0, num_ranges, min_tiles, flags, stream,
+                      true);
 }

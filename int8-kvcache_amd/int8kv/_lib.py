@@ -34,6 +34,7 @@ ERRORS = {
     -3: "INT8KV_E_SHAPE (unsupported or inconsistent size)",
     -4: "INT8KV_E_STRIDE (innermost stride != 1 or rows not 16-byte aligned)",
     -5: "INT8KV_E_WORKSPACE (workspace missing or too small)",
+    -6: "INT8KV_E_SCRATCH (the call's split partials exceed the library's fixed scratch array)",
 }
 
 _c_i64p = ctypes.POINTER(ctypes.c_int64)
@@ -75,6 +76,12 @@ def load() -> ctypes.CDLL:
         _vp, ctypes.c_int, i64, i32, i32, _c_i64p, _vp, _vp, ctypes.c_int, i64, i32, i32,
         _c_i64p, _c_i64p, _vp, ctypes.c_int, i64, _c_i64p, _vp, ctypes.c_int, _vp, _vp, f32,
         _vp, _c_i64p, _vp, sz, i32, i32, u32, _vp,
+    ]
+    lib.int8kv_paged_decode_noalloc.restype = ctypes.c_int
+    lib.int8kv_paged_decode_noalloc.argtypes = [
+        _vp, ctypes.c_int, i64, i32, i32, _c_i64p, _vp, _vp, ctypes.c_int, i64, i32, i32,
+        _c_i64p, _c_i64p, _vp, ctypes.c_int, i64, _c_i64p, _vp, ctypes.c_int, _vp, _vp, f32,
+        _vp, _c_i64p, i32, i32, u32, _vp,
     ]
     lib.int8kv_add_rms_norm.restype = ctypes.c_int
     lib.int8kv_add_rms_norm.argtypes = [_vp, _vp, _vp, _vp, i64, i32, i64, i64, i64, f32, _vp]

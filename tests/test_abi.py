@@ -40,6 +40,7 @@ def test_header_declares_expected_entry_points():
         "int8kv_decode_workspace_bytes",
         "int8kv_dynamic_cache_write",
         "int8kv_paged_decode",
+        "int8kv_paged_decode_noalloc",
         "int8kv_rotary_cache_write",
         "int8kv_rotary_inplace",
         "int8kv_silu_mul",
@@ -111,6 +112,32 @@ def test_decode_rejects_bad_arguments_without_launching(lib):
     assert _decode_call(lib, wsb=1000) == -5
     assert _decode_call(lib, ws=24) == -5
     assert _decode_call(lib, batch=0) == 0  # nothing to do
+
+
+def test_noalloc_decode_rejects_without_touching_the_device(lib):
+    """int8kv_paged_decode_noalloc validates like int8kv_paged_decode, then refuses a call whose
+    partials exceed the fixed scratch array (INT8KV_E_SCRATCH) -- before any device call."""
+
+    def call(**over):
+        args = dict(query=16, query_dtype=2, batch=1, num_q_heads=28, head_dim=128,
+                    qs=(ctypes.c_int64 * 3)(28 * 128, 128, 1), kc=16, vc=16, cache_dtype=3,
+                    num_blocks=8, block_size=16, num_kv_heads=4,
+                    kcs=(ctypes.c_int64 * 4)(16 * 4 * 128, 4 * 128, 128, 1),
+                    vcs=(ctypes.c_int64 * 4)(16 * 4 * 128, 4 * 128, 128, 1), bt=16,
+                    table_dtype=4, width=8, bts=(ctypes.c_int64 * 2)(8, 1), sl=16, sl_dtype=4,
+                    ks=16, vs=16, sm=0.088, out=16, os=(ctypes.c_int64 * 3)(28 * 128, 128, 1),
+                    ranges=0, min_tiles=0, flags=3, stream=None)
+        args.update(over)
+        return lib.int8kv_paged_decode_noalloc(*args.values())
+
+    limit = 16 << 20  # INT8KV_DECODE_SCRATCH_BYTES
+    per_range = lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 1)
+    too_many = limit // per_range + 1
+    assert call(ranges=too_many) == -6
+    assert call(ranges=too_many, num_q_heads=56) == -6
+    assert call(query_dtype=3) == -2 and call(head_dim=96) == -3 and call(query=None) == -1
+    assert call(query=24) == -4
+    assert call(batch=0) == 0
 
 
 def test_write_rejects_bad_arguments_without_launching(lib):

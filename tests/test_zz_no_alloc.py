@@ -1,0 +1,89 @@
+"""The no-allocation decode entry point, int8kv_paged_decode_noalloc, called through the C ABI.
+
+It must give exactly what int8kv_paged_decode gives with a caller's workspace (same kernels,
+same plan, partials in the library's fixed scratch array instead).  Two calls in a row on the
+same GPU, the second with a smaller input, both bit-identical to the workspace entry point and
+within the oracle bar; then the INT8 x BF16-cache and forced-range variants.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from cases import bf16_caches, decode_case, oracle_int8, to_dev
+from conftest import MAX_ABS, MIN_COS, metrics
+from int8kv import _decode, _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def _noalloc(q, kc, vc, bt, sl, ks, vs, out, num_ranges=0, flags=_lib.DECODE_ALL):
+    lib = _lib.load()
+    B, Hq, D = q.shape
+    nb, bs, hkv, _ = kc.shape
+    status = lib.int8kv_paged_decode_noalloc(
+        q.data_ptr(), _lib.DTYPE_CODE[q.dtype], B, Hq, D, _lib.strides(q), kc.data_ptr(),
+        vc.data_ptr(), _lib.DTYPE_CODE[kc.dtype], nb, bs, hkv, _lib.strides(kc), _lib.strides(vc),
+        bt.data_ptr(), _lib.DTYPE_CODE[bt.dtype], bt.shape[1], _lib.strides(bt), sl.data_ptr(),
+        _lib.DTYPE_CODE[sl.dtype], ks.data_ptr() if ks is not None else None,
+        vs.data_ptr() if vs is not None else None, 1.0 / math.sqrt(D), out.data_ptr(),
+        _lib.strides(out), num_ranges, 0, flags, _lib.stream_handle(q.device))
+    _lib.check(status, "int8kv_paged_decode_noalloc")
+    return out
+
+
+def _with_workspace(q, kc, vc, bt, sl, ks, vs, num_ranges=0):
+    out = torch.full_like(q, float("nan"))
+    need = _lib.load().int8kv_decode_workspace_bytes(q.shape[1], kc.shape[2], q.shape[2],
+                                                     kc.shape[1], num_ranges)
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+    return _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, out, num_ranges, workspace=ws)
+
+
+# (lengths, seed, forced range count): the first call is the larger one.
+CALLS = [
+    ([4096, 1, 777, 2048, 3000, 15, 4096, 1500], 31, 0),
+    ([300, 3, 150], 32, 6),
+]
+
+
+def test_two_calls_match_the_workspace_entry_point(cuda):
+    for lens, seed, ranges in CALLS:
+        print(f"noalloc: lens={lens} ranges={ranges}", flush=True)
+        c = decode_case(lens, seed=seed)
+        q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+        want = _with_workspace(q, kc, vc, bt, sl, ks, vs, ranges)
+        got = _noalloc(q, kc, vc, bt, sl, ks, vs, torch.full_like(q, float("nan")), ranges)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"lens={lens}: outputs differ from int8kv_paged_decode"
+        err, cos, _ = metrics(got.float().cpu().numpy(), oracle_int8(c))
+        assert err <= MAX_ABS and cos >= MIN_COS, (lens, err, cos)
+
+
+def test_bf16_cache_and_paired_ranges(cuda):
+    c = decode_case([4096, 1, 2500, 4096, 333, 4096, 2048, 4000], seed=33)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    for ranges in (512, 0):  # 512: two ranges per workgroup (INT8); 0: automatic
+        want = _with_workspace(q, kc, vc, bt, sl, ks, vs, ranges)
+        got = _noalloc(q, kc, vc, bt, sl, ks, vs, torch.full_like(q, float("nan")), ranges)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"int8, ranges={ranges}"
+    k16, v16 = (t.to(cuda) for t in bf16_caches(c))
+    want = _with_workspace(q, k16, v16, bt, sl, None, None)
+    got = _noalloc(q, k16, v16, bt, sl, None, None, torch.full_like(q, float("nan")))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), "bf16 cache"
+
+
+def test_oversized_request_is_refused(cuda):
+    c = decode_case([64], seed=34)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    out = torch.zeros_like(q)
+    per_range = _lib.load().int8kv_decode_workspace_bytes(28, 4, 128, 16, 1)
+    with pytest.raises(_lib.Int8KVError, match="INT8KV_E_SCRATCH"):
+        _noalloc(q, kc, vc, bt, sl, ks, vs, out, (16 << 20) // per_range + 1)
+    torch.cuda.synchronize()
+    assert not out.any()  # nothing was launched
