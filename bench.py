@@ -191,10 +191,13 @@ def settle(fn, batch: int = 20, min_ms: float = 100.0, tol: float = 0.01,
             "last_batch_us": round(means[-1] * 1e3, 2)}
 
 
-def write_legs(dev) -> dict:
-    """The cache writes beside the headline (config 1 and an HBM-sized write), each with a
-    same-mix ceiling: torch's bf16 -> int8 dense conversion of the same number of elements (the
-    write's bytes read and written, without the slot scatter).  Config 1 (16,384 tokens + 512
+def write_legs(dev, cfg1_graph: bool = True) -> dict:
+    """The cache writes beside the headline (config 1 and an HBM-sized write), each beside two
+    plain streaming kernels over the same bytes, without the slot scatter: a device-to-device
+    copy (hipMemcpyAsync) of the same byte count (half read, half written), and an elementwise
+    kernel with the write's 2:1 read/write mix (torch.ne on the bf16 K/V into a bool tensor: 2
+    bytes read, 1 written per element).  The faster of the two is the copy ceiling the write is
+    compared with.  Config 1 (16,384 tokens + 512
     padding slots into a 2048-block cache, ~50 MB) fits the 256 MB Infinity Cache, so its rate is
     cache-resident; it is timed as HIP-graph replays (the host's launch cost exceeds the kernel).
     The 262,144-token write (805 MB moved) streams from HBM and is timed with events around
@@ -221,8 +224,11 @@ def write_legs(dev) -> dict:
         vc = torch.zeros_like(kc)
         ksc = torch.zeros(nb, 16, 4, dtype=torch.float32, device=dev)
         vsc = torch.zeros_like(ksc)
-        kd = torch.empty(k.shape, dtype=torch.int8, device=dev)
+        kd = torch.empty(k.shape, dtype=torch.bool, device=dev)
         vd = torch.empty_like(kd)
+        moved = (n_tok + n_pad) * 4 * 128 * 6  # K/V bf16 read + int8 written, every row
+        src = torch.empty(moved // 2, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
 
         def static():
             int8kv.int8_kv_cache_write(k, v, kc, vc, sd, ks_d, vs_d)
@@ -230,38 +236,41 @@ def write_legs(dev) -> dict:
         def dynamic():
             cache_ops.reshape_and_cache_int8(k, v, kc, vc, ksc, vsc, sd)
 
-        def ceiling():
-            kd.copy_(k)
-            vd.copy_(v)
+        def mix21():
+            torch.ne(k, 0, out=kd)
+            torch.ne(v, 0, out=vd)
+
+        def copy():
+            dst.copy_(src)
 
         if graph:
             timer = time_graph
         else:
             settle(static, batch=10, min_ms=50.0)
             timer = lambda fn: time_events(fn, 40, 10)  # noqa: E731
-        ms_s, ms_d, ms_c = timer(static), timer(dynamic), timer(ceiling)
+        ms_s, ms_d = timer(static), timer(dynamic)
+        ms_m, ms_c = timer(mix21), timer(copy)
         elems = n_tok * 4 * 128
         sbytes = elems * (2 + 2 + 1 + 1) + (n_tok + n_pad) * 8 + 2 * 4 * 4
         dbytes = sbytes - 2 * 4 * 4 + n_tok * 4 * 4 * 2
-        cbytes = (n_tok + n_pad) * 4 * 128 * 6
+        ceiling = moved / min(ms_m, ms_c) / 1e6
         out = {"tokens": n_tok, "padding_slots": n_pad, "cache_blocks": nb,
                "static_us": round(ms_s * 1e3, 2), "static_bytes": sbytes,
                "static_GBps": round(sbytes / ms_s / 1e6, 1),
                "dynamic_us": round(ms_d * 1e3, 2), "dynamic_bytes": dbytes,
                "dynamic_GBps": round(dbytes / ms_d / 1e6, 1),
-               "ceiling_convert_us": round(ms_c * 1e3, 2),
-               "ceiling_convert_GBps": round(cbytes / ms_c / 1e6, 1),
-               "static_frac_of_ceiling": round(ms_c / ms_s, 3),
+               "copy_same_bytes_us": round(ms_c * 1e3, 2),
+               "copy_same_bytes_GBps": round(moved / ms_c / 1e6, 1),
+               "mix_2to1_elementwise_us": round(ms_m * 1e3, 2),
+               "mix_2to1_elementwise_GBps": round(moved / ms_m / 1e6, 1),
+               "static_frac_of_copy_ceiling": round(sbytes / ms_s / 1e6 / ceiling, 3),
                "timing": "HIP-graph replays" if graph else "HIP events, back-to-back launches"}
         return out
 
-    res["cfg1"] = leg(16384, 512, 2048, g, graph=True)
-    log(f"cfg1 write: static {res['cfg1']['static_us']} us ({res['cfg1']['static_GBps']} GB/s), "
-        f"dynamic {res['cfg1']['dynamic_us']} us, same-mix ceiling {res['cfg1']['ceiling_convert_us']} us")
+    res["cfg1"] = leg(16384, 512, 2048, g, graph=cfg1_graph)
+    log(f"cfg1 write: {json.dumps(res['cfg1'])}")
     res["hbm_262k"] = leg(262144, 0, 32768, torch.Generator().manual_seed(13), graph=False)
-    log(f"262k write: static {res['hbm_262k']['static_us']} us ({res['hbm_262k']['static_GBps']} GB/s), "
-        f"dynamic {res['hbm_262k']['dynamic_us']} us, same-mix ceiling "
-        f"{res['hbm_262k']['ceiling_convert_us']} us ({res['hbm_262k']['ceiling_convert_GBps']} GB/s)")
+    log(f"262k write: {json.dumps(res['hbm_262k'])}")
     torch.cuda.empty_cache()
     return res
 
@@ -506,6 +515,20 @@ def tpot_config4(dev, out_path: str | None, batch: int = 32, context: int = 8192
     return res
 
 
+def calibrate_copy(dev) -> None:
+    """Three plain 1 GiB device-to-device copies: each reads and writes exactly 1,048,576 KiB,
+    which scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -518,6 +541,9 @@ def main() -> int:
                     help="seconds of one CPU-baseline pass (the sample is sized to it)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-writes", action="store_true", help="skip the cache-write legs")
+    ap.add_argument("--writes-only", action="store_true",
+                    help="run only the cache-write legs (config 1 eagerly, not as graph replays: "
+                         "for rocprofv3 counter passes) and print their JSON")
     ap.add_argument("--sweep", metavar="JSON", default=None,
                     help="also measure the config-2 decode sweep, written to JSON")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -555,6 +581,12 @@ def main() -> int:
     if args.tpot_only:
         tpot_config4(dev, args.tpot, *tpot_args, gemm_tuning=args.gemm_tuning,
                      tuning_file=args.gemm_tuning_file)
+        return 0
+    if args.writes_only:
+        res = write_legs(dev, cfg1_graph=False)
+        if args.calibrate_copy:
+            calibrate_copy(dev)
+        print(json.dumps({"writes": res}), flush=True)
         return 0
     log("building workload (B=64, ctx ~ U[1, 32768]) ...")
     w = build_workload(dev, seed=args.seed)
@@ -595,21 +627,29 @@ def main() -> int:
     ms16 = time_loop(bf16_call, args.steps, args.warmup)
     ms_q = time_loop(lambda: int8kv.int8_paged_attention(w["q"], w["kc"], w["vc"], w["bt"], w["sl"], w["ks"],
                                                          w["vs"], quantize_q=True), args.steps, args.warmup)
-    # Host cost of one eager call: wall time of back-to-back calls whose device work is tiny
-    # compared with it would need another workload; here the host's own time per call is read
-    # as the wall time of enqueueing `steps` calls without waiting (the device runs behind).
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        int8_call()
-    host_us = (time.perf_counter() - t0) * 1e6 / args.steps
-    torch.cuda.synchronize()
+    # Host cost of one eager call: the wall time of enqueueing `steps` calls without waiting (each
+    # call's ~190 us of device work keeps the device behind the host), through the torch
+    # extension (the default path) and through the ctypes binding of the same C ABI.
+    from int8kv import _ext
+
+    def enqueue_us():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            int8_call()
+        us = (time.perf_counter() - t0) * 1e6 / args.steps
+        torch.cuda.synchronize()
+        return us
+
+    host_us = enqueue_us()
+    with _ext.use_ctypes():
+        host_us_ctypes = enqueue_us()
     value = nbytes8 / (ms * 1e-3) / 1e9
     achieved = nbytes8 / (ms_main * 1e-3) / 1e9
     log(f"int8 op: {ms * 1e3:.1f} us/call ({value:.0f} GB/s); decode kernel {ms_main * 1e3:.1f} us "
         f"({achieved:.0f} GB/s); merge kernel {ms_merge * 1e3:.1f} us; bf16 op {ms16 * 1e3:.1f} us "
         f"({nbytes16 / (ms16 * 1e-3) / 1e9:.0f} GB/s); int8 quantize_q op {ms_q * 1e3:.1f} us; "
-        f"host enqueue {host_us:.1f} us/call")
+        f"host enqueue {host_us:.1f} us/call (ctypes path {host_us_ctypes:.1f})")
 
     result = {
         "metric": METRIC,
@@ -641,6 +681,8 @@ def main() -> int:
             "int8_quantize_q_us_per_call": round(ms_q * 1e3, 2),
             "frac_of_hbm_peak_whole_call": round(value / HBM_PEAK_GBS, 4),
             "host_enqueue_us_per_call": round(host_us, 2),
+            "host_enqueue_us_per_call_ctypes": round(host_us_ctypes, 2),
+            "host_path": "torch extension" if _ext.module() is not None else "ctypes",
             "settle": st,
         },
         "roofline": {
@@ -674,13 +716,7 @@ def main() -> int:
         tpot_config4(dev, args.tpot, *tpot_args, gemm_tuning=args.gemm_tuning,
                      tuning_file=args.gemm_tuning_file)
     if args.calibrate_copy:
-        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        calibrate_copy(dev)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -9,11 +9,17 @@
 //
 // Mapping (wide kernels, head_dim % 16 == 0 and 16-byte aligned cache rows): grid.y = kv head,
 // one lane owns 16 consecutive head_dim elements of one (token, head) row of both K and V --
-// 32-byte source loads, 16-byte cache stores, 8 lanes per 128-element row.  The slot and the
-// K/V loads are all issued before the slot is tested.  Sources are read and caches written
-// with the non-temporal hint: both are streamed once (262k-token write on MI355X: 193 ->
-// 166 us, 4.2 -> 4.9 TB/s).  Other layouts (head_dim % 16 == 8, or cache rows only 8-byte
-// aligned) use the narrow kernels: one lane per 8 elements, 8-byte stores.
+// 32-byte source loads, 16-byte cache stores, 8 lanes per 128-element row.  The slot is read
+// first, so skipped rows cost no source bytes.  Sources are read and caches written with the
+// non-temporal hint: both are streamed once (262k-token write on MI355X: 193 -> 166 us, 4.2 ->
+// 4.9 TB/s).  Other layouts (head_dim % 16 == 8, or cache rows only 8-byte aligned) use the
+// narrow kernels: one lane per 8 elements, 8-byte stores.
+//
+// The quotient x / scale is not divided per element: quantise() (int8kv_common.h) multiplies by
+// the correctly rounded reciprocal and divides only the elements whose quotient lies within
+// 2^-20 relative of a half-integer, which provably gives the divide's codes (the divide is ~10
+// VALU instructions per element and made the write VALU-bound: 262,144 tokens 158 -> 155.6 us
+// static, 197 -> 175.6 us dynamic; 16,384 tokens 14.6 -> 12.1 us).
 
 #include "int8kv_common.h"
 
@@ -39,19 +45,6 @@ struct WriteArgs {
   int32_t slots_is64;
 };
 
-__device__ __forceinline__ uint32_t quant4(const float* x, float s) {
-  uint32_t w = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    // x / s is the correctly rounded IEEE quotient (hipcc's default fp32 division lowering,
-    // not a reciprocal multiply); rintf is round-half-to-even.
-    float q = rintf(x[i] / s);
-    q = fminf(fmaxf(q, -127.0f), 127.0f);
-    w |= ((uint32_t)((int32_t)q) & 0xffu) << (8 * i);
-  }
-  return w;
-}
-
 template <int SRC>
 __global__ __launch_bounds__(256) void cache_write_kernel(WriteArgs a) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -68,18 +61,17 @@ __global__ __launch_bounds__(256) void cache_write_kernel(WriteArgs a) {
   const int64_t off = slot - blk * a.block_size;
 
   constexpr int esize = SRC == kF32 ? 4 : 2;
-  const float ks = fmaxf(a.k_scale[h], 1e-6f);
-  const float vs = fmaxf(a.v_scale[h], 1e-6f);
+  const QuantScale ks = quant_scale(fmaxf(a.k_scale[h], 1e-6f));
+  const QuantScale vs = quant_scale(fmaxf(a.v_scale[h], 1e-6f));
 
   float x[8];
+  uint32_t w[2];
   load8_f32<SRC>(a.key + (t * a.k_st + h * a.k_sh + 8 * dv) * esize, x);
-  u32x2 kq;
-  kq[0] = quant4(x, ks);
-  kq[1] = quant4(x + 4, ks);
+  quantise<8, false>(x, ks, w);
+  const u32x2 kq = {w[0], w[1]};
   load8_f32<SRC>(a.value + (t * a.v_st + h * a.v_sh + 8 * dv) * esize, x);
-  u32x2 vq;
-  vq[0] = quant4(x, vs);
-  vq[1] = quant4(x + 4, vs);
+  quantise<8, false>(x, vs, w);
+  const u32x2 vq = {w[0], w[1]};
 
   *reinterpret_cast<u32x2*>(a.kc + blk * a.kc_sb + off * a.kc_ss + h * a.kc_sh + 8 * dv) = kq;
   *reinterpret_cast<u32x2*>(a.vc + blk * a.vc_sb + off * a.vc_ss + h * a.vc_sh + 8 * dv) = vq;
@@ -133,21 +125,23 @@ __global__ __launch_bounds__(256) void cache_write16_kernel(WriteArgs a) {
   if ((int64_t)t >= a.num_tokens) return;
   const int dv = (int)(gid - t * lpr);
   constexpr int esize = SRC == kF32 ? 4 : 2;
+  // The slot first: a skipped row (slot < 0, or past the cache) loads no source bytes.  The
+  // extra dependent load is hidden by the other resident waves (MI355X: 262,144-token write
+  // 155.6 us either way).
   const int64_t slot = load_index(a.slots, t, a.slots_is64);
+  if (slot < 0 || slot >= a.capacity) return;
   float x[16], y[16];
   load16_f32<SRC>(a.key + ((int64_t)t * a.k_st + h * a.k_sh + 16 * dv) * esize, x);
   load16_f32<SRC>(a.value + ((int64_t)t * a.v_st + h * a.v_sh + 16 * dv) * esize, y);
-  const float ks = fmaxf(a.k_scale[h], 1e-6f);
-  const float vs = fmaxf(a.v_scale[h], 1e-6f);
-  if (slot < 0 || slot >= a.capacity) return;
+  const QuantScale ks = quant_scale(fmaxf(a.k_scale[h], 1e-6f));
+  const QuantScale vs = quant_scale(fmaxf(a.v_scale[h], 1e-6f));
   const int64_t blk = slot / a.block_size;
   const int64_t off = slot - blk * a.block_size;
-  u32x4 kq, vq;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    kq[i] = quant4(x + 4 * i, ks);
-    vq[i] = quant4(y + 4 * i, vs);
-  }
+  uint32_t wk[4], wv[4];
+  quantise<16, false>(x, ks, wk);
+  quantise<16, false>(y, vs, wv);
+  const u32x4 kq = {wk[0], wk[1], wk[2], wk[3]};
+  const u32x4 vq = {wv[0], wv[1], wv[2], wv[3]};
   store16_nt(a.kc + blk * a.kc_sb + off * a.kc_ss + h * a.kc_sh + 16 * dv, kq);
   store16_nt(a.vc + blk * a.vc_sb + off * a.vc_ss + h * a.vc_sh + 16 * dv, vq);
 }
@@ -165,22 +159,6 @@ struct DynWriteArgs {
   int64_t ksc_sb, ksc_ss, ksc_sh;  // element strides of the [NB, BS, Hkv] scale caches
   int64_t vsc_sb, vsc_ss, vsc_sh;
 };
-
-__device__ __forceinline__ float round_half_away(float x) {
-  return x >= 0.0f ? floorf(x + 0.5f) : ceilf(x - 0.5f);
-}
-
-__device__ __forceinline__ uint32_t quant4_dyn(const float* x, float s) {
-  uint32_t w = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    // IEEE fp32 quotient, clamped before rounding as the reference kernel does (:80-92).
-    float q = fminf(fmaxf(x[i] / s, -127.0f), 127.0f);
-    q = round_half_away(q);
-    w |= ((uint32_t)((int32_t)q) & 0xffu) << (8 * i);
-  }
-  return w;
-}
 
 __device__ __forceinline__ float row_absmax(const float* x, int lanes_per_row) {
   float m = 0.0f;
@@ -219,11 +197,11 @@ __global__ __launch_bounds__(256) void dynamic_write_kernel(DynWriteArgs d) {
   if (slot < 0 || slot >= a.capacity) return;
   const int64_t blk = slot / a.block_size;
   const int64_t off = slot - blk * a.block_size;
-  u32x2 kq, vq;
-  kq[0] = quant4_dyn(x, ks);
-  kq[1] = quant4_dyn(x + 4, ks);
-  vq[0] = quant4_dyn(y, vs);
-  vq[1] = quant4_dyn(y + 4, vs);
+  uint32_t wk[2], wv[2];
+  quantise<8, true>(x, quant_scale(ks), wk);
+  quantise<8, true>(y, quant_scale(vs), wv);
+  const u32x2 kq = {wk[0], wk[1]};
+  const u32x2 vq = {wv[0], wv[1]};
   *reinterpret_cast<u32x2*>(a.kc + blk * a.kc_sb + off * a.kc_ss + h * a.kc_sh + 8 * dv) = kq;
   *reinterpret_cast<u32x2*>(a.vc + blk * a.vc_sb + off * a.vc_ss + h * a.vc_sh + 8 * dv) = vq;
   if (dv == 0) {
@@ -271,12 +249,11 @@ __global__ __launch_bounds__(256) void dynamic_write16_kernel(DynWriteArgs d) {
   if (!in_range || slot < 0 || slot >= a.capacity) return;
   const int64_t blk = slot / a.block_size;
   const int64_t off = slot - blk * a.block_size;
-  u32x4 kq, vq;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    kq[i] = quant4_dyn(x + 4 * i, ks);
-    vq[i] = quant4_dyn(y + 4 * i, vs);
-  }
+  uint32_t wk[4], wv[4];
+  quantise<16, true>(x, quant_scale(ks), wk);
+  quantise<16, true>(y, quant_scale(vs), wv);
+  const u32x4 kq = {wk[0], wk[1], wk[2], wk[3]};
+  const u32x4 vq = {wv[0], wv[1], wv[2], wv[3]};
   store16_nt(a.kc + blk * a.kc_sb + off * a.kc_ss + h * a.kc_sh + 16 * dv, kq);
   store16_nt(a.vc + blk * a.vc_sb + off * a.vc_ss + h * a.vc_sh + 16 * dv, vq);
   if (dv == 0) {

@@ -54,6 +54,83 @@ __device__ __forceinline__ void load8_f32(const void* p, float (&x)[8]) {
   }
 }
 
+// ------------------------------------------------------------------------ int8 quantisation
+// The cache writes need code = clamp(round(RN(x / s)), -127, 127), RN the correctly rounded fp32
+// divide (the reference's torch path divides a widened fp32 value by an fp32 scale), rounded to
+// even (static scales) or half away from zero (dynamic scales).  A correctly rounded divide is
+// about ten VALU instructions, so the kernels take a shortcut that provably gives the same code:
+//   q0 = RN(x * r) with r = RN(1 / s):  |r - 1/s| <= 2^-24 / s, so with the rounding of the product
+//   and of the divide  |q0 - RN(x/s)| <= 3.0000002 * 2^-24 |x/s|  (r normal: s < 2^100).
+//   qc = q0 clamped to [-256, 256].  When qc lies more than 2^-20 |qc| from every half-integer,
+//   RN(x/s) lies in the same open interval between half-integers and rounds to rint(qc) under either
+//   rounding rule (they differ only at half-integers); quotients past +-256, infinities included,
+//   clamp to +-127 either way, and a NaN gives -127 on both paths (fmaxf first returns the bound).
+// The rest (about 1e-4 of the elements, all of them when s >= 2^100) are divided.  The argument and
+// an exhaustive check over every bf16 and fp16 value: tests/test_quant_fast_path.py.
+struct QuantScale {
+  float s;    // the scale (already floored at 1e-6)
+  float r;    // RN(1 / s)
+  bool fast;  // r is normal, the bound above holds
+};
+
+__device__ __forceinline__ QuantScale quant_scale(float s) { return {s, 1.0f / s, s < 0x1p100f}; }
+
+// The shortcut code of x (as a float in [-127, 127]); sets `divide` when x needs the divide.
+__device__ __forceinline__ float code_shortcut(float x, float r, bool& divide) {
+#pragma clang fp contract(off)
+  const float q0 = x * r;
+  const float qc = fminf(fmaxf(q0, -256.0f), 256.0f);
+  const float n = rintf(qc);
+  const float t = __builtin_fmaf(fabsf(qc), 0x1p-20f, fabsf(qc - n));
+  divide = !(t < 0.5f);
+  return fminf(fmaxf(n, -127.0f), 127.0f);
+}
+
+// The codes through the correctly rounded divide (the definition the shortcut reproduces).
+__device__ __forceinline__ float code_divide_even(float x, float s) {
+  return fminf(fmaxf(rintf(x / s), -127.0f), 127.0f);
+}
+__device__ __forceinline__ float code_divide_half_away(float x, float s) {
+  const float q = fminf(fmaxf(x / s, -127.0f), 127.0f);
+  return q >= 0.0f ? floorf(q + 0.5f) : ceilf(q - 0.5f);
+}
+
+// Four codes (floats holding integers in [-127, 127]) packed as int8 bytes, first in the lowest:
+// adding 1.5 * 2^23 leaves each integer's two's-complement low byte in the float's low byte.
+__device__ __forceinline__ uint32_t pack_codes(float c0, float c1, float c2, float c3) {
+  const uint32_t u0 = __builtin_bit_cast(uint32_t, c0 + 0x1.8p23f);
+  const uint32_t u1 = __builtin_bit_cast(uint32_t, c1 + 0x1.8p23f);
+  const uint32_t u2 = __builtin_bit_cast(uint32_t, c2 + 0x1.8p23f);
+  const uint32_t u3 = __builtin_bit_cast(uint32_t, c3 + 0x1.8p23f);
+  // v_perm_b32(hi, lo, sel): selector byte k < 4 picks byte k of lo, 4..7 byte k - 4 of hi,
+  // 0x0c gives 0.
+  const uint32_t lo = __builtin_amdgcn_perm(u1, u0, 0x0c0c0400u);  // [c0, c1, 0, 0]
+  const uint32_t hi = __builtin_amdgcn_perm(u3, u2, 0x04000c0cu);  // [0, 0, c2, c3]
+  return lo | hi;
+}
+
+// N codes of x with scale q; HALF_AWAY picks the dynamic write's rounding.  Returns the packed
+// bytes (N / 4 dwords).
+template <int N, bool HALF_AWAY>
+__device__ __forceinline__ void quantise(const float (&x)[N], QuantScale q, uint32_t (&out)[N / 4]) {
+  float c[N];
+  bool dv[N];
+  bool any = !q.fast;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    c[i] = code_shortcut(x[i], q.r, dv[i]);
+    any |= dv[i];
+  }
+  if (any) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (dv[i] || !q.fast)
+        c[i] = HALF_AWAY ? code_divide_half_away(x[i], q.s) : code_divide_even(x[i], q.s);
+  }
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) out[i] = pack_codes(c[4 * i], c[4 * i + 1], c[4 * i + 2], c[4 * i + 3]);
+}
+
 __device__ __forceinline__ int64_t load_index(const void* p, int64_t i, bool is64) {
   return is64 ? reinterpret_cast<const int64_t*>(p)[i]
               : (int64_t) reinterpret_cast<const int32_t*>(p)[i];

@@ -20,6 +20,10 @@ INCLUDE_DIR = PKG_DIR.parent.parent / "include"
 LIB_PATH = PKG_DIR / "libint8kv.so"
 
 SOURCES = ["cache_write.hip", "paged_decode.hip", "decode_loop_ops.hip"]
+# The torch extension over the C ABI (host code only; torch headers, linked to libint8kv.so).
+EXT_SOURCE = "torch_ops.cpp"
+EXT_NAME = "_int8kv_torch"
+EXT_PATH = PKG_DIR / f"{EXT_NAME}.so"
 
 # -packed-fp32-ops keeps hipcc from emitting packed fp32 VALU instructions (v_pk_fma_f32 and
 # friends) from ordinary float code; the host pass merely warns that it does not know it.
@@ -56,9 +60,28 @@ def _run(cmd, verbose: bool) -> None:
         print("\n".join(msgs), flush=True)
 
 
-def build_library(verbose: bool = False) -> Path:
-    """Compiles every HIP source into LIB_PATH (always rebuilds): one hipcc process per source,
-    in parallel, then one link."""
+def _torch_ext_flags():
+    """Compile and link flags of a host-only torch extension for this interpreter's torch."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    cflags = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-parameter",
+              "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-DTORCH_EXTENSION_NAME={EXT_NAME}",
+              "-DTORCH_API_INCLUDE_EXTENSION_H",
+              f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+              *[f"-I{p}" for p in cpp_extension.include_paths()],
+              f"-I{sysconfig.get_paths()['include']}", "-I/opt/rocm/include", f"-I{INCLUDE_DIR}"]
+    lflags = [f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+              f"-L{PKG_DIR}", "-lint8kv", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}"]
+    return cflags, lflags
+
+
+def build_library(verbose: bool = False, torch_ext: bool = True) -> Path:
+    """Compiles every HIP source into LIB_PATH and the torch extension into EXT_PATH (always
+    rebuilds): one compiler process per source, in parallel, then the links."""
     from concurrent.futures import ThreadPoolExecutor
 
     hipcc = hipcc_path()
@@ -68,6 +91,10 @@ def build_library(verbose: bool = False) -> Path:
         objs = [obj_dir / (Path(s).stem + ".o") for s in SOURCES]
         cmds = [[hipcc, *compile_flags, f"-I{INCLUDE_DIR}", "-c", str(CSRC_DIR / s), "-o", str(o)]
                 for s, o in zip(SOURCES, objs)]
+        ext_obj = obj_dir / "torch_ops.o"
+        if torch_ext:
+            cflags, lflags = _torch_ext_flags()
+            cmds.append(["g++", *cflags, "-c", str(CSRC_DIR / EXT_SOURCE), "-o", str(ext_obj)])
         with ThreadPoolExecutor(max_workers=len(cmds)) as pool:
             for fut in [pool.submit(_run, c, verbose) for c in cmds]:
                 fut.result()
@@ -75,6 +102,10 @@ def build_library(verbose: bool = False) -> Path:
         _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)],
              verbose)
         os.replace(tmp, LIB_PATH)
+        if torch_ext:
+            tmp = EXT_PATH.with_suffix(".so.tmp")
+            _run(["g++", "-shared", str(ext_obj), *lflags, "-o", str(tmp)], verbose)
+            os.replace(tmp, EXT_PATH)
     finally:
         shutil.rmtree(obj_dir, ignore_errors=True)
     return LIB_PATH

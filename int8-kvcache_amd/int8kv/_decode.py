@@ -7,7 +7,7 @@ import os
 
 import torch
 
-from . import _lib
+from . import _ext, _lib
 
 QUERY_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
@@ -100,6 +100,10 @@ def paged_decode(
     min_tiles: int = 0,
 ) -> torch.Tensor:
     """Launches int8kv_paged_decode on torch's current stream; returns ``out``."""
+    ext = _ext.module()
+    if ext is not None:
+        return ext.paged_decode(query, key_cache, value_cache, block_tables, seq_lens, k_scale,
+                                v_scale, out, num_ranges, flags, workspace, min_tiles)
     B, Hq, D = query.shape
     num_blocks, block_size, Hkv, _ = key_cache.shape
     width = block_tables.shape[1]

@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _decode
+from . import _decode, _ext
 
 
 def bf16_paged_attention(
@@ -22,6 +22,10 @@ def bf16_paged_attention(
     num_splits: int | None = None,
 ) -> torch.Tensor:
     """Paged decode on a 16-bit KV cache [num_blocks, BS, Hkv, D] (bf16 or fp16)."""
+    ext = _ext.module()
+    if ext is not None and not _decode.DEBUG_CHECKS:
+        return ext.bf16_paged_attention(query, key_cache, value_cache, block_tables, seq_lens,
+                                        num_splits)
     assert query.ndim == 3 and key_cache.ndim == 4 and value_cache.ndim == 4
     assert block_tables.ndim == 2 and seq_lens.ndim == 1
     assert query.dtype in _decode.QUERY_DTYPES

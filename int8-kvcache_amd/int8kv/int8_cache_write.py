@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _decode, _lib
+from . import _decode, _ext, _lib
 from .torch_reference import torch_int8_kv_cache_write_reference  # noqa: F401  (reference checker)
 
 _SRC_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
@@ -45,6 +45,11 @@ def int8_kv_cache_write(
     k_scale/v_scale: [Hkv].  ``num_warps``/``num_stages`` are accepted for signature
     compatibility and ignored (the launch shape is fixed by the kernel design).
     """
+    ext = _ext.module()
+    if ext is not None and not _decode.DEBUG_CHECKS:
+        # The same checks, conversions and launch in one call of the torch extension.
+        ext.int8_kv_cache_write(key, value, key_cache, value_cache, slot_mapping, k_scale, v_scale)
+        return None
     # Validation mirrors src/triton_ops/int8_cache_write.py:100-115.
     assert key.ndim == 3 and value.ndim == 3
     assert key_cache.ndim == 4 and value_cache.ndim == 4

@@ -26,7 +26,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _decode, _lib
+from . import _decode, _ext, _lib
 from .torch_reference import torch_int8_paged_attention_reference  # noqa: F401  (reference checker)
 
 
@@ -45,6 +45,11 @@ def int8_paged_attention(
     num_splits: int | None = None,
 ) -> torch.Tensor:
     """Paged decode on an INT8 KV cache.  Returns [B, Hq, D] in query.dtype."""
+    ext = _ext.module()
+    if ext is not None and not _decode.DEBUG_CHECKS:
+        # The same checks, allocation and launch in one call of the torch extension.
+        return ext.int8_paged_attention(query, key_cache, value_cache, block_tables, seq_lens,
+                                        k_scale, v_scale, bool(quantize_q), impl, num_splits)
     # Validation mirrors src/triton_ops/int8_paged_attention.py:698-719.
     assert query.ndim == 3 and key_cache.ndim == 4 and value_cache.ndim == 4
     assert block_tables.ndim == 2 and seq_lens.ndim == 1

@@ -7,8 +7,26 @@ import pytest
 import torch
 
 import int8kv
-from int8kv import _decode
+from int8kv import _decode, _ext
 from int8kv import synthetic as syn
+
+
+@pytest.fixture(autouse=True, params=["extension", "ctypes"])
+def host_path(request):
+    """Every check here runs on both host paths: the torch extension (the default when built)
+    and the ctypes binding of the same C ABI."""
+    if request.param == "extension":
+        if _ext.module() is None:
+            pytest.skip("the torch extension is not built")
+        yield request.param
+    else:
+        with _ext.use_ctypes():
+            yield request.param
+
+
+def test_extension_is_built_and_default(host_path):
+    assert _ext.EXT_PATH.exists(), "build() makes int8kv/_int8kv_torch.so"
+    assert (_ext.module() is not None) == (host_path == "extension")
 
 
 def _attn_args(**over):
