@@ -624,9 +624,17 @@ def main() -> int:
     # The merge kernel takes a few microseconds, less than the host's cost of one call: HIP-graph
     # replays give its device time.
     ms_merge = time_graph(merge_kernel)
+    # Each later op gets a short settle of its own: switching from one sustained load to another
+    # (the BF16 op after the INT8 one) showed the same kind of dip for a few ms.
+    settle(bf16_call, batch=10, min_ms=30.0)
     ms16 = time_loop(bf16_call, args.steps, args.warmup)
-    ms_q = time_loop(lambda: int8kv.int8_paged_attention(w["q"], w["kc"], w["vc"], w["bt"], w["sl"], w["ks"],
-                                                         w["vs"], quantize_q=True), args.steps, args.warmup)
+
+    def int8_q_call():
+        return int8kv.int8_paged_attention(w["q"], w["kc"], w["vc"], w["bt"], w["sl"], w["ks"], w["vs"],
+                                           quantize_q=True)
+
+    settle(int8_q_call, batch=10, min_ms=30.0)
+    ms_q = time_loop(int8_q_call, args.steps, args.warmup)
     # Host cost of one eager call: the wall time of enqueueing `steps` calls without waiting (each
     # call's ~190 us of device work keeps the device behind the host), through the torch
     # extension (the default path) and through the ctypes binding of the same C ABI.

@@ -438,12 +438,15 @@ __device__ __forceinline__ void issue_v(VTile<CACHE, NB, HD>& r, const char* vb,
 // 16-bit matrix cores keeps fp32 accuracy: the rounding of p would otherwise dominate the error
 // (2^-12 relative for fp16, 2^-9 for bf16).
 //   valid: number of tokens of this tile inside the sequence (1..16 NB).
+//   QSPLIT (an fp32 query): q is held as 16-bit hi + lo operands and each k-step takes two MFMAs,
+//   so the scores keep ~2^-22 (fp16) / 2^-16 (bf16) relative accuracy instead of one rounding of q.
 //   QQ (INT8 cache with a quantised query): the scores are the exact integer products of the
 //   int8 K rows and q8 on the int8 matrix cores (2 k-steps of 64, no K conversion); otherwise
 //   K is converted to 16-bit operands (4 k-steps of 32).
-template <int CACHE, int NB, bool QQ, int HD>
+template <int CACHE, int NB, bool QQ, int HD, bool QSPLIT>
 __device__ __forceinline__ void tile_scores(const KTile<CACHE, NB, HD>& r,
                                             const typename MfmaOp<CACHE>::T (&qop)[HD / 32],
+                                            const typename MfmaOp<CACHE>::T (&qlo)[HD / 32],
                                             const i32x4 (&q8op)[HD / 64], f32x4 (&acc)[HD / 16],
                                             float& m_run, float& l_part, int valid, int lg,
                                             float s_scale,
@@ -474,6 +477,7 @@ __device__ __forceinline__ void tile_scores(const KTile<CACHE, NB, HD>& r,
         kop = __builtin_bit_cast(OpT, r.k[s][ks]);
       }
       S[s] = mfma(kop, qop[ks], S[s]);
+      if constexpr (QSPLIT) S[s] = mfma(kop, qlo[ks], S[s]);
     }
   }
 
@@ -629,6 +633,7 @@ __device__ __forceinline__ float round_half_away(float x) {
 template <int CACHE, int QT, bool QQ, int HD>
 __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRaw<QT, HD>& raw,
                                               int kvh, typename MfmaOp<CACHE>::T (&qop)[HD / 32],
+                                              typename MfmaOp<CACHE>::T (&qlo)[HD / 32],
                                               i32x4 (&q8op)[HD / 64]) {
   constexpr int KS = HD / 32;  // 16-bit k-steps
   float x[KS][8];
@@ -696,7 +701,11 @@ __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRa
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qop[ks][e] = (typename MfmaOp<CACHE>::E)(x[ks][e] * qmul);
+    for (int e = 0; e < 8; ++e) {
+      const float v = x[ks][e] * qmul;  // exact: a power of two
+      qop[ks][e] = (typename MfmaOp<CACHE>::E)v;
+      if constexpr (QT == kF32) qlo[ks][e] = (typename MfmaOp<CACHE>::E)(v - (float)qop[ks][e]);
+    }
   return s_scale;
 }
 
@@ -804,14 +813,18 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   // The query, the first chunk's block ids and its first DEPTH tiles are requested back to
   // back; the query operand is built once they are all in flight (otherwise three memory
   // latencies would line up at every segment start).
+  // An fp32 query keeps a lo part (QSPLIT); a quantised query is exact in one operand.
+  constexpr bool QSPLIT = QT == kF32 && !QQ;
   OpT qop[HD / 32];
+  OpT qlo[HD / 32];  // unused (and removed by the compiler) unless QSPLIT
   i32x4 q8op[HD / 64];
   float s_scale;
   {
     QueryRaw<QT, HD> qraw;
     issue_query<QT, HD>(a, b, kvh, li, lg, qraw);
     chunk_prologue();
-    s_scale = finish_query<CACHE, QT, QQ, HD>(a, qraw, kvh, qop, q8op);
+    s_scale = finish_query<CACHE, QT, QQ, HD>(a, qraw, kvh, qop,
+                                              qlo, q8op);
   }
 
   // Tile t + d (buffer d): scores, refill K with tile t + d + DEPTH, P*V, refill V.  refill is a
@@ -822,7 +835,8 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   // that follows them (which would shorten the prefetch distance).
   auto tile_step = [&](int64_t t, int d, bool refill) {
     const int valid = valid_of(t + d);
-    tile_scores<CACHE, NB, QQ, HD>(kt[d], qop, q8op, acc, m_run, l_part, valid, lg, s_scale, pop);
+    tile_scores<CACHE, NB, QQ, HD, QSPLIT>(kt[d], qop, qlo, q8op,
+                                           acc, m_run, l_part, valid, lg, s_scale, pop);
     if (refill) {
       blocks_of(t + d + DEPTH, ph[d]);
       issue_k<CACHE, NB, NT, HD>(kt[d], kb, ph[d], a, li, lg);
@@ -851,7 +865,8 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     for (int d = 0; d + 1 < DEPTH; ++d) {
       if (t + d < c1) {
         const int valid = valid_of(t + d);
-        tile_scores<CACHE, NB, QQ, HD>(kt[d], qop, q8op, acc, m_run, l_part, valid, lg, s_scale,
+        tile_scores<CACHE, NB, QQ, HD, QSPLIT>(kt[d], qop, qlo,
+                                               q8op, acc, m_run, l_part, valid, lg, s_scale,
                                        pop);
         tile_pv<CACHE, NB, HD>(vt[d], pop, acc, valid, lg);
       }
@@ -909,8 +924,16 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
 // workgroup (x, y) handles kv head y * W + w % W over stream range x (HALVES = 1), or, with two
 // ranges per workgroup, 2x + w / W (paired ranges) or x + (w / W) grid.x.  DEPTH: tiles in flight
 // per wave (4 only in the one-wave-per-SIMD layout, whose register budget allows it).
+// Register budget: one wave per SIMD (512 registers) for INT8 waves with four tiles in flight and
+// for 16-bit caches, whose 16 KB tiles spilled to scratch under the two-wave budget (their
+// automatic range count is one wave per SIMD anyway); two waves per SIMD otherwise.
+template <int CACHE, int DEPTH>
+constexpr int decode_waves_per_eu() {
+  return (DEPTH > 2 || CACHE != kI8) ? 1 : 2;
+}
+
 template <int CACHE, int QT, bool NT, bool QQ, int HALVES, int HD, int DEPTH>
-__global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(DEPTH > 2 ? 1 : 2))) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<CACHE, DEPTH>()))) void decode_kernel(DecodeArgs a) {
   __shared__ int32_t s_ids[HALVES * kMaxWavesPerWG][kChunkTiles * tile_blocks<CACHE>()];
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -1287,7 +1310,8 @@ void launch_main(const DecodeArgs& a, dim3 grid, int W, hipStream_t s) {
                          s, a);
       return;
     }
-    if (a.depth == 4) {
+    // Four tiles in flight leave no registers for an fp32 query's lo operands: two for those.
+    if (a.depth == 4 && QT != kF32) {
       hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 4>), grid, dim3(W * kWave), 0, s,
                          a);
       return;
