@@ -315,3 +315,90 @@ def test_write_misaligned_sources_are_copied(cuda):
     torch.cuda.synchronize()
     assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
     assert torch.equal(ksc, ksc2) and torch.equal(vsc, vsc2)
+
+
+@pytest.mark.parametrize("hkv,d", [(1, 128), (3, 128), (8, 128), (4, 256), (8, 256), (2, 64)])
+def test_writes_across_kv_head_counts(cuda, hkv, d):
+    """Static and dynamic writes for kv-head counts and head sizes on both sides of the
+    token-major lane map (a token's heads in one wave when Hkv is a power of two and
+    Hkv * head_dim / 16 <= 64; the head-major kernels otherwise): bit-exact to the oracle."""
+    g = torch.Generator().manual_seed(100 * hkv + d)
+    T, nb = 77, 9
+    k = (torch.randn(T, hkv, d, generator=g) * 2).to(torch.bfloat16)
+    v = torch.randn(T, hkv, d, generator=g).to(torch.bfloat16)
+    slots = torch.randperm(nb * 16, generator=g)[:T]
+    slots[3::11] = -1
+    ks = (k.float().abs().amax(dim=(0, 2)) / 127).clamp_min(1e-6)
+    vs = (v.float().abs().amax(dim=(0, 2)) / 127).clamp_min(1e-6)
+    _assert_equal(*_run(k, v, slots, ks, vs, nb, cuda))
+    got, ref = _run_dynamic(k, v, slots, nb, cuda)
+    for name, a, b in zip(("K codes", "V codes", "K scales", "V scales"), got, ref):
+        assert np.array_equal(a, b), f"{name} differ from the oracle (Hkv={hkv}, D={d})"
+
+
+def test_dynamic_write_head_strided_scale_cache(cuda):
+    """Scale caches whose kv-head stride is not 1 (a transposed view): per-head scale stores."""
+    g = torch.Generator().manual_seed(55)
+    T, hkv, d, nb = 60, 4, 128, 7
+    k = (torch.randn(T, hkv, d, generator=g) * 3).to(torch.bfloat16)
+    v = torch.randn(T, hkv, d, generator=g).to(torch.bfloat16)
+    slots = torch.randperm(nb * 16, generator=g)[:T]
+    kc = torch.full((nb, 16, hkv, d), SENTINEL, dtype=torch.int8, device=cuda)
+    vc = torch.full_like(kc, SENTINEL)
+    ksc = torch.full((hkv, nb, 16), -1.0, device=cuda).permute(1, 2, 0)  # [nb, 16, hkv], stride(2) != 1
+    vsc = torch.full((hkv, nb, 16), -1.0, device=cuda).permute(1, 2, 0)
+    assert ksc.stride(2) != 1
+    got, ref = _run_dynamic(k, v, slots, nb, cuda, kc, vc, ksc, vsc)
+    for name, a, b in zip(("K codes", "V codes", "K scales", "V scales"), got, ref):
+        assert np.array_equal(a, b), f"{name} differ from the oracle"
+
+
+@pytest.mark.parametrize("src_dtype,T", [(torch.bfloat16, 262_144), (torch.float32, 65_536)])
+def test_hbm_sized_writes_sampled(cuda, src_dtype, T):
+    """Writes larger than the 256 MB Infinity Cache (the static write's token-major kernel runs
+    only there): every sampled token's K/V codes (and dynamic scales) equal the oracle's for that
+    token, and every slot the mapping does not name keeps the sentinel."""
+    g = torch.Generator().manual_seed(T)
+    hkv, d, nb = 4, 128, 2 * T // 16
+    k = (torch.randn(T, hkv, d, generator=g) * 2).to(src_dtype).to(cuda)
+    v = torch.randn(T, hkv, d, generator=g).to(src_dtype).to(cuda)
+    slots = torch.randperm(nb * 16, generator=g)[:T]
+    slots[7::1001] = -1
+    ks = (k.float().abs().amax(dim=(0, 2)) / 127).clamp_min(1e-6).cpu()
+    vs = (v.float().abs().amax(dim=(0, 2)) / 127).clamp_min(1e-6).cpu()
+    idx = torch.cat([torch.tensor([0, T - 1]), torch.randperm(T, generator=g)[:4094]])
+    idx = idx[slots[idx] >= 0]
+    n = idx.numel()
+    small = (n + 15) // 16
+    kx, vx = k[idx.to(cuda)].float().cpu().numpy(), v[idx.to(cuda)].float().cpu().numpy()
+    written = torch.zeros(nb * 16, dtype=torch.bool, device=cuda)
+    written[slots[slots >= 0].to(cuda)] = True
+    rows = slots[idx].to(cuda)
+
+    kc = torch.full((nb, 16, hkv, d), SENTINEL, dtype=torch.int8, device=cuda)
+    vc = torch.full_like(kc, SENTINEL)
+    int8kv.int8_kv_cache_write(k, v, kc, vc, slots.to(cuda), ks.to(cuda), vs.to(cuda))
+    torch.cuda.synchronize()
+    kr = np.full((small, 16, hkv, d), SENTINEL, np.int8)
+    vr = np.full_like(kr, SENTINEL)
+    O.int8_kv_cache_write(kx, vx, kr, vr, np.arange(n), ks.numpy(), vs.numpy())
+    for name, c, r in (("K", kc, kr), ("V", vc, vr)):
+        flat = c.view(nb * 16, hkv * d)
+        assert np.array_equal(flat[rows].cpu().numpy(), r.reshape(-1, hkv * d)[:n]), f"static {name}"
+        assert bool((flat[~written] == SENTINEL).all()), f"static {name}: unnamed slot written"
+
+    from int8kv import cache_ops
+    kc.fill_(SENTINEL)
+    vc.fill_(SENTINEL)
+    ksc = torch.full((nb, 16, hkv), -1.0, device=cuda)
+    vsc = torch.full_like(ksc, -1.0)
+    cache_ops.reshape_and_cache_int8(k, v, kc, vc, ksc, vsc, slots.to(cuda))
+    torch.cuda.synchronize()
+    ref = [np.full((small, 16, hkv, d), SENTINEL, np.int8), np.full((small, 16, hkv, d), SENTINEL, np.int8),
+           np.full((small, 16, hkv), -1.0, np.float32), np.full((small, 16, hkv), -1.0, np.float32)]
+    O.reshape_and_cache_int8(kx, vx, *ref, np.arange(n))
+    for name, c, r, fill in (("K", kc, ref[0], SENTINEL), ("V", vc, ref[1], SENTINEL),
+                             ("K scale", ksc, ref[2], -1.0), ("V scale", vsc, ref[3], -1.0)):
+        flat = c.view(nb * 16, -1)
+        assert np.array_equal(flat[rows].cpu().numpy(), r.reshape(small * 16, -1)[:n]), f"dynamic {name}"
+        assert bool((flat[~written] == fill).all()), f"dynamic {name}: unnamed slot written"
