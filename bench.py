@@ -125,9 +125,12 @@ def time_events(fn, steps: int, warmup: int) -> float:
     return a.elapsed_time(b) / steps
 
 
-def time_graph(fn, calls: int = 20, replays: int = 10) -> float:
+def time_graph(fn, calls: int = 20, replays: int = 10, settle_ms: float = 30.0) -> float:
     """Device time per call (ms) of ``fn`` captured ``calls`` times in one HIP graph and replayed:
-    removes the host's per-call launch cost, which dominates calls of a few microseconds."""
+    removes the host's per-call launch cost, which dominates calls of a few microseconds.  The
+    replays are timed after a settle phase of replays (``settle``): capturing leaves the device
+    idle for a few ms, and the start-up transient that follows would otherwise fall on the timed
+    replays (B=32 x 8256 tokens: 56.7 us per decode + merge call inside it, ~53 us after it)."""
     import torch
 
     s = torch.cuda.Stream()
@@ -142,9 +145,7 @@ def time_graph(fn, calls: int = 20, replays: int = 10) -> float:
         for _ in range(calls):
             fn()
     torch.cuda.synchronize()
-    for _ in range(2):
-        graph.replay()
-    torch.cuda.synchronize()
+    settle(graph.replay, batch=2, min_ms=settle_ms, max_ms=4 * settle_ms)
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     a.record()
@@ -205,7 +206,7 @@ def write_legs(dev, cfg1_graph: bool = True) -> dict:
     import torch
 
     import int8kv
-    from int8kv import cache_ops
+    from int8kv import cache_ops, roofline
     from int8kv import synthetic as syn
 
     res = {}
@@ -250,9 +251,8 @@ def write_legs(dev, cfg1_graph: bool = True) -> dict:
             timer = lambda fn: time_events(fn, 40, 10)  # noqa: E731
         ms_s, ms_d = timer(static), timer(dynamic)
         ms_m, ms_c = timer(mix21), timer(copy)
-        elems = n_tok * 4 * 128
-        sbytes = elems * (2 + 2 + 1 + 1) + (n_tok + n_pad) * 8 + 2 * 4 * 4
-        dbytes = sbytes - 2 * 4 * 4 + n_tok * 4 * 4 * 2
+        sbytes = roofline.write_bytes(n_tok, n_tok + n_pad, 4, 128)
+        dbytes = roofline.write_bytes(n_tok, n_tok + n_pad, 4, 128, dynamic=True)
         ceiling = moved / min(ms_m, ms_c) / 1e6
         out = {"tokens": n_tok, "padding_slots": n_pad, "cache_blocks": nb,
                "static_us": round(ms_s * 1e3, 2), "static_bytes": sbytes,
@@ -293,7 +293,7 @@ def cpu_baseline(w, out_gpu, target_s: float = 4.0, runs: int = 3):
     returns the agreement of the GPU output with this CPU result on the sample."""
     import torch
 
-    from oracle import int8kv_oracle as O
+    from int8kv import roofline
     from oracle import torch_cpu_path as TP
 
     threads = cpu_threads()
@@ -321,7 +321,7 @@ def cpu_baseline(w, out_gpu, target_s: float = 4.0, runs: int = 3):
             times.append(time.perf_counter() - t0)
         med = statistics.median(times)
         s_lens = lens[sample].numpy()
-        nbytes = O.decode_bytes(s_lens, 4, 128, 1, len(sample), 28)
+        nbytes = roofline.decode_bytes(s_lens, 4, 128, 1, len(sample), 28)
         got = out_gpu.float().cpu()[sample].double()
         r = ref[sample].double()
         check = {"sequences": len(sample), "max_abs": round(float((got - r).abs().max()), 6),
@@ -348,6 +348,7 @@ def cpu_baseline(w, out_gpu, target_s: float = 4.0, runs: int = 3):
 def cpu_oracle_single_thread(w, budget_s: float = 3.0) -> dict:
     """The numpy oracle on one thread over the workload's sequences until ``budget_s`` seconds
     of work (a secondary figure beside the all-core torch baseline)."""
+    from int8kv import roofline
     from oracle import int8kv_oracle as O
 
     try:
@@ -367,7 +368,7 @@ def cpu_oracle_single_thread(w, budget_s: float = 3.0) -> dict:
             t0 = time.perf_counter()
             O.paged_attention_ref(q[b:b + 1], kc, vc, bt[b:b + 1], lens[b:b + 1], ks, vs)
             t_total += time.perf_counter() - t0
-            nbytes += O.decode_bytes(lens[b:b + 1], 4, 128, 1, 1, 28)
+            nbytes += roofline.decode_bytes(lens[b:b + 1], 4, 128, 1, 1, 28)
             calls += 1
             if t_total >= budget_s:
                 break
@@ -402,8 +403,8 @@ def sweep_configs(dev, out_path: str | None) -> dict:
     import torch
 
     import int8kv
+    from int8kv import roofline
     from int8kv import synthetic as syn
-    from oracle import int8kv_oracle as O
 
     res = {}
     dist = syn.make_distribution(11)
@@ -438,13 +439,74 @@ def sweep_configs(dev, out_path: str | None) -> dict:
             ):
                 ms = time_graph(fn)
                 e = 2 if name.startswith("bf16") else 1
-                nbytes = O.decode_bytes([ctx] * B, 4, 128, e, B, 28)
+                nbytes = roofline.decode_bytes([ctx] * B, 4, 128, e, B, 28)
                 row[name + "_us"] = round(ms * 1e3, 2)
                 row[name + "_GBps"] = round(nbytes / ms / 1e6, 1)
             rows.append(row)
             log(f"cfg2 B={B} ctx={ctx}: int8 {row['int8_auto_us']} us (single pass "
                 f"{row['int8_single_pass_us']}), bf16 {row['bf16_auto_us']} us")
     res["cfg2_sweep"] = rows
+    if out_path:
+        Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+        Path(out_path).write_text(json.dumps(res, indent=1))
+    return res
+
+
+# Decode calls between config 2 and config 3 (0.03-0.27 GB of INT8 K/V per call): config 4's
+# attention shape (B=32 x ~8.2k tokens) and its neighbours.  (name, batch, length, ragged):
+# ragged batches draw lengths uniformly from [1, length].
+MIDSIZE_CASES = (("B32x8256", 32, 8256, False), ("B32xU16k", 32, 16384, True),
+                 ("B128xU4k", 128, 4096, True), ("B16x16k", 16, 16384, False),
+                 ("B8x32k", 8, 32768, False), ("B1x32k", 1, 32768, False),
+                 ("B256xU2k", 256, 2048, True))
+
+
+def midsize_legs(dev, out_path: str | None) -> dict:
+    """INT8 decode at the mid sizes above (random int8 K/V in a pool just larger than the batch
+    needs, shuffled block tables, Qwen2.5-7B attention shape).  Per case: the decode kernel alone
+    (HIP events over back-to-back launches after a settle phase), the merge kernel alone and the
+    whole op (HIP-graph replays), and GB/s of algorithmic bytes for the kernel and the op."""
+    import torch
+
+    from int8kv import _decode, _lib, roofline
+    from int8kv import synthetic as syn
+
+    rows = []
+    for i, (name, B, ctx, ragged) in enumerate(MIDSIZE_CASES):
+        lens = syn.ragged_lengths(B, ctx, 5 + i) if ragged else torch.full((B,), ctx, dtype=torch.int64)
+        need = int(((lens + 15) // 16).sum())
+        nb = need + 64
+        g = torch.Generator().manual_seed(100 + i)
+        bt = syn.random_block_tables(lens.tolist(), nb, g).to(dev)
+        kc = torch.randint(-127, 128, (nb, 16, 4, 128), dtype=torch.int8, generator=g).to(dev)
+        vc = torch.randint(-127, 128, (nb, 16, 4, 128), dtype=torch.int8, generator=g).to(dev)
+        q = torch.randn(B, 28, 128, generator=g).to(torch.bfloat16).to(dev)
+        ks = torch.full((4,), 0.02, device=dev)
+        vs = torch.full((4,), 0.01, device=dev)
+        sl = lens.to(torch.int32).to(dev)
+        out = torch.empty_like(q)
+        ws = torch.empty(_lib.load().int8kv_decode_workspace_bytes(28, 4, 128, 16, 0),
+                         dtype=torch.uint8, device=dev)
+
+        def call(flags):
+            return lambda: _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, out, 0, flags, ws, 0)
+
+        settle(call(_lib.DECODE_ALL), batch=20, min_ms=30.0)
+        ms_main = time_events(call(_lib.DECODE_MAIN), 50, 10)
+        ms_op = time_graph(call(_lib.DECODE_ALL))
+        ms_merge = time_graph(call(_lib.DECODE_MERGE))
+        nbytes = roofline.decode_bytes(lens.numpy(), 4, 128, 1, B, 28)
+        row = {"case": name, "batch": B, "tokens": int(lens.sum()), "bytes": nbytes,
+               "decode_kernel_us": round(ms_main * 1e3, 2),
+               "decode_kernel_TBps": round(nbytes / ms_main / 1e9, 3),
+               "merge_graph_us": round(ms_merge * 1e3, 2), "op_graph_us": round(ms_op * 1e3, 2),
+               "op_TBps": round(nbytes / ms_op / 1e9, 3)}
+        rows.append(row)
+        log(f"midsize {name}: decode kernel {row['decode_kernel_us']} us "
+            f"({row['decode_kernel_TBps']} TB/s), op {row['op_graph_us']} us ({row['op_TBps']} TB/s), "
+            f"merge {row['merge_graph_us']} us")
+        del kc, vc
+    res = {"midsize": rows}
     if out_path:
         Path(out_path).parent.mkdir(parents=True, exist_ok=True)
         Path(out_path).write_text(json.dumps(res, indent=1))
@@ -544,6 +606,8 @@ def main() -> int:
     ap.add_argument("--writes-only", action="store_true",
                     help="run only the cache-write legs (config 1 eagerly, not as graph replays: "
                          "for rocprofv3 counter passes) and print their JSON")
+    ap.add_argument("--midsize", metavar="JSON", default=None,
+                    help="only the mid-size INT8 decode cases (B=32 x 8256 ...), results to JSON")
     ap.add_argument("--sweep", metavar="JSON", default=None,
                     help="also measure the config-2 decode sweep, written to JSON")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -571,8 +635,7 @@ def main() -> int:
     import torch
 
     import int8kv
-    from int8kv import _decode, _lib
-    from oracle import int8kv_oracle as O
+    from int8kv import _decode, _lib, roofline
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     _lib.load()
@@ -581,6 +644,9 @@ def main() -> int:
     if args.tpot_only:
         tpot_config4(dev, args.tpot, *tpot_args, gemm_tuning=args.gemm_tuning,
                      tuning_file=args.gemm_tuning_file)
+        return 0
+    if args.midsize:
+        midsize_legs(dev, args.midsize)
         return 0
     if args.writes_only:
         res = write_legs(dev, cfg1_graph=False)
@@ -591,8 +657,8 @@ def main() -> int:
     log("building workload (B=64, ctx ~ U[1, 32768]) ...")
     w = build_workload(dev, seed=args.seed)
     lens = w["lens"]
-    nbytes8 = O.decode_bytes(lens.numpy(), 4, 128, 1, 64, 28)
-    nbytes16 = O.decode_bytes(lens.numpy(), 4, 128, 2, 64, 28)
+    nbytes8 = roofline.decode_bytes(lens.numpy(), 4, 128, 1, 64, 28)
+    nbytes16 = roofline.decode_bytes(lens.numpy(), 4, 128, 2, 64, 28)
     log(f"tokens={int(lens.sum())} blocks={w['num_blocks']} int8 bytes/call={nbytes8}")
 
     def int8_call():

@@ -448,6 +448,28 @@ def test_batches_beyond_one_wave_of_sequences(cuda, splits):
 
 
 @pytest.mark.parametrize("splits", [None, 3])
+def test_batches_beyond_eight_chunks(cuda, splits):
+    """B = 600: the merge kernel requests the lengths of the first 8 x 64 sequences at once and
+    walks the rest chunk by chunk; sequences cut by range bounds on both sides of sequence 512,
+    and empty ones in both parts, against the oracle."""
+    g = torch.Generator().manual_seed(600)
+    lens = torch.randint(1, 300, (600,), generator=g).tolist()
+    lens[511], lens[512], lens[513] = 2000, 3000, 1500
+    c = decode_case(lens, seed=600, extra_blocks=7)
+    sl = c.seq_lens.clone()
+    for b in (5, 300, 520, 599):
+        sl[b] = 0
+    q, kc, vc, bt, _, ks, vs = to_dev(c, cuda)
+    out = int8kv.int8_paged_attention(q, kc, vc, bt, sl.to(cuda), ks, vs, num_splits=splits)
+    torch.cuda.synchronize()
+    ref = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                sl.numpy(), c.k_scale.numpy(), c.v_scale.numpy())
+    for b in (5, 300, 520, 599):
+        assert (out[b] == 0).all(), b
+    _check(out, ref, f"B=600 splits={splits}")
+
+
+@pytest.mark.parametrize("splits", [None, 3])
 def test_wide_tables_take_the_64bit_unit_scan(cuda, splits):
     """A table wide enough that one sequence could hold 2^25 tiles (4096-token blocks, 2^18
     table entries per row) makes the kernels count stream units with 64-bit wave scans instead
