@@ -1262,7 +1262,14 @@ constexpr int kWavesPerCU = 4;
 // INT8 ranges of at least this many units (host-side bound) keep four tiles in flight per wave;
 // shorter ones two (the deeper prologue and its unused refills cost 2-3 us on short ranges).
 constexpr int64_t kDeepMinUnits = 32;
-constexpr int64_t kInfinityCacheBytes = 256LL << 20;  // MI355X last-level (MALL) capacity
+// INT8 K/V loads carry the non-temporal hint when a call may read more than this (half of
+// MI355X's 256 MB Infinity Cache): such a stream does not stay resident across calls, and
+// keeping it out of the caches stops it from evicting other lines.  Measured with half the cache
+// against the whole: B=16 x 16k 48.5 vs 50.0 us on one pool and 49.4 vs 55.7 us rotating over 4
+// layers' pools, B=8 x 32k 47.7 vs 52.2 / 49.6 vs 55.8 us (both ~268 MB, just at the old
+// bound), no change at 135 and 250 MB; cache-resident pools (config 2, <= 34 MB) read ~10 %
+// slower with the hint, so they keep plain loads.
+constexpr int64_t kNonTemporalMinBytes = 128LL << 20;
 // Share (1/256) of a range pair's units given to the first half of the workgroup.  Two waves
 // share each SIMD, and the first (waves 0..W-1) streams ~30 % faster than the second on
 // MI355X; with equal halves the second then runs alone for the last quarter of the call.
@@ -1624,11 +1631,11 @@ int decode_entry(
   a.scan32 = (double)kWave * (std::ceil((double)table_width * block_size / a.tile_tokens) +
                               a.seq_cost) < 2147483647.0;
 
-  // Non-temporal K/V loads when the call may stream more than the Infinity Cache holds: the
-  // most it can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).
+  // Non-temporal K/V loads when the call may stream more than kNonTemporalMinBytes: the most it
+  // can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).
   const int64_t touch_blocks = batch * table_width < num_blocks ? batch * table_width : num_blocks;
   const bool nt = (double)touch_blocks * block_size * num_kv_heads * head_dim * ce * 2 >
-                  (double)kInfinityCacheBytes;
+                  (double)kNonTemporalMinBytes;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (cache_dtype) {
     case INT8KV_I8:
