@@ -1038,20 +1038,23 @@ __global__ __launch_bounds__(kGroupWaves * 64) __attribute__((amdgpu_waves_per_e
     }
   }
   __syncthreads();
-  if (wave != 0 || li >= G) return;
-  // Online-softmax merge of the NW states (exp2 domain), as merge_kernel does for records.
+  // Online-softmax merge of the NW states (exp2 domain), as merge_kernel does for records.  The
+  // four row groups rr of the accumulator layout are independent, so waves 0..3 take one each
+  // (head_dim elements HD/4 lg + HD/16 rr + [0, HD/16) of lane (li, lg)): wave 0 merging all
+  // of them took 2.3 us of a 9.4 us call at B = 1 x 512 tokens.
+  if (wave >= 4 || li >= G) return;
+  const int rr = wave;
   float M = -INFINITY, Ls = 0.0f;
-  f32x4 O[HD / 16];
+  float O[HD / 16];
 #pragma unroll
-  for (int dt = 0; dt < HD / 16; ++dt) O[dt] = (f32x4)(0.0f);
+  for (int dt = 0; dt < HD / 16; ++dt) O[dt] = 0.0f;
+#pragma unroll
   for (int w = 0; w < NW; ++w) {
     const float m = s_m[w][li];
     const float l = s_l[w][li];
-    f32x4 A[HD / 16];
+    float A[HD / 16];
 #pragma unroll
-    for (int dt = 0; dt < HD / 16; ++dt)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) A[dt][rr] = s_acc[w][(rr * (HD / 16) + dt) * kWave + lane];
+    for (int dt = 0; dt < HD / 16; ++dt) A[dt] = s_acc[w][(rr * (HD / 16) + dt) * kWave + lane];
     const float Mn = fmaxf(M, m);
     if (Mn == -INFINITY) {  // nothing finite yet: add unscaled (a NaN still reaches the output)
       Ls += l;
@@ -1069,13 +1072,10 @@ __global__ __launch_bounds__(kGroupWaves * 64) __attribute__((amdgpu_waves_per_e
   const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
   const float inv = Ls > 0.0f ? vscale / Ls : 0.0f;
   char* op = a.out + (b * a.o_sb + (int64_t)(kvh * G + li) * a.o_sh) * esize<QT>();
+  float o[HD / 16];
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    float o[HD / 16];
-#pragma unroll
-    for (int dt = 0; dt < HD / 16; ++dt) o[dt] = O[dt][rr] * inv;
-    store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), o);
-  }
+  for (int dt = 0; dt < HD / 16; ++dt) o[dt] = O[dt] * inv;
+  store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), o);
 }
 
 // Stores 4 consecutive fp32 values as DT (aligned to 4 elements).
