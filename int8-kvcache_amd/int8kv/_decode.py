@@ -4,6 +4,7 @@ from __future__ import annotations
 
 import math
 import os
+import threading
 
 import torch
 
@@ -26,10 +27,13 @@ def _aligned16(t: torch.Tensor, dims) -> bool:
 
 MAX_RANGES = 1 << 20
 
-# Decode workspaces reused across calls, one per (device, stream): calls on one stream run in
-# order, so they never use it at the same time.  A call under HIP-graph capture gets its own
+# Decode workspaces reused across calls, one per (host thread, device, stream).  A call is two
+# launches (decode, then merge) that read and write its workspace; calls from one thread on one
+# stream are enqueued whole, one after the other, so they never interleave.  Two threads that
+# enqueue on one stream can interleave their launches (thread B's decode between thread A's
+# decode and merge), so each thread keeps its own.  A call under HIP-graph capture gets its own
 # (allocated from the graph's pool), so a graph never shares memory with eager calls.
-_WORKSPACES: dict = {}
+_WORKSPACES = threading.local()
 _WS_BYTES: dict = {}
 
 
@@ -44,10 +48,13 @@ def _workspace_bytes(lib, Hq, Hkv, D, block_size, num_ranges) -> int:
 def _cached_workspace(dev, stream: int, need: int) -> torch.Tensor:
     if torch.cuda.is_current_stream_capturing():
         return torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    cache = getattr(_WORKSPACES, "by_stream", None)
+    if cache is None:
+        cache = _WORKSPACES.by_stream = {}
     key = (dev.index, stream)
-    ws = _WORKSPACES.get(key)
+    ws = cache.get(key)
     if ws is None or ws.numel() < need:
-        ws = _WORKSPACES[key] = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+        ws = cache[key] = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
     return ws
 
 

@@ -1,8 +1,8 @@
 """The operators under concurrent host use: two host threads on their own streams, two threads on
 one shared stream, and HIP-graph replays interleaved with eager calls on one stream.
 
-The host paths keep state across calls: the ctypes path caches a decode workspace per (device,
-stream) and ctypes stride arrays per stride tuple; the extension allocates outputs and workspaces
+The host paths keep state across calls: the ctypes path caches a decode workspace per (host thread,
+device, stream) and ctypes stride arrays per stride tuple; the extension allocates outputs and workspaces
 through torch's stream-ordered caching allocator.  Every output must equal the same call made
 alone on the default stream, bit for bit (the kernels are deterministic for given inputs).
 """
