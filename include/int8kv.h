@@ -124,8 +124,9 @@ int32_t int8kv_decode_auto_ranges(int32_t num_kv_heads);
 
 /*
  * Bytes of device workspace int8kv_paged_decode needs (the split partials: one running max,
- * one running sum and one head_dim accumulator per range, slot and query head); independent of
- * the batch, the context lengths and the block-table width.  num_ranges is the value that will
+ * one running sum and one head_dim accumulator per range, slot and query head, and per range a
+ * 32-byte descriptor of the cut sequence it starts); independent of the batch, the context
+ * lengths and the block-table width.  num_ranges is the value that will
  * be passed to int8kv_paged_decode (0 = automatic, for the current device).  Returns 0 for
  * sizes int8kv_paged_decode would reject.
  */

@@ -23,7 +23,10 @@
 //     two waves sharing a SIMD the first streams faster (see kFirstShare).
 //   * A sequence wholly inside one range is finished by that wave (output written directly).
 //     A sequence cut by range bounds leaves (max, sum, accumulator) partials in the workspace,
-//     at most two per range and head; merge_kernel combines them.
+//     at most two per range and head; a merge kernel combines them: merge_kernel (one workgroup
+//     per sequence and query head, which finds its ranges from seq_lens) for batches below half
+//     the range count, merge_by_range_kernel (one per range and query head, from the descriptor
+//     of the cut sequence each range starts, which the decode kernel writes) otherwise.
 //   * Per 32-token tile and wave:  S^T = K * Q^T  (2 x 4 MFMA 16x16x32; rows = tokens, cols =
 //     heads), online softmax in the exp2 domain, then out^T += V^T * P^T (2 x 8 MFMA 16x16x32,
 //     P split into 16-bit hi + lo parts; rows = head_dim, cols = heads).  The MFMA accumulator
@@ -90,6 +93,10 @@ struct DecodeArgs {
   float* ws_acc;       // [max_ranges * 2][num_q_heads][head_dim]
   float* ws_m;         // [max_ranges * 2][num_q_heads]
   float* ws_l;         // [max_ranges * 2][num_q_heads]
+  int64_t* ws_cut;     // [max_ranges][4]: (sequence, unit of its last tile) of the cut sequence a
+                       // range starts (its tile 0 lies in the range and its tiles run past it;
+                       // sequence -1 when the range starts none), then the plan (U; P, share,
+                       // paired packed), from which the merge finds the sequence's last range
   int64_t num_blocks;
   int64_t batch;
   int32_t num_kv_heads;
@@ -112,6 +119,7 @@ struct DecodeArgs {
   int32_t group_mode;   // one workgroup per (sequence, kv head), states merged in LDS
   int32_t head_dim;     // 64 or 128
   int32_t scan32;       // a 64-sequence chunk's units fit 32 bits (see units_scan)
+  int32_t cut_desc;     // write ws_cut (merge_by_range_kernel follows)
 };
 
 // ------------------------------------------------------------------------ wave utilities
@@ -170,6 +178,36 @@ __device__ __forceinline__ int64_t seq_len_of(const DecodeArgs& a, int64_t b) {
   return L < 0 ? 0 : (L > cap ? cap : L);
 }
 
+// Lengths (as seq_len_of) of sequences (c0 + k) 64 + lane, k < K, with all K loads issued before
+// any is used (the index clamped into the batch, 0 past it): seq_len_of's bounds test around
+// each load made every chunk wait for the previous one.
+template <int K>
+__device__ __forceinline__ void seq_len_chunks(const DecodeArgs& a, int64_t c0, int lane,
+                                               int64_t (&L)[K]) {
+  const int64_t last = a.batch - 1;
+  if (a.sl_is64) {
+    const int64_t* t = reinterpret_cast<const int64_t*>(a.sl);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int64_t i = (c0 + k) * kWave + lane;
+      L[k] = t[i < last ? i : last];
+    }
+  } else {
+    const int32_t* t = reinterpret_cast<const int32_t*>(a.sl);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int64_t i = (c0 + k) * kWave + lane;
+      L[k] = t[i < last ? i : last];
+    }
+  }
+  const int64_t cap = (int64_t)a.width << a.block_shift;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int64_t x = L[k] < 0 ? 0 : (L[k] > cap ? cap : L[k]);
+    L[k] = (c0 + k) * kWave + lane <= last ? x : 0;
+  }
+}
+
 __device__ __forceinline__ int64_t tiles_of(const DecodeArgs& a, int64_t L) {
   static_assert(tile_blocks<kI8>() == 2 && tile_blocks<kBF16>() == 2, "32-token tiles");
   return (L + 2 * kRows - 1) / (2 * kRows);
@@ -209,6 +247,15 @@ struct Plan {
   int32_t share;  // first_share
   bool paired;
 };
+
+// A plan's P, share and paired in one word (P < 2^31, share < 2^8), and back, with U.
+__device__ __forceinline__ int64_t pack_plan(const Plan& p) {
+  return p.P | ((int64_t)p.share << 32) | ((int64_t)p.paired << 40);
+}
+
+__device__ __forceinline__ Plan unpack_plan(int64_t U, int64_t w) {
+  return {U, w & 0x7fffffff, (int32_t)((w >> 32) & 0xff), ((w >> 40) & 1) != 0};
+}
 
 // The plan of a batch of U units.
 __device__ __forceinline__ Plan plan_of_units(const DecodeArgs& a, int64_t U) {
@@ -954,6 +1001,17 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(de
   if constexpr (HALVES == 2)
     r = plan.paired ? 2 * (int64_t)blockIdx.x + half
                     : (int64_t)blockIdx.x + half * (int64_t)gridDim.x;
+  // The range's cut-sequence descriptor for merge_by_range_kernel: "none" first, overwritten by
+  // the same lane below if the range starts a cut sequence.  Every range below max_ranges gets
+  // one per call, so the workspace needs no initialisation.  It holds only values the walk
+  // already has (the merge derives the last range from them), so the walk keeps no more of the
+  // plan live than before.
+  const bool cut_writer = a.cut_desc && kvh == 0 && lane == 0 && r < a.max_ranges;
+  if (cut_writer) {
+    a.ws_cut[4 * r] = -1;
+    a.ws_cut[4 * r + 2] = plan.U;
+    a.ws_cut[4 * r + 3] = pack_plan(plan);
+  }
   if (r >= plan.P) return;
   const int64_t u0 = range_start(plan, r);
   const int64_t u1 = range_start(plan, r + 1);
@@ -989,6 +1047,10 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(de
         const int64_t te = (u1 < first + nb ? u1 : first + nb) - first;
         if (ta >= te) continue;
         const bool full = ta == 0 && te == nb;
+        if (cut_writer && ta == 0 && te < nb) {  // b starts here and runs past this range
+          a.ws_cut[4 * r] = base + j;
+          a.ws_cut[4 * r + 1] = first + nb - 1;
+        }
         run_segment<CACHE, QT, NT, QQ, HD, DEPTH>(a, s_ids[wave], base + j, Lb, kvh, ta, te, full,
                                2 * r + cut_slot(ta), lane);
       }
@@ -1111,33 +1173,86 @@ __device__ __forceinline__ void merge_in(float& M, float& L, f32x4& O, float m, 
   M = Mn;
 }
 
-// Combines the partials of every sequence cut by range bounds.  grid (batch, num_q_heads), MW
-// waves per query head.  A wave's lanes are RS = 256 / HD range slots of HD / 4 columns: lane
-// (slot rs, column c4) of wave w owns head_dim elements [4 c4, 4 c4 + 4) of ranges
+// Folds the partial records of query head h of a cut sequence b whose tiles lie in ranges
+// r0 .. r0 + nr - 1 (range r0's slot-1 record, the later ranges' slot-0 records) and stores its
+// output row; a workgroup of MW waves.  A wave's lanes are RS = 256 / HD range slots of HD / 4
+// columns: lane (slot rs, column c4) of wave w owns head_dim elements [4 c4, 4 c4 + 4) of ranges
 // RS w + rs, RS w + rs + RS MW, ... and folds them in with one online-softmax pass, four ranges'
 // loads in flight at a time (4 RS MW ranges per round for the workgroup); the RS MW running
-// states per column are then merged through LDS.  A sequence's merge costs about
-// 1 + nr / (4 RS MW) dependent memory latencies; the host picks MW from the average number of
-// ranges per sequence (one wave when a round covers them, up to four for a few long sequences).
-// More waves do not help a long sequence: its workgroup streams nr x 512 bytes per query head on
-// one compute unit (one 32k-token sequence cut 256 ways: 8.1 us with four waves, 8.8 with 16).
-constexpr int kMergeChunks = 8;  // 64-sequence chunks of seq_lens a merge wave requests at once
-
+// states per column are then merged through LDS.  About 1 + nr / (4 RS MW) dependent memory
+// latencies.  More waves do not help a long sequence: its workgroup streams nr x 512 bytes per
+// query head on one compute unit (one 32k-token sequence cut 256 ways: 8.1 us with four waves,
+// 8.8 with 16).
 template <int CACHE, int QT, int MW, int HD>
-__global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
+__device__ __forceinline__ void merge_records(const DecodeArgs& a, int64_t b, int h, int64_t r0,
+                                              int64_t nr) {
   constexpr int C4 = HD / 4;      // float4 columns of a head
   constexpr int RS = kWave / C4;  // range slots per wave
   __shared__ float s_m[RS * MW][C4];
   __shared__ float s_l[RS * MW][C4];
   __shared__ f32x4 s_o[RS * MW][C4];
-  const int64_t b = blockIdx.x;
-  const int h = blockIdx.y;
   const int kvh = h / a.group;
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int rs = lane / C4;  // range slot of this lane within the wave
   const int c4 = lane % C4;  // head_dim elements [4 c4, 4 c4 + 4)
   const int slot = RS * wave + rs;  // 0 .. RS MW - 1
+  auto row_of = [&](int64_t c) -> int64_t {  // partial row of range r0 + c, head h
+    return (2 * (r0 + c) + cut_slot(c)) * a.num_q_heads + h;  // tile 0 lies in range r0
+  };
+
+  constexpr int kStride = RS * MW;
+  float M = -INFINITY, L = 0.0f;
+  f32x4 O = (f32x4)(0.0f);
+  for (int64_t cb = slot; cb < nr; cb += 4 * kStride) {
+    // All four loads unconditionally (a slot past the last range reads the last range's record
+    // again and is then ignored): a branch around each load made the compiler wait for the
+    // previous ones before issuing the next, one memory latency per range instead of per round.
+    float m[4], l[4];
+    f32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t c = cb + u * kStride;
+      const int64_t row = row_of(c < nr ? c : nr - 1);
+      m[u] = a.ws_m[row];
+      l[u] = a.ws_l[row];
+      v[u] = *reinterpret_cast<const f32x4*>(a.ws_acc + row * HD + 4 * c4);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool in = cb + u * kStride < nr;
+      merge_in(M, L, O, in ? m[u] : -INFINITY, in ? l[u] : 0.0f, in ? v[u] : (f32x4)(0.0f));
+    }
+  }
+  s_m[slot][c4] = M;
+  s_l[slot][c4] = L;
+  s_o[slot][c4] = O;
+  __syncthreads();
+  if (threadIdx.x >= C4) return;
+  M = -INFINITY;
+  L = 0.0f;
+  O = (f32x4)(0.0f);
+#pragma unroll
+  for (int k = 0; k < kStride; ++k) merge_in(M, L, O, s_m[k][c4], s_l[k][c4], s_o[k][c4]);
+  const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
+  const float inv = L > 0.0f ? vscale / L : 0.0f;
+  store4<QT>(a.out + (b * a.o_sb + (int64_t)h * a.o_sh + 4 * c4) * esize<QT>(), O * inv);
+}
+
+// The merge indexed by sequence: grid (batch, num_q_heads), MW waves per query head; workgroup
+// (b, h) finds b's ranges from the plan (every sequence's units before b, i.e. a scan of
+// seq_lens[0 .. b]) and merges them if b is cut.  The host picks MW from the average number of
+// ranges per sequence (one wave when a round covers them, up to four for a few long sequences).
+// Each wave's scan reads and sums all of the batch's lengths, so the cost grows with the batch
+// (B x num_q_heads waves x B / 64 chunks): the host takes it for batches below half the range
+// count, where its grid is also the smaller one.
+constexpr int kMergeChunks = 8;  // 64-sequence chunks of seq_lens a merge wave requests at once
+
+template <int CACHE, int QT, int MW, int HD>
+__global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
+  const int64_t b = blockIdx.x;
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x % kWave;
 
   // The plan (units of the whole batch) and S, the units before sequence b.  Above 64 sequences
   // the lengths of the first kMergeChunks x 64 are requested at once instead of one 64-sequence
@@ -1154,8 +1269,7 @@ __global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
     n = tiles_of(a, readlane64(L0, bl));
   } else {
     int64_t Lc[kMergeChunks];
-#pragma unroll
-    for (int c = 0; c < kMergeChunks; ++c) Lc[c] = c < nch ? seq_len_of(a, c * kWave + lane) : 0;
+    seq_len_chunks(a, 0, lane, Lc);
 #pragma unroll
     for (int c = 0; c < kMergeChunks; ++c) {
       if (c >= nch) break;
@@ -1187,47 +1301,34 @@ __global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
   const int64_t r0 = range_of(plan, first);
   const int64_t r1 = range_of(plan, first + n - 1);
   if (r0 == r1) return;  // finished inside one range by decode_kernel
-  const int64_t nr = r1 - r0 + 1;
-  auto row_of = [&](int64_t c) -> int64_t {  // partial row of range r0 + c, head h
-    return (2 * (r0 + c) + cut_slot(c)) * a.num_q_heads + h;  // tile 0 lies in range r0
-  };
+  merge_records<CACHE, QT, MW, HD>(a, b, h, r0, r1 - r0 + 1);
+}
 
-  constexpr int kStride = RS * MW;
-  float M = -INFINITY, L = 0.0f;
-  f32x4 O = (f32x4)(0.0f);
-  for (int64_t cb = slot; cb < nr; cb += 4 * kStride) {
-    float m[4], l[4];
-    f32x4 v[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t c = cb + u * kStride;
-      if (c < nr) {
-        const int64_t row = row_of(c);
-        m[u] = a.ws_m[row];
-        l[u] = a.ws_l[row];
-        v[u] = *reinterpret_cast<const f32x4*>(a.ws_acc + row * HD + 4 * c4);
-      } else {
-        m[u] = -INFINITY;
-        l[u] = 0.0f;
-        v[u] = (f32x4)(0.0f);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) merge_in(M, L, O, m[u], l[u], v[u]);
-  }
-  s_m[slot][c4] = M;
-  s_l[slot][c4] = L;
-  s_o[slot][c4] = O;
-  __syncthreads();
-  if (threadIdx.x >= C4) return;
-  M = -INFINITY;
-  L = 0.0f;
-  O = (f32x4)(0.0f);
-#pragma unroll
-  for (int k = 0; k < kStride; ++k) merge_in(M, L, O, s_m[k][c4], s_l[k][c4], s_o[k][c4]);
-  const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
-  const float inv = L > 0.0f ? vscale / L : 0.0f;
-  store4<QT>(a.out + (b * a.o_sb + (int64_t)h * a.o_sh + 4 * c4) * esize<QT>(), O * inv);
+// The merge indexed by range: grid (max_ranges, num_q_heads), one wave per query head; workgroup
+// (r0, h) merges the cut sequence that range r0 starts, named by the decode kernel's descriptor
+// with the unit of its last tile, whose range under the plan is its last range r1 (ranges that
+// start none return at once).  No scan of seq_lens: its
+// cost does not grow with the batch (B = 256 x U[1, 2048]: 9.6 -> 5.0 us; B = 128 x U[1, 4096]:
+// 6.2 -> 5.0 us), but every range costs a workgroup, which for batches below half the range
+// count is the larger grid (B = 64 at 256 ranges: 4.6 -> 6.1 us).
+template <int CACHE, int QT, int HD>
+__global__ __launch_bounds__(64) void merge_by_range_kernel(DecodeArgs a) {
+  const int64_t r0 = blockIdx.x;
+  const int64_t b = a.ws_cut[4 * r0];
+  const int64_t last = a.ws_cut[4 * r0 + 1];
+  const Plan plan = unpack_plan(a.ws_cut[4 * r0 + 2], a.ws_cut[4 * r0 + 3]);
+  // b < 0: range r0 starts no cut sequence.  The other bounds hold for every descriptor the
+  // decode kernel writes (a MERGE call that does not follow MAIN on the same workspace reads
+  // whatever is there; they keep it inside the buffers).  One test of all of them (no
+  // short-circuit) has the kernel arguments read with the descriptor, not one dependent load
+  // after another.
+  const int64_t max_ranges = a.max_ranges;
+  if ((b < 0) | (b >= a.batch) | (plan.U <= 0) | (plan.P <= 0) | (plan.P > max_ranges) |
+      (last < 0) | (last >= plan.U) | ((int)blockIdx.y >= a.num_q_heads))
+    return;
+  const int64_t r1 = range_of(plan, last);
+  if (r1 <= r0 || r1 >= max_ranges) return;
+  merge_records<CACHE, QT, 1, HD>(a, b, (int)blockIdx.y, r0, r1 - r0 + 1);
 }
 
 }  // namespace int8kv
@@ -1331,8 +1432,11 @@ int32_t auto_ranges(int32_t num_kv_heads, int64_t cu) {
   return (int32_t)(p < 1 ? 1 : (p > kMaxRangesLimit ? kMaxRangesLimit : p));
 }
 
+// Per range: 2 x num_q_heads partial records (head_dim + 2 floats each) and the 32-byte
+// cut-sequence descriptor.  The records' bytes are a multiple of 16, so the descriptors that
+// follow them stay 16-byte aligned.
 size_t workspace_bytes(int32_t num_q_heads, int32_t ranges, int32_t head_dim) {
-  return (size_t)ranges * 2 * num_q_heads * (head_dim + 2) * sizeof(float);
+  return (size_t)ranges * (2 * num_q_heads * (head_dim + 2) * sizeof(float) + 4 * sizeof(int64_t));
 }
 
 bool aligned16(const void* p, int64_t stride_bytes) {
@@ -1406,16 +1510,21 @@ int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
     if (e != hipSuccess) return (int)e;
   }
   if (flags & INT8KV_DECODE_MERGE) {
-    dim3 grid((unsigned)a.batch, (unsigned)a.num_q_heads);
-    // Ranges per sequence on average; one round of a wave takes 8 of them.
-    const int64_t per_seq = ((int64_t)a.max_ranges + a.batch - 1) / a.batch;
-    const int64_t mw = (per_seq + 7) / 8;
-    if (mw <= 1)
-      hipLaunchKernelGGL((merge_kernel<CACHE, QT, 1, HD>), grid, dim3(kWave), 0, s, a);
-    else if (mw == 2)
-      hipLaunchKernelGGL((merge_kernel<CACHE, QT, 2, HD>), grid, dim3(2 * kWave), 0, s, a);
-    else
-      hipLaunchKernelGGL((merge_kernel<CACHE, QT, 4, HD>), grid, dim3(4 * kWave), 0, s, a);
+    if (a.cut_desc) {  // the smaller grid, and no scan of seq_lens
+      dim3 grid((unsigned)a.max_ranges, (unsigned)a.num_q_heads);
+      hipLaunchKernelGGL((merge_by_range_kernel<CACHE, QT, HD>), grid, dim3(kWave), 0, s, a);
+    } else {
+      dim3 grid((unsigned)a.batch, (unsigned)a.num_q_heads);
+      // Ranges per sequence on average; one round of a wave takes 8 of them.
+      const int64_t per_seq = ((int64_t)a.max_ranges + a.batch - 1) / a.batch;
+      const int64_t mw = (per_seq + 7) / 8;
+      if (mw <= 1)
+        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 1, HD>), grid, dim3(kWave), 0, s, a);
+      else if (mw == 2)
+        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 2, HD>), grid, dim3(2 * kWave), 0, s, a);
+      else
+        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 4, HD>), grid, dim3(4 * kWave), 0, s, a);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }
@@ -1460,8 +1569,8 @@ extern "C" size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num
 // process ends.  In host code `scratch` names a host-side stand-in, not device memory: its
 // device address is looked up once per device with hipGetSymbolAddress and only that address is
 // ever passed to a kernel.  Every call on a GPU shares that GPU's array (calls that overlap on one
-// GPU race); the decode kernel writes every partial record the merge kernel reads, so nothing
-// needs clearing between calls.
+// GPU race); the decode kernel writes every partial record and range descriptor the merge kernel
+// reads, so nothing needs clearing between calls.
 constexpr size_t kScratchBytes = INT8KV_DECODE_SCRATCH_BYTES;
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
@@ -1578,6 +1687,7 @@ int decode_entry(
   a.ws_acc = ws;
   a.ws_m = ws + recs * head_dim;
   a.ws_l = ws + recs * (head_dim + 1);
+  a.ws_cut = reinterpret_cast<int64_t*>(ws + recs * (head_dim + 2));
   a.head_dim = head_dim;
   a.num_blocks = num_blocks;
   a.batch = batch;
@@ -1630,6 +1740,10 @@ int decode_entry(
   // more than 2^25 tiles.
   a.scan32 = (double)kWave * (std::ceil((double)table_width * block_size / a.tile_tokens) +
                               a.seq_cost) < 2147483647.0;
+  // The merge indexed by range (from descriptors the decode kernel then writes) for batches of
+  // at least half the range count, where its grid is the smaller one; below that, the merge
+  // indexed by sequence, and no descriptors.
+  a.cut_desc = 2 * batch >= (int64_t)a.max_ranges;
 
   // Non-temporal K/V loads when the call may stream more than kNonTemporalMinBytes: the most it
   // can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).

@@ -55,17 +55,22 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_workspace_bytes(lib):
-    # 512 ranges x 2 slots x 28 query heads x (128 accumulators + max + sum) fp32
-    assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 512) == 512 * 2 * 28 * 130 * 4
-    assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 1) == 2 * 28 * 130 * 4
+    # per range: 2 slots x 28 query heads x (128 accumulators + max + sum) fp32, and the range's
+    # 32-byte cut-sequence descriptor (sequence id, unit of its last tile, the batch's units)
+    def per_range(hq, d):
+        return 2 * hq * (d + 2) * 4 + 32
+
+    assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 512) == 512 * per_range(28, 128)
+    assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 1) == per_range(28, 128)
+    assert per_range(28, 128) % 16 == 0 and per_range(7, 64) % 16 == 0
     # unsupported sizes -> 0
     for d in (32, 96, 256):  # head_dim: 64 or 128
         assert lib.int8kv_decode_workspace_bytes(28, 4, d, 16, 0) == 0
-    assert lib.int8kv_decode_workspace_bytes(28, 4, 64, 16, 3) == 3 * 2 * 28 * 66 * 4
+    assert lib.int8kv_decode_workspace_bytes(28, 4, 64, 16, 3) == 3 * per_range(28, 64)
     for bs in (8, 24, 48, 1 << 17):  # block size: a power of two in [16, 65536]
         assert lib.int8kv_decode_workspace_bytes(28, 4, 128, bs, 0) == 0
     for bs in (16, 32, 64, 1 << 16):  # the partials do not depend on the block size
-        assert lib.int8kv_decode_workspace_bytes(28, 4, 128, bs, 7) == 7 * 2 * 28 * 130 * 4
+        assert lib.int8kv_decode_workspace_bytes(28, 4, 128, bs, 7) == 7 * per_range(28, 128)
     assert lib.int8kv_decode_workspace_bytes(34, 2, 128, 16, 0) == 0  # group 17
     assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, -1) == 0
     assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, (1 << 20) + 1) == 0

@@ -582,3 +582,44 @@ def test_per_sequence_mode(cuda, hq, hkv, d):
                                   c.block_tables.numpy(), c.seq_lens.numpy())
     _check(_group(q, k16.to(cuda), v16.to(cuda), bt, sl, None, None), ref16,
            f"per-sequence bf16 {hq}/{hkv}/{d}")
+
+
+@pytest.mark.parametrize("ranges", [100, 200, 201, 640])
+def test_merge_grids_on_both_sides_of_the_rule(cuda, ranges):
+    """The merge indexed by range (one workgroup per range, from the decode kernel's cut-sequence
+    descriptors; taken when 2 x batch >= ranges: 100 and 200 ranges for B = 100) and the merge
+    indexed by sequence (a scan of seq_lens; 201 and 640 ranges): oracle parity with sequences
+    cut once, cut many ways (one 6000-token sequence), uncut and empty, INT8 with a bf16 and an
+    fp32 query, quantize_q, and a BF16 cache."""
+    from int8kv import _decode, _lib
+
+    g = torch.Generator().manual_seed(100)
+    lens = torch.randint(1, 400, (100,), generator=g).tolist()
+    lens[50], lens[0], lens[99] = 6000, 2500, 1200
+    for b in (3, 51, 98):
+        lens[b] = 0
+    c = decode_case(lens, seed=101, extra_blocks=5)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+
+    def run(qq, k, v, kscale, vscale, flags=_lib.DECODE_ALL):
+        out = torch.empty_like(qq)
+        _decode.paged_decode(qq, k, v, bt, sl, kscale, vscale, out, ranges, flags, None, 2)
+        torch.cuda.synchronize()
+        return out
+
+    ref = oracle_int8(c)
+    out = run(q, kc, vc, ks, vs)
+    for b in (3, 51, 98):
+        assert (out[b] == 0).all(), b
+    _check(out, ref, f"int8 ranges={ranges}")
+    err, _, _ = metrics(run(q.float(), kc, vc, ks, vs).cpu().numpy(), ref)
+    assert err <= 1e-3, f"fp32 query ranges={ranges}: {err}"
+    ref_q = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                  c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
+                                  quantize_q=True)
+    _check(run(q, kc, vc, ks, vs, _lib.DECODE_ALL | _lib.DECODE_QUANTIZE_Q), ref_q,
+           f"int8 quantize_q ranges={ranges}")
+    k16, v16 = bf16_caches(c)
+    ref16 = O.paged_attention_ref(c.query.float().numpy(), k16.float().numpy(), v16.float().numpy(),
+                                  c.block_tables.numpy(), c.seq_lens.numpy())
+    _check(run(q, k16.to(cuda), v16.to(cuda), None, None), ref16, f"bf16 ranges={ranges}")
