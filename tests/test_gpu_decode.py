@@ -623,3 +623,29 @@ def test_merge_grids_on_both_sides_of_the_rule(cuda, ranges):
     ref16 = O.paged_attention_ref(c.query.float().numpy(), k16.float().numpy(), v16.float().numpy(),
                                   c.block_tables.numpy(), c.seq_lens.numpy())
     _check(run(q, k16.to(cuda), v16.to(cuda), None, None), ref16, f"bf16 ranges={ranges}")
+
+
+def test_paired_ranges_with_the_range_indexed_merge(cuda):
+    """B = 256 at two waves per SIMD (512 ranges for 4 kv heads): the ranges come in pairs (every
+    range holds more than 16 stream units) and 2 x batch = ranges takes the merge indexed by range,
+    whose descriptors carry the paired plan; against the oracle, INT8 with and without quantize_q,
+    with empty sequences at both ends."""
+    g = torch.Generator().manual_seed(256)
+    lens = torch.randint(600, 1500, (256,), generator=g).tolist()
+    lens[0] = lens[255] = lens[128] = 0
+    lens[7] = 9000
+    splits = _pair_splits(4, len(lens))
+    assert splits == 2
+    c = decode_case(lens, seed=256, extra_blocks=5)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    out = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs, num_splits=splits)
+    torch.cuda.synchronize()
+    for b in (0, 128, 255):
+        assert (out[b] == 0).all(), b
+    _check(out, oracle_int8(c), "paired, merge by range")
+    ref_q = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                  c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
+                                  quantize_q=True)
+    out_q = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs, num_splits=splits, quantize_q=True)
+    torch.cuda.synchronize()
+    _check(out_q, ref_q, "paired quantize_q, merge by range")
