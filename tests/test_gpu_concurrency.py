@@ -1,5 +1,6 @@
 """The operators under concurrent host use: two host threads on their own streams, two threads on
-one shared stream, and HIP-graph replays interleaved with eager calls on one stream.
+one shared stream, and HIP-graph replays interleaved with eager calls on one stream (also for the
+merge indexed by range, whose per-range descriptors live in the workspace).
 
 The host paths keep state across calls: the ctypes path caches a decode workspace per (host thread,
 device, stream) and ctypes stride arrays per stride tuple; the extension allocates outputs and workspaces
@@ -140,4 +141,44 @@ def test_graph_replays_interleaved_with_eager_calls(cuda, host_path):
             _check(captured, want, f"replay {rep}")
             _check(before, refs[1], f"eager call before replay {rep}")
             _check(after, refs[0], f"eager call after replay {rep}")
+            _ = (after[0].float() * 2).sum().item()  # eager work and a sync between replays
+
+
+def test_graph_replays_of_the_range_indexed_merge(cuda, host_path):
+    """B = 256 decodes (the merge indexed by range, which reads the per-range descriptors the
+    decode kernel leaves in the workspace): one captured in a graph and replayed between eager
+    calls of another B = 256 decode and of a B = 5 decode (the merge indexed by sequence) on the
+    same stream; every replay and every eager output bit-identical to the call made alone."""
+    g = torch.Generator().manual_seed(77)
+    cases = []
+    for seed, B in ((71, 256), (72, 256), (73, 5)):
+        lens = torch.randint(1, 1200, (B,), generator=g).tolist()
+        lens[B // 2] = 0
+        c = decode_case(lens, seed=seed, extra_blocks=3)
+        q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+        cases.append(lambda q=q, kc=kc, vc=vc, bt=bt, sl=sl, ks=ks, vs=vs:
+                     (int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs),))
+    refs = [job() for job in cases]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for job, ref in zip(cases, refs):
+            _check(job(), ref, "eager warm-up")
+    s.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        captured = cases[0]()
+    with torch.cuda.stream(s):
+        for rep in range(5):
+            captured[0].zero_()
+            before = cases[1]()
+            graph.replay()
+            between = cases[2]()
+            after = cases[1]()
+            s.synchronize()
+            _check(captured, refs[0], f"replay {rep}")
+            _check(before, refs[1], f"eager B=256 before replay {rep}")
+            _check(between, refs[2], f"eager B=5 after replay {rep}")
+            _check(after, refs[1], f"eager B=256 after replay {rep}")
             _ = (after[0].float() * 2).sum().item()  # eager work and a sync between replays
