@@ -184,9 +184,9 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *                 does nothing.  Suited to short sequences (each workgroup streams its whole
  *                 sequence on one compute unit).
  *
- * Supported sizes: head_dim 64 or 128, block_size a power of two in [16, 65536] (16 and 32 are
- * vLLM's usual values), group = num_q_heads / num_kv_heads in [1, 16].  Other sizes return
- * INT8KV_E_SHAPE.
+ * Supported sizes: head_dim 64, 128 or 256 (256 without INT8KV_DECODE_PER_SEQUENCE), block_size
+ * a power of two in [16, 65536] (16 and 32 are vLLM's usual values), group = num_q_heads /
+ * num_kv_heads in [1, 16].  Other sizes return INT8KV_E_SHAPE.
  */
 int int8kv_paged_decode(const void* query, int query_dtype, int64_t batch, int32_t num_q_heads,
                         int32_t head_dim, const int64_t query_strides[3], const void* key_cache,

@@ -62,7 +62,7 @@
 
 namespace int8kv {
 
-// head_dim: 64 or 128 (template parameter HD of the kernels).
+// head_dim: 64, 128 or 256 (template parameter HD of the kernels).
 constexpr int kRows = 16;           // tokens per MFMA row group (half a tile)
 constexpr int kMaxGroup = 16;       // query heads per kv head (MFMA column count)
 constexpr int kChunkTiles = 256;    // tiles whose block ids a wave stages in LDS at a time
@@ -117,7 +117,7 @@ struct DecodeArgs {
   int32_t halves;       // ranges per workgroup (1, or 2 with the paired layout)
   int32_t depth;        // tiles of K/V loads in flight per wave (2, or 4: INT8, one range per WG)
   int32_t group_mode;   // one workgroup per (sequence, kv head), states merged in LDS
-  int32_t head_dim;     // 64 or 128
+  int32_t head_dim;     // 64, 128 or 256
   int32_t scan32;       // a 64-sequence chunk's units fit 32 bits (see units_scan)
   int32_t cut_desc;     // write ws_cut (merge_by_range_kernel follows)
 };
@@ -303,7 +303,7 @@ __device__ __forceinline__ int64_t cut_slot(int64_t first_tile) { return first_t
 
 // ------------------------------------------------------------------------ tile registers
 // Registers holding the K or the V half of one tile (NB 16-token row groups) for one lane, for
-// head_dim HD (64 or 128).
+// head_dim HD (64, 128 or 256).
 //   K: lane (i = lane % 16, g = lane / 16) holds token i of row group s, head_dim elements
 //      [HD/4 g, HD/4 (g + 1)): HD/4 elements, HD E / 64 16-byte pieces.
 //   V: lane (i, g) holds tokens 4g + r (r = 0..3) of row group s, head_dim elements
@@ -405,11 +405,16 @@ __device__ __forceinline__ void store8(char* p, const float (&x)[8]) {
   }
 }
 
-// Stores N (4 or 8) consecutive fp32 values as DT (aligned to N elements).
+// Stores N (4, 8 or 16) consecutive fp32 values as DT (aligned to min(N, 8) elements).
 template <int DT, int N>
 __device__ __forceinline__ void store_n(char* p, const float (&x)[N]) {
-  static_assert(N == 4 || N == 8, "4 or 8 elements");
-  if constexpr (N == 8) {
+  static_assert(N == 4 || N == 8 || N == 16, "4, 8 or 16 elements");
+  if constexpr (N == 16) {
+    const float lo[8] = {x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
+    const float hi[8] = {x[8], x[9], x[10], x[11], x[12], x[13], x[14], x[15]};
+    store8<DT>(p, lo);
+    store8<DT>(p + 8 * esize<DT>(), hi);
+  } else if constexpr (N == 8) {
     store8<DT>(p, x);
   } else if constexpr (DT == kF32) {
     *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
@@ -476,9 +481,13 @@ __device__ __forceinline__ void issue_v(VTile<CACHE, NB, HD>& r, const char* vb,
         r.v[s][rr][0] = x[0];
         r.v[s][rr][1] = x[1];
       } else {
-        const u32x4 x = stream_load<CACHE, NT>(reinterpret_cast<const u32x4*>(rp));
+        static_assert(DW % 4 == 0, "whole 16-byte pieces");
 #pragma unroll
-        for (int k = 0; k < 4; ++k) r.v[s][rr][k] = x[k];
+        for (int h = 0; h < DW / 4; ++h) {
+          const u32x4 x = stream_load<CACHE, NT>(reinterpret_cast<const u32x4*>(rp) + h);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) r.v[s][rr][4 * h + k] = x[k];
+        }
       }
     }
   }
@@ -708,7 +717,7 @@ __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRa
   float s_scale = a.sm_scale_log2e;
   if constexpr (CACHE == kI8) s_scale *= fmaxf(a.k_scale[kvh], 1e-6f);
   if (a.quantize_q) {
-    // absmax over the head's 128 elements: the 4 lanes (li, lg = 0..3) of this head column
+    // absmax over the head's HD elements: the 4 lanes (li, lg = 0..3) of this head column
     amax = fmaxf(amax, __shfl_xor(amax, 16));
     amax = fmaxf(amax, __shfl_xor(amax, 32));
     const float qs = fmaxf(amax / 127.0f, 1e-6f);
@@ -720,7 +729,7 @@ __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRa
           uint32_t word = 0;
 #pragma unroll
           for (int bb = 0; bb < 4; ++bb) {
-            const int d = 16 * ks + 4 * w + bb;  // element of the lane's 32
+            const int d = 16 * ks + 4 * w + bb;  // element of the lane's HD / 4
             const float v = fminf(fmaxf(round_half_away(x[d / 8][d % 8] / qs), -127.0f), 127.0f);
             word |= ((uint32_t)(int32_t)v & 0xffu) << (8 * bb);
           }
@@ -976,16 +985,17 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
 // workgroup (x, y) handles kv head y * W + w % W over stream range x (HALVES = 1), or, with two
 // ranges per workgroup, 2x + w / W (paired ranges) or x + (w / W) grid.x.  DEPTH: tiles in flight
 // per wave (4 only in the one-wave-per-SIMD layout, whose register budget allows it).
-// Register budget: one wave per SIMD (512 registers) for INT8 waves with four tiles in flight and
-// for 16-bit caches, whose 16 KB tiles spilled to scratch under the two-wave budget (their
-// automatic range count is one wave per SIMD anyway); two waves per SIMD otherwise.
-template <int CACHE, int DEPTH>
+// Register budget: one wave per SIMD (512 registers) for INT8 waves with four tiles in flight,
+// for head_dim 256 (twice the tile and accumulator registers) and for 16-bit caches, whose 16 KB
+// tiles spilled to scratch under the two-wave budget (their automatic range count is one wave
+// per SIMD anyway); two waves per SIMD otherwise.
+template <int CACHE, int DEPTH, int HD>
 constexpr int decode_waves_per_eu() {
-  return (DEPTH > 2 || CACHE != kI8) ? 1 : 2;
+  return (DEPTH > 2 || CACHE != kI8 || HD > 128) ? 1 : 2;
 }
 
 template <int CACHE, int QT, bool NT, bool QQ, int HALVES, int HD, int DEPTH>
-__global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<CACHE, DEPTH>()))) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<CACHE, DEPTH, HD>()))) void decode_kernel(DecodeArgs a) {
   __shared__ int32_t s_ids[HALVES * kMaxWavesPerWG][kChunkTiles * tile_blocks<CACHE>()];
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -1452,13 +1462,14 @@ bool block_size_ok(int32_t block_size) {
 
 bool shape_ok(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size) {
   return num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0 &&
-         num_q_heads / num_kv_heads <= kMaxGroup && (head_dim == 64 || head_dim == 128) &&
+         num_q_heads / num_kv_heads <= kMaxGroup &&
+         (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
          block_size_ok(block_size);
 }
 
 template <int CACHE, int QT, bool NT, bool QQ, int HD>
 void launch_main(const DecodeArgs& a, dim3 grid, int W, hipStream_t s) {
-  if constexpr (CACHE == kI8) {
+  if constexpr (CACHE == kI8 && HD <= 128) {  // HD 256: one range per workgroup, two tiles
     if (a.halves == 2) {
       hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 2, HD, 2>), grid, dim3(2 * W * kWave), 0,
                          s, a);
@@ -1478,18 +1489,24 @@ template <int CACHE, int QT, int HD>
 int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
   const int W = waves_per_wg(a.num_kv_heads);
   if (a.group_mode) {  // one kernel; nothing to merge afterwards
-    if (flags & INT8KV_DECODE_MAIN) {
-      dim3 grid((unsigned)a.batch, (unsigned)a.num_kv_heads);
-      if (a.quantize_q)
-        hipLaunchKernelGGL((group_kernel<CACHE, QT, true, HD>), grid, dim3(kGroupWaves * kWave), 0,
-                           s, a);
-      else
-        hipLaunchKernelGGL((group_kernel<CACHE, QT, false, HD>), grid, dim3(kGroupWaves * kWave), 0,
-                           s, a);
-      hipError_t e = hipGetLastError();
-      return e == hipSuccess ? INT8KV_OK : (int)e;
+    // Not at head_dim 256: the 8 waves' states would need 128 KB of LDS (decode_entry rejects
+    // the flag there and the automatic choice skips the layout).
+    if constexpr (HD > 128) {
+      return INT8KV_E_SHAPE;
+    } else {
+      if (flags & INT8KV_DECODE_MAIN) {
+        dim3 grid((unsigned)a.batch, (unsigned)a.num_kv_heads);
+        if (a.quantize_q)
+          hipLaunchKernelGGL((group_kernel<CACHE, QT, true, HD>), grid, dim3(kGroupWaves * kWave),
+                             0, s, a);
+        else
+          hipLaunchKernelGGL((group_kernel<CACHE, QT, false, HD>), grid, dim3(kGroupWaves * kWave),
+                             0, s, a);
+        hipError_t e = hipGetLastError();
+        return e == hipSuccess ? INT8KV_OK : (int)e;
+      }
+      return INT8KV_OK;
     }
-    return INT8KV_OK;
   }
   if (flags & INT8KV_DECODE_MAIN) {
     dim3 grid((unsigned)((a.max_ranges + a.halves - 1) / a.halves), (unsigned)(a.num_kv_heads / W));
@@ -1535,14 +1552,17 @@ template <int CACHE>
 int launch_q(const DecodeArgs& a, int query_dtype, uint32_t flags, bool nt, hipStream_t s) {
   switch (query_dtype) {
     case INT8KV_F32:
-      return a.head_dim == 64 ? launch<CACHE, kF32, 64>(a, flags, nt, s)
-                              : launch<CACHE, kF32, 128>(a, flags, nt, s);
+      return a.head_dim == 64    ? launch<CACHE, kF32, 64>(a, flags, nt, s)
+             : a.head_dim == 128 ? launch<CACHE, kF32, 128>(a, flags, nt, s)
+                                 : launch<CACHE, kF32, 256>(a, flags, nt, s);
     case INT8KV_F16:
-      return a.head_dim == 64 ? launch<CACHE, kF16, 64>(a, flags, nt, s)
-                              : launch<CACHE, kF16, 128>(a, flags, nt, s);
+      return a.head_dim == 64    ? launch<CACHE, kF16, 64>(a, flags, nt, s)
+             : a.head_dim == 128 ? launch<CACHE, kF16, 128>(a, flags, nt, s)
+                                 : launch<CACHE, kF16, 256>(a, flags, nt, s);
     default:
-      return a.head_dim == 64 ? launch<CACHE, kBF16, 64>(a, flags, nt, s)
-                              : launch<CACHE, kBF16, 128>(a, flags, nt, s);
+      return a.head_dim == 64    ? launch<CACHE, kBF16, 64>(a, flags, nt, s)
+             : a.head_dim == 128 ? launch<CACHE, kBF16, 128>(a, flags, nt, s)
+                                 : launch<CACHE, kBF16, 256>(a, flags, nt, s);
   }
 }
 
@@ -1700,8 +1720,10 @@ int decode_entry(
   a.seq_cost = kSeqStartCost;
   a.quantize_q = (flags & INT8KV_DECODE_QUANTIZE_Q) != 0;
   a.group_mode = (flags & INT8KV_DECODE_PER_SEQUENCE) != 0 ||
-                 (automatic && use_per_sequence(cache_dtype == INT8KV_I8, batch, num_kv_heads,
-                                                table_width, block_size, cus));
+                 (automatic && head_dim <= 128 &&
+                  use_per_sequence(cache_dtype == INT8KV_I8, batch, num_kv_heads, table_width,
+                                   block_size, cus));
+  if (a.group_mode && head_dim > 128) return INT8KV_E_SHAPE;
   a.block_shift = __builtin_ctz((unsigned)block_size);
   a.tile_tokens = kRows * (cache_dtype == INT8KV_I8 ? tile_blocks<kI8>() : tile_blocks<kBF16>());
   a.bt_is64 = table_dtype == INT8KV_I64;
@@ -1718,14 +1740,14 @@ int decode_entry(
     const int64_t pair_min = (2LL * cus + wgs_y - 1) / wgs_y;
     const double units_max =
         (double)batch * (std::ceil((double)table_width * block_size / a.tile_tokens) + a.seq_cost);
-    const bool paired = cache_dtype == INT8KV_I8 && num_ranges >= pair_min &&
+    const bool paired = cache_dtype == INT8KV_I8 && head_dim <= 128 && num_ranges >= pair_min &&
                         units_max >= (double)pair_min * min_tiles &&
                         units_max >= (double)pair_min * kPairMinUnits;
     a.halves = paired ? 2 : 1;
     a.pair_min = paired ? (int32_t)pair_min : 0x7fffffff;
     // One wave per SIMD at most (every range's waves resident at once) and long ranges: INT8
     // waves keep four tiles in flight instead of two, the bytes in flight of two waves.
-    a.depth = cache_dtype == INT8KV_I8 && !paired &&
+    a.depth = cache_dtype == INT8KV_I8 && !paired && head_dim <= 128 &&
                       (int64_t)num_ranges * num_kv_heads <= 4LL * cus &&
                       units_max >= (double)kDeepMinUnits * num_ranges
                   ? 4
@@ -1746,10 +1768,13 @@ int decode_entry(
   a.cut_desc = 2 * batch >= (int64_t)a.max_ranges;
 
   // Non-temporal K/V loads when the call may stream more than kNonTemporalMinBytes: the most it
-  // can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).
+  // can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).  Not at
+  // head_dim 256, whose lanes read 64 contiguous bytes of K (like the 16-bit caches at 128): the
+  // hint made those calls 13-15 % slower (Gemma-2-9B shape, B = 64 x U[1, 16384]: 399 vs 347 us).
   const int64_t touch_blocks = batch * table_width < num_blocks ? batch * table_width : num_blocks;
-  const bool nt = (double)touch_blocks * block_size * num_kv_heads * head_dim * ce * 2 >
-                  (double)kNonTemporalMinBytes;
+  const bool nt = head_dim <= 128 &&
+                  (double)touch_blocks * block_size * num_kv_heads * head_dim * ce * 2 >
+                      (double)kNonTemporalMinBytes;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (cache_dtype) {
     case INT8KV_I8:

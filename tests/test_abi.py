@@ -64,8 +64,9 @@ def test_workspace_bytes(lib):
     assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 1) == per_range(28, 128)
     assert per_range(28, 128) % 16 == 0 and per_range(7, 64) % 16 == 0
     # unsupported sizes -> 0
-    for d in (32, 96, 256):  # head_dim: 64 or 128
+    for d in (32, 96, 192, 512):  # head_dim: 64, 128 or 256
         assert lib.int8kv_decode_workspace_bytes(28, 4, d, 16, 0) == 0
+    assert lib.int8kv_decode_workspace_bytes(16, 8, 256, 16, 5) == 5 * per_range(16, 256)
     assert lib.int8kv_decode_workspace_bytes(28, 4, 64, 16, 3) == 3 * per_range(28, 64)
     for bs in (8, 24, 48, 1 << 17):  # block size: a power of two in [16, 65536]
         assert lib.int8kv_decode_workspace_bytes(28, 4, 128, bs, 0) == 0

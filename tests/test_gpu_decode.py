@@ -537,7 +537,7 @@ def test_head_dim_64_paired_regime(cuda):
 def test_unsupported_head_dims_raise(cuda):
     c = decode_case([40], seed=3)
     q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
-    for d in (32, 96, 256):
+    for d in (32, 96, 192, 512):  # 64, 128 and 256 are supported
         kx = torch.zeros(kc.shape[0], 16, 4, d, dtype=torch.int8, device=cuda)
         qx = torch.zeros(q.shape[0], q.shape[1], d, dtype=q.dtype, device=cuda)
         with pytest.raises(RuntimeError, match="E_SHAPE"):
