@@ -1190,9 +1190,9 @@ __device__ __forceinline__ void merge_in(float& M, float& L, f32x4& O, float m, 
 // RS w + rs, RS w + rs + RS MW, ... and folds them in with one online-softmax pass, four ranges'
 // loads in flight at a time (4 RS MW ranges per round for the workgroup); the RS MW running
 // states per column are then merged through LDS.  About 1 + nr / (4 RS MW) dependent memory
-// latencies.  More waves do not help a long sequence: its workgroup streams nr x 512 bytes per
-// query head on one compute unit (one 32k-token sequence cut 256 ways: 8.1 us with four waves,
-// 8.8 with 16).
+// latencies.  Sixteen waves do not help a long sequence (one 32k-token sequence cut 256 ways: 7.2
+// us with eight waves, 8.7 with 16: its workgroup streams nr x 512 bytes per query head on one
+// compute unit).
 template <int CACHE, int QT, int MW, int HD>
 __device__ __forceinline__ void merge_records(const DecodeArgs& a, int64_t b, int h, int64_t r0,
                                               int64_t nr) {
@@ -1252,7 +1252,7 @@ __device__ __forceinline__ void merge_records(const DecodeArgs& a, int64_t b, in
 // The merge indexed by sequence: grid (batch, num_q_heads), MW waves per query head; workgroup
 // (b, h) finds b's ranges from the plan (every sequence's units before b, i.e. a scan of
 // seq_lens[0 .. b]) and merges them if b is cut.  The host picks MW from the average number of
-// ranges per sequence (one wave when a round covers them, up to four for a few long sequences).
+// ranges per sequence (one wave when a round covers them, up to eight for a few long sequences).
 // Each wave's scan reads and sums all of the batch's lengths, so the cost grows with the batch
 // (B x num_q_heads waves x B / 64 chunks): the host takes it for batches below half the range
 // count, where its grid is also the smaller one.
@@ -1532,15 +1532,19 @@ int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
       hipLaunchKernelGGL((merge_by_range_kernel<CACHE, QT, HD>), grid, dim3(kWave), 0, s, a);
     } else {
       dim3 grid((unsigned)a.batch, (unsigned)a.num_q_heads);
-      // Ranges per sequence on average; one round of a wave takes 8 of them.
+      // Ranges per sequence on average; one round of a wave takes 8 of them (at head_dim 128).
+      // Eight waves only above 64 ranges per sequence: one 32k-token sequence cut 256 ways
+      // merges in 7.2 instead of 8.1 us (op 21.2 -> 19.2 us), while at 32 ranges per sequence
+      // the extra waves cost 1 us (B = 8 x 4096).
       const int64_t per_seq = ((int64_t)a.max_ranges + a.batch - 1) / a.batch;
-      const int64_t mw = (per_seq + 7) / 8;
-      if (mw <= 1)
+      if (per_seq <= 8)
         hipLaunchKernelGGL((merge_kernel<CACHE, QT, 1, HD>), grid, dim3(kWave), 0, s, a);
-      else if (mw == 2)
+      else if (per_seq <= 16)
         hipLaunchKernelGGL((merge_kernel<CACHE, QT, 2, HD>), grid, dim3(2 * kWave), 0, s, a);
-      else
+      else if (per_seq <= 64)
         hipLaunchKernelGGL((merge_kernel<CACHE, QT, 4, HD>), grid, dim3(4 * kWave), 0, s, a);
+      else
+        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 8, HD>), grid, dim3(8 * kWave), 0, s, a);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
