@@ -1187,13 +1187,13 @@ __device__ __forceinline__ void merge_in(float& M, float& L, f32x4& O, float m, 
 // r0 .. r0 + nr - 1 (range r0's slot-1 record, the later ranges' slot-0 records) and stores its
 // output row; a workgroup of MW waves.  A wave's lanes are RS = 256 / HD range slots of HD / 4
 // columns: lane (slot rs, column c4) of wave w owns head_dim elements [4 c4, 4 c4 + 4) of ranges
-// RS w + rs, RS w + rs + RS MW, ... and folds them in with one online-softmax pass, four ranges'
-// loads in flight at a time (4 RS MW ranges per round for the workgroup); the RS MW running
-// states per column are then merged through LDS.  About 1 + nr / (4 RS MW) dependent memory
+// RS w + rs, RS w + rs + RS MW, ... and folds them in with one online-softmax pass, FOLD ranges'
+// loads in flight at a time (FOLD RS MW ranges per round for the workgroup); the RS MW running
+// states per column are then merged through LDS.  About 1 + nr / (FOLD RS MW) dependent memory
 // latencies.  Sixteen waves do not help a long sequence (one 32k-token sequence cut 256 ways: 7.2
 // us with eight waves, 8.7 with 16: its workgroup streams nr x 512 bytes per query head on one
 // compute unit).
-template <int CACHE, int QT, int MW, int HD>
+template <int CACHE, int QT, int MW, int HD, int FOLD = 4>
 __device__ __forceinline__ void merge_records(const DecodeArgs& a, int64_t b, int h, int64_t r0,
                                               int64_t nr) {
   constexpr int C4 = HD / 4;      // float4 columns of a head
@@ -1214,14 +1214,14 @@ __device__ __forceinline__ void merge_records(const DecodeArgs& a, int64_t b, in
   constexpr int kStride = RS * MW;
   float M = -INFINITY, L = 0.0f;
   f32x4 O = (f32x4)(0.0f);
-  for (int64_t cb = slot; cb < nr; cb += 4 * kStride) {
-    // All four loads unconditionally (a slot past the last range reads the last range's record
+  for (int64_t cb = slot; cb < nr; cb += FOLD * kStride) {
+    // All FOLD loads unconditionally (a slot past the last range reads the last range's record
     // again and is then ignored): a branch around each load made the compiler wait for the
     // previous ones before issuing the next, one memory latency per range instead of per round.
-    float m[4], l[4];
-    f32x4 v[4];
+    float m[FOLD], l[FOLD];
+    f32x4 v[FOLD];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < FOLD; ++u) {
       const int64_t c = cb + u * kStride;
       const int64_t row = row_of(c < nr ? c : nr - 1);
       m[u] = a.ws_m[row];
@@ -1229,7 +1229,7 @@ __device__ __forceinline__ void merge_records(const DecodeArgs& a, int64_t b, in
       v[u] = *reinterpret_cast<const f32x4*>(a.ws_acc + row * HD + 4 * c4);
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < FOLD; ++u) {
       const bool in = cb + u * kStride < nr;
       merge_in(M, L, O, in ? m[u] : -INFINITY, in ? l[u] : 0.0f, in ? v[u] : (f32x4)(0.0f));
     }
@@ -1258,7 +1258,7 @@ __device__ __forceinline__ void merge_records(const DecodeArgs& a, int64_t b, in
 // count, where its grid is also the smaller one.
 constexpr int kMergeChunks = 8;  // 64-sequence chunks of seq_lens a merge wave requests at once
 
-template <int CACHE, int QT, int MW, int HD>
+template <int CACHE, int QT, int MW, int HD, int FOLD>
 __global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
   const int64_t b = blockIdx.x;
   const int h = blockIdx.y;
@@ -1311,7 +1311,7 @@ __global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
   const int64_t r0 = range_of(plan, first);
   const int64_t r1 = range_of(plan, first + n - 1);
   if (r0 == r1) return;  // finished inside one range by decode_kernel
-  merge_records<CACHE, QT, MW, HD>(a, b, h, r0, r1 - r0 + 1);
+  merge_records<CACHE, QT, MW, HD, FOLD>(a, b, h, r0, r1 - r0 + 1);
 }
 
 // The merge indexed by range: grid (max_ranges, num_q_heads), one wave per query head; workgroup
@@ -1532,19 +1532,22 @@ int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
       hipLaunchKernelGGL((merge_by_range_kernel<CACHE, QT, HD>), grid, dim3(kWave), 0, s, a);
     } else {
       dim3 grid((unsigned)a.batch, (unsigned)a.num_q_heads);
-      // Ranges per sequence on average; one round of a wave takes 8 of them (at head_dim 128).
-      // Eight waves only above 64 ranges per sequence: one 32k-token sequence cut 256 ways
-      // merges in 7.2 instead of 8.1 us (op 21.2 -> 19.2 us), while at 32 ranges per sequence
-      // the extra waves cost 1 us (B = 8 x 4096).
+      // Ranges per sequence on average; one round of a wave takes 2 x FOLD of them (at head_dim
+      // 128).  More waves and eight records per round only for long cut sequences: one 32k-token
+      // sequence cut 256 ways merges in 7.0 us with 8 waves x 8 (8.1 with 4 x 4; op 21.2 -> 18.3
+      // us), B = 4 x 8192 (64 ranges each) gains 0.5 us with 4 x 8, while at 32 ranges per
+      // sequence (B = 8 x 4096) either costs 0.2-1 us.
       const int64_t per_seq = ((int64_t)a.max_ranges + a.batch - 1) / a.batch;
       if (per_seq <= 8)
-        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 1, HD>), grid, dim3(kWave), 0, s, a);
+        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 1, HD, 4>), grid, dim3(kWave), 0, s, a);
       else if (per_seq <= 16)
-        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 2, HD>), grid, dim3(2 * kWave), 0, s, a);
+        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 2, HD, 4>), grid, dim3(2 * kWave), 0, s, a);
+      else if (per_seq <= 32)
+        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 4, HD, 4>), grid, dim3(4 * kWave), 0, s, a);
       else if (per_seq <= 64)
-        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 4, HD>), grid, dim3(4 * kWave), 0, s, a);
+        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 4, HD, 8>), grid, dim3(4 * kWave), 0, s, a);
       else
-        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 8, HD>), grid, dim3(8 * kWave), 0, s, a);
+        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 8, HD, 8>), grid, dim3(8 * kWave), 0, s, a);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
