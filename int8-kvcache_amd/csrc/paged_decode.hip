@@ -1533,18 +1533,25 @@ int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
     } else {
       dim3 grid((unsigned)a.batch, (unsigned)a.num_q_heads);
       // Ranges per sequence on average; one round of a wave takes 2 x FOLD of them (at head_dim
-      // 128).  More waves and eight records per round only for long cut sequences: one 32k-token
-      // sequence cut 256 ways merges in 7.0 us with 8 waves x 8 (8.1 with 4 x 4; op 21.2 -> 18.3
-      // us), B = 4 x 8192 (64 ranges each) gains 0.5 us with 4 x 8, while at 32 ranges per
-      // sequence (B = 8 x 4096) either costs 0.2-1 us.
-      const int64_t per_seq = ((int64_t)a.max_ranges + a.batch - 1) / a.batch;
+      // 128).  More waves and eight records per round only for long cut sequences (MI355X, op =
+      // decode + merge): one 32k-token sequence cut 256 ways 21.3 -> 18.4 us with 8 waves x 8,
+      // B = 1 x 4096 (67 ranges) 12.1 -> 11.6 us and B = 2 x 16384 (128 ranges each) 18.4 ->
+      // 17.4 us with 4 x 8, while at 32-36 ranges per sequence (B = 8 x 4096, 1 x 2048,
+      // 4 x 2048) eight per round costs 0.2-0.3 us and eight waves 1 us.
+      // The estimate is bounded by the longest sequence the table allows: a range holds at least
+      // min_tiles units, so no sequence spans more than units_max / min_tiles + 1 ranges.
+      const int64_t units_max =
+          (((int64_t)a.width << a.block_shift) + a.tile_tokens - 1) / a.tile_tokens + a.seq_cost;
+      const int64_t span_max = (units_max + a.min_tiles - 1) / a.min_tiles + 1;
+      int64_t per_seq = ((int64_t)a.max_ranges + a.batch - 1) / a.batch;
+      if (per_seq > span_max) per_seq = span_max;
       if (per_seq <= 8)
         hipLaunchKernelGGL((merge_kernel<CACHE, QT, 1, HD, 4>), grid, dim3(kWave), 0, s, a);
       else if (per_seq <= 16)
         hipLaunchKernelGGL((merge_kernel<CACHE, QT, 2, HD, 4>), grid, dim3(2 * kWave), 0, s, a);
-      else if (per_seq <= 32)
+      else if (per_seq <= 48)
         hipLaunchKernelGGL((merge_kernel<CACHE, QT, 4, HD, 4>), grid, dim3(4 * kWave), 0, s, a);
-      else if (per_seq <= 64)
+      else if (per_seq <= 128)
         hipLaunchKernelGGL((merge_kernel<CACHE, QT, 4, HD, 8>), grid, dim3(4 * kWave), 0, s, a);
       else
         hipLaunchKernelGGL((merge_kernel<CACHE, QT, 8, HD, 8>), grid, dim3(8 * kWave), 0, s, a);
