@@ -169,9 +169,10 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *                 block size only).
  *                 With num_ranges = 0 and min_tiles = 0, short calls take the per-sequence layout
  *                 below instead (decided from batch, num_kv_heads, table width and block size
- *                 only: at most one workgroup per compute unit, and sequences of at most 512
- *                 tokens, or of at most 2048 (1024 for a 16-bit cache) when the workgroups fill
- *                 half the compute units).
+ *                 only: at most one workgroup per compute unit; for an INT8 cache sequences of at
+ *                 most 768 tokens, or of at most 2048 when there are (tiles per wave - 3) x
+ *                 CUs / 8 workgroups (at most CUs / 2); for a 16-bit cache at most 512 tokens, or
+ *                 1024 when the workgroups fill half the compute units).
  *   flags:        INT8KV_DECODE_ALL normally; MAIN and MERGE separately let a caller time the
  *                 two kernels on their own (MERGE must follow MAIN with identical arguments).
  *                 OR INT8KV_DECODE_QUANTIZE_Q to quantise each (sequence, query head) row of q

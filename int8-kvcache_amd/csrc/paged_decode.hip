@@ -1420,21 +1420,28 @@ int32_t auto_min_tiles(int64_t batch, int64_t table_width, int32_t block_size, i
 }
 
 // The automatic choice of the per-sequence layout (group_kernel), from host-side bounds only:
-// the longest possible sequence (table width x block size) and the workgroup count.  Measured on
-// MI355X (graph replays, uniform lengths): it saves 1.4-1.8 us per call when every wave gets at
-// most 2 tiles (ctx <= 512: 10.4-10.6 vs 11.8-12.4 us at B = 1-8), and 1.8-3.2 us at up to 8
-// tiles per wave once its workgroups fill half the CUs (B=32 x 1024 14.3 vs 17.4 us, B=64 x 1024
-// 18.8 vs 22.0 us, B=32 x 2048 20.3 vs 22.1 us); with fewer workgroups one CU streams a whole
-// sequence and it loses (B=8 x 2048: 19.2 vs 14.4 us).  BF16 tiles hold twice the bytes: up to 4
-// tiles per wave.  At most one workgroup per CU (its LDS holds the 8 waves' states).
+// the longest possible sequence (table width x block size) and the workgroup count.  It saves the
+// merge launch and the range plan, but each workgroup streams a whole sequence on one CU, so it
+// pays when the waves hold few tiles or the workgroups cover enough of the chip.  Measured on
+// MI355X (INT8, graph replays, uniform lengths, op time per call against the range layout): with
+// at most 3 tiles per wave it wins at every batch (ctx 640-768: 10.0-10.6 vs 10.6-12.2 us, B = 1
+// to 16); with 4 from 32 workgroups on (ctx 1024: B = 8 11.77 vs 11.89, B = 16 11.84 vs 13.22,
+// B = 24 12.27 vs 14.44 us; B = 1-4 lose 0.3-0.45 us); with 6 from ~96 (ctx 1536: B = 24 15.58 vs
+// 16.54 us, B = 16 loses 0.9 us); with 8 from 128 (ctx 2048 B = 32 even, B = 16 loses 2.1 us).
+// So an INT8 call needs (tiles per wave - 3) x CUs / 8 workgroups, at most CUs / 2.  BF16 tiles
+// hold twice the bytes: up to 2 tiles per wave at any count, up to 4 from CUs / 2 workgroups.
+// At most one workgroup per CU (its LDS holds the 8 waves' states).
 bool use_per_sequence(bool int8_cache, int64_t batch, int32_t num_kv_heads, int64_t table_width,
                       int32_t block_size, int64_t cu) {
   const int64_t wgs = batch * num_kv_heads;
   if (wgs > cu) return false;
   const double tiles = std::ceil((double)table_width * block_size / 32.0);  // longest sequence
-  const double per_wave = std::ceil(tiles / kGroupWaves);
-  if (per_wave <= 2) return true;
-  return per_wave <= (int8_cache ? 8 : 4) && 2 * wgs >= cu;
+  const int64_t per_wave = (int64_t)std::ceil(tiles / kGroupWaves);
+  if (!int8_cache) return per_wave <= 2 || (per_wave <= 4 && 2 * wgs >= cu);
+  if (per_wave <= 3) return true;
+  if (per_wave > 8) return false;
+  const int64_t need = (per_wave - 3) * cu / 8;
+  return wgs >= (need < cu / 2 ? need : cu / 2);
 }
 
 int32_t auto_ranges(int32_t num_kv_heads, int64_t cu) {
