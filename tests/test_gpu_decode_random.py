@@ -5,8 +5,8 @@ a GQA shape (group 1-16, including one kv head), head_dim 64 or 128, a cache blo
 tokens, the query dtype, the table and length dtypes, the split count, ``impl`` and
 ``quantize_q``, then checks ``int8_paged_attention`` (and, for a third of the cases,
 ``bf16_paged_attention`` on the same K/V in a 16-bit cache) against the fp32 oracle at the
-usual bar (max |diff| <= 2e-2, cosine >= 0.9999; empty sequences exactly zero).  The seeds are
-fixed, so a failure names a reproducible case.
+usual bar (max |diff| <= 2e-2, cosine >= 0.9999; empty sequences exactly zero).  A second set repeats
+the draws at head_dim 256.  The seeds are fixed, so a failure names a reproducible case.
 """
 
 from __future__ import annotations
@@ -70,6 +70,42 @@ def test_random_configuration(cuda, seed):
                                       impl=p["impl"], num_splits=p["splits"])
     torch.cuda.synchronize()
     assert out.dtype == p["qdtype"] and tuple(out.shape) == tuple(q.shape), what
+    ref = O.paged_attention_ref(q.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
+                                quantize_q=p["qq"])
+    _check(out, ref, p["lens"], "int8 " + what)
+    if p["bf16"]:
+        k16, v16 = bf16_caches(c)
+        out16 = int8kv.bf16_paged_attention(q.to(cuda), k16.to(cuda), v16.to(cuda), bt, sl,
+                                            num_splits=p["splits"])
+        torch.cuda.synchronize()
+        ref16 = O.paged_attention_ref(q.float().numpy(), k16.float().numpy(), v16.float().numpy(),
+                                      c.block_tables.numpy(), c.seq_lens.numpy())
+        _check(out16, ref16, p["lens"], "bf16 " + what)
+
+
+@pytest.mark.parametrize("seed", range(100, 110))
+def test_random_configuration_head_dim_256(cuda, seed):
+    """The same random draws at head_dim 256 (GQA groups 1-8 as the Gemma family uses; 16-bit
+    caches with bf16/fp16 queries, the fp32 query being covered in tests/test_gpu_decode_hd256.py)."""
+    p = _draw(seed)
+    hq, hkv = [(16, 8), (16, 16), (8, 1), (8, 2), (32, 4)][seed % 5]
+    p.update(hq=hq, hkv=hkv, d=256)
+    if p["qdtype"] == torch.float32 and p["bf16"]:
+        p["qdtype"] = torch.bfloat16
+    p["lens"] = [min(n, 4000) for n in p["lens"]]
+    what = f"seed {seed}: {p}"
+    c = decode_case(p["lens"], seed=seed, hq=hq, hkv=hkv, head_dim=256, block_size=p["bs"],
+                    randn_kv=p["randn"], extra_blocks=5)
+    q = c.query.to(p["qdtype"])
+    _, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    if p["bt64"]:
+        bt = bt.to(torch.int64)
+    if p["sl64"]:
+        sl = sl.to(torch.int64)
+    out = int8kv.int8_paged_attention(q.to(cuda), kc, vc, bt, sl, ks, vs, quantize_q=p["qq"],
+                                      impl=p["impl"], num_splits=p["splits"])
+    torch.cuda.synchronize()
     ref = O.paged_attention_ref(q.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
                                 c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
                                 quantize_q=p["qq"])
