@@ -3,7 +3,8 @@
 It must give exactly what int8kv_paged_decode gives with a caller's workspace (same kernels,
 same plan, partials in the library's fixed scratch array instead).  Two calls in a row on the
 same GPU, the second with a smaller input, both bit-identical to the workspace entry point and
-within the oracle bar; then the INT8 x BF16-cache and forced-range variants.
+within the oracle bar; then the INT8 x BF16-cache and forced-range variants, the merge indexed by
+range and head_dim 256.
 """
 
 from __future__ import annotations
@@ -76,6 +77,25 @@ def test_bf16_cache_and_paired_ranges(cuda):
     got = _noalloc(q, k16, v16, bt, sl, None, None, torch.full_like(q, float("nan")))
     torch.cuda.synchronize()
     assert torch.equal(got, want), "bf16 cache"
+
+
+def test_range_indexed_merge_and_head_dim_256(cuda):
+    """A batch of at least half the range count (the merge indexed by range, whose per-range
+    descriptors then live in the scratch array too), followed by a smaller head_dim-256 call."""
+    g = torch.Generator().manual_seed(35)
+    lens = torch.randint(1, 900, (160,), generator=g).tolist()
+    lens[7], lens[80] = 6000, 0
+    for case, what in ((decode_case(lens, seed=35, extra_blocks=4), "B=160 range merge"),
+                       (decode_case([700, 3, 2500, 64], seed=36, hq=16, hkv=8, head_dim=256,
+                                    extra_blocks=3), "head_dim 256")):
+        print(f"noalloc: {what}", flush=True)
+        q, kc, vc, bt, sl, ks, vs = to_dev(case, cuda)
+        want = _with_workspace(q, kc, vc, bt, sl, ks, vs)
+        got = _noalloc(q, kc, vc, bt, sl, ks, vs, torch.full_like(q, float("nan")))
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"{what}: outputs differ from int8kv_paged_decode"
+        err, cos, _ = metrics(got.float().cpu().numpy(), oracle_int8(case))
+        assert err <= MAX_ABS and cos >= MIN_COS, (what, err, cos)
 
 
 def test_oversized_request_is_refused(cuda):
