@@ -447,18 +447,32 @@ struct TileRows {
   int32_t row[NB];
 };
 
+// The lane's HD/4 K elements of its token: one contiguous run [HD/4 lg, HD/4 (lg + 1)) up to
+// head_dim 128; at 256 two runs of HD/8, [HD/8 lg, ...) and [HD/2 + HD/8 lg, ...), so that an
+// INT8 lane reads 32 contiguous bytes per run as at 128 (the order the lane's elements are held
+// in, run 0 then run 1, is the order issue_query loads the query in, so the products pair the
+// same elements).
+template <int HD>
+__device__ __forceinline__ constexpr int k_run(int run, int lg) {
+  return HD > 128 ? run * (HD / 2) + lg * (HD / 8) : lg * (HD / 4);
+}
+
 template <int CACHE, int NB, bool NT, int HD>
 __device__ __forceinline__ void issue_k(KTile<CACHE, NB, HD>& r, const char* kb,
                                         const TileRows<NB>& ph, const DecodeArgs& a, int li,
                                         int lg) {
   constexpr int E = esize<CACHE>();
+  constexpr int kRuns = HD > 128 ? 2 : 1;
+  constexpr int PR = k_pieces<CACHE, HD>() / kRuns;  // 16-byte pieces per run
 #pragma unroll
   for (int s = 0; s < NB; ++s) {
-    const u32x4* k4 =
-        reinterpret_cast<const u32x4*>(kb + ph.id[s] * a.kc_sb + (ph.row[s] + li) * a.kc_ss +
-                                       lg * (HD / 4 * E));
+    const char* row = kb + ph.id[s] * a.kc_sb + (ph.row[s] + li) * a.kc_ss;
 #pragma unroll
-    for (int i = 0; i < k_pieces<CACHE, HD>(); ++i) r.k[s][i] = stream_load<CACHE, NT>(&k4[i]);
+    for (int run = 0; run < kRuns; ++run) {
+      const u32x4* k4 = reinterpret_cast<const u32x4*>(row + k_run<HD>(run, lg) * E);
+#pragma unroll
+      for (int i = 0; i < PR; ++i) r.k[s][run * PR + i] = stream_load<CACHE, NT>(&k4[i]);
+    }
   }
 }
 
@@ -649,7 +663,7 @@ __device__ __forceinline__ void tile_pv(VTile<CACHE, NB, HD>& r,
   }
 }
 
-// Raw query row piece of one lane: head li, elements [HD/4 lg, HD/4 (lg + 1)) as loaded.
+// Raw query row piece of one lane: head li, its HD/4 elements (the runs of k_run) as loaded.
 template <int QT, int HD>
 struct QueryRaw {
   u32x4 w[HD / 32];  // HD/4 16-bit elements
@@ -659,19 +673,24 @@ struct QueryRaw<kF32, HD> {
   f32x4 w[HD / 16];  // HD/4 fp32 elements
 };
 
-// Issues the query loads (no wait): lane (head li, group lg) fetches q[b, kvh * G + li,
-// HD/4 lg .. HD/4 (lg + 1) - 1]; lanes of padding heads (li >= G) hold zeros.
+// Issues the query loads (no wait): lane (head li, group lg) fetches the HD/4 elements of
+// q[b, kvh * G + li] whose K elements it holds (the runs of k_run, in the same order); lanes of
+// padding heads (li >= G) hold zeros.
 template <int QT, int HD>
 __device__ __forceinline__ void issue_query(const DecodeArgs& a, int64_t b, int kvh, int li,
                                             int lg, QueryRaw<QT, HD>& raw) {
   constexpr int QE = esize<QT>();
   typedef typename std::remove_reference<decltype(raw.w[0])>::type Vec;
   constexpr int N = sizeof(raw.w) / sizeof(raw.w[0]);
+  constexpr int kRuns = HD > 128 ? 2 : 1;
   if (li < a.group) {
-    const Vec* qp = reinterpret_cast<const Vec*>(
-        a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh + HD / 4 * lg) * QE);
+    const char* qrow = a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh) * QE;
 #pragma unroll
-    for (int i = 0; i < N; ++i) raw.w[i] = qp[i];
+    for (int run = 0; run < kRuns; ++run) {
+      const Vec* qp = reinterpret_cast<const Vec*>(qrow + k_run<HD>(run, lg) * QE);
+#pragma unroll
+      for (int i = 0; i < N / kRuns; ++i) raw.w[run * (N / kRuns) + i] = qp[i];
+    }
   } else {
 #pragma unroll
     for (int i = 0; i < N; ++i) raw.w[i] = (Vec)(0);
@@ -682,7 +701,8 @@ __device__ __forceinline__ float round_half_away(float x) {
   return x >= 0.0f ? floorf(x + 0.5f) : -floorf(-x + 0.5f);
 }
 
-// Builds the Q^T operand (lane (li, lg) holds q[li][HD/4 lg + 8 ks + e]) from the raw loads and
+// Builds the Q^T operand (lane (li, lg) holds element 8 ks + e of its HD/4 query elements, in
+// k_run order: q[li][HD/4 lg + 8 ks + e] up to head_dim 128) from the raw loads and
 // returns the lane's fp32 factor turning MFMA scores into log2-domain logits.
 //   * default: q is scaled by 2^e so the largest |q| of the wave lands in [2^14, 2^15) for fp16
 //     operands (exact for bf16 input, never overflows); bf16 operands take q as is;
@@ -690,7 +710,7 @@ __device__ __forceinline__ float round_half_away(float x) {
 //     q8 = clamp(round_half_away(q / q_scale), -127, 127) (src/triton_ops/int8_paged_attention.py:
 //     137-146, :798-802); the operand is q8 and q_scale joins the score factor.  With QQ the
 //     q8 values are packed as int8 operands instead (q8op[ks] byte e of lane (li, lg) =
-//     q8[li][HD/4 lg + 16 ks + e], matching the int8 K bytes the lane holds).
+//     lane element 16 ks + e of q8, matching the int8 K bytes the lane holds).
 template <int CACHE, int QT, bool QQ, int HD>
 __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRaw<QT, HD>& raw,
                                               int kvh, typename MfmaOp<CACHE>::T (&qop)[HD / 32],
@@ -1789,13 +1809,14 @@ int decode_entry(
   a.cut_desc = 2 * batch >= (int64_t)a.max_ranges;
 
   // Non-temporal K/V loads when the call may stream more than kNonTemporalMinBytes: the most it
-  // can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).  Not at
-  // head_dim 256, whose lanes read 64 contiguous bytes of K (like the 16-bit caches at 128): the
-  // hint made those calls 13-15 % slower (Gemma-2-9B shape, B = 64 x U[1, 16384]: 399 vs 347 us).
+  // can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).  Only
+  // INT8 caches use the hint (stream_load); their lanes read K in 32-byte runs at every head_dim
+  // (k_run).  With one 64-byte run per lane at head_dim 256 the hint had made those calls 13-15 %
+  // slower; with two 32-byte runs it makes them 10 % faster (Gemma-2-9B shape, B = 64 x
+  // U[1, 16384]: 347 -> 313 us, 6.44 TB/s).
   const int64_t touch_blocks = batch * table_width < num_blocks ? batch * table_width : num_blocks;
-  const bool nt = head_dim <= 128 &&
-                  (double)touch_blocks * block_size * num_kv_heads * head_dim * ce * 2 >
-                      (double)kNonTemporalMinBytes;
+  const bool nt = (double)touch_blocks * block_size * num_kv_heads * head_dim * ce * 2 >
+                  (double)kNonTemporalMinBytes;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (cache_dtype) {
     case INT8KV_I8:
