@@ -119,6 +119,9 @@ int int8kv_dynamic_cache_write(const void* key, const void* value, int src_dtype
  * Automatic range count of int8kv_paged_decode (num_ranges = 0) on the current device: the
  * token stream of a decode call is cut into at most this many equal ranges, one wave per SIMD
  * (4 x compute units / num_kv_heads: 256 for 4 kv heads on MI355X).
+ * At head_dim 64 with an even num_kv_heads and at most 8 query heads per kv head, the decode
+ * takes kv heads in pairs (one wave per pair) and its automatic count is that of
+ * num_kv_heads / 2 (int8kv_decode_workspace_bytes(..., 0) accounts for it).
  */
 int32_t int8kv_decode_auto_ranges(int32_t num_kv_heads);
 

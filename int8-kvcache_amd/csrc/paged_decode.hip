@@ -120,6 +120,7 @@ struct DecodeArgs {
   int32_t head_dim;     // 64, 128 or 256
   int32_t scan32;       // a 64-sequence chunk's units fit 32 bits (see units_scan)
   int32_t cut_desc;     // write ws_cut (merge_by_range_kernel follows)
+  int32_t kv_pair;      // head_dim 64: each wave takes kv heads 2k and 2k + 1 as one 128-wide head
 };
 
 // ------------------------------------------------------------------------ wave utilities
@@ -676,13 +677,30 @@ struct QueryRaw<kF32, HD> {
 // Issues the query loads (no wait): lane (head li, group lg) fetches the HD/4 elements of
 // q[b, kvh * G + li] whose K elements it holds (the runs of k_run, in the same order); lanes of
 // padding heads (li >= G) hold zeros.
-template <int QT, int HD>
+//   PAIR (head_dim 64 as kv heads kvh, kvh + 1 side by side, HD = 128): column li < 2G is query
+//   head kvh G + li; its 64 elements go to the lanes of its own kv head's half (lg / 2 = 0 for
+//   li < G, 1 above) and the other half's lanes hold zeros, so each column's scores use only its
+//   own kv head's K elements.
+template <int QT, int HD, bool PAIR = false>
 __device__ __forceinline__ void issue_query(const DecodeArgs& a, int64_t b, int kvh, int li,
                                             int lg, QueryRaw<QT, HD>& raw) {
   constexpr int QE = esize<QT>();
   typedef typename std::remove_reference<decltype(raw.w[0])>::type Vec;
   constexpr int N = sizeof(raw.w) / sizeof(raw.w[0]);
   constexpr int kRuns = HD > 128 ? 2 : 1;
+  if constexpr (PAIR) {
+    static_assert(HD == 128, "pairs of 64-wide kv heads");
+    if (li < 2 * a.group && (lg >> 1) == (li >= a.group ? 1 : 0)) {
+      const Vec* qp = reinterpret_cast<const Vec*>(
+          a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh + 32 * (lg & 1)) * QE);
+#pragma unroll
+      for (int i = 0; i < N; ++i) raw.w[i] = qp[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) raw.w[i] = (Vec)(0);
+    }
+    return;
+  }
   if (li < a.group) {
     const char* qrow = a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh) * QE;
 #pragma unroll
@@ -711,7 +729,7 @@ __device__ __forceinline__ float round_half_away(float x) {
 //     137-146, :798-802); the operand is q8 and q_scale joins the score factor.  With QQ the
 //     q8 values are packed as int8 operands instead (q8op[ks] byte e of lane (li, lg) =
 //     lane element 16 ks + e of q8, matching the int8 K bytes the lane holds).
-template <int CACHE, int QT, bool QQ, int HD>
+template <int CACHE, int QT, bool QQ, int HD, bool PAIR = false>
 __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRaw<QT, HD>& raw,
                                               int kvh, typename MfmaOp<CACHE>::T (&qop)[HD / 32],
                                               typename MfmaOp<CACHE>::T (&qlo)[HD / 32],
@@ -735,7 +753,11 @@ __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRa
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[ks][e]));
   float s_scale = a.sm_scale_log2e;
-  if constexpr (CACHE == kI8) s_scale *= fmaxf(a.k_scale[kvh], 1e-6f);
+  if constexpr (CACHE == kI8) {
+    // PAIR: the lane's column belongs to kv head kvh + 1 from column G on.
+    const int kv = PAIR ? kvh + ((int)(__lane_id() & 15) >= a.group ? 1 : 0) : kvh;
+    s_scale *= fmaxf(a.k_scale[kv], 1e-6f);
+  }
   if (a.quantize_q) {
     // absmax over the head's HD elements: the 4 lanes (li, lg = 0..3) of this head column
     amax = fmaxf(amax, __shfl_xor(amax, 16));
@@ -829,7 +851,8 @@ __device__ __forceinline__ void write_zero_rows(const DecodeArgs& a, int64_t b, 
 // DEPTH: tiles of K/V loads kept in flight (register buffers).  GROUP: leave the state
 // (running max, sum, accumulators) in this wave's LDS slot (g_acc [HD/4][64], g_m, g_l [16])
 // for the workgroup to merge, instead of an output row or a partial record.
-template <int CACHE, int QT, bool NT, bool QQ, int HD, int DEPTH, bool GROUP = false>
+template <int CACHE, int QT, bool NT, bool QQ, int HD, int DEPTH, bool GROUP = false,
+          bool PAIR = false>
 __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, int64_t b,
                                             int64_t L, int kvh, int64_t ta, int64_t tb,
                                             bool full, int64_t rec, int lane,
@@ -902,10 +925,9 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   float s_scale;
   {
     QueryRaw<QT, HD> qraw;
-    issue_query<QT, HD>(a, b, kvh, li, lg, qraw);
+    issue_query<QT, HD, PAIR>(a, b, kvh, li, lg, qraw);
     chunk_prologue();
-    s_scale = finish_query<CACHE, QT, QQ, HD>(a, qraw, kvh, qop,
-                                              qlo, q8op);
+    s_scale = finish_query<CACHE, QT, QQ, HD, PAIR>(a, qraw, kvh, qop, qlo, q8op);
   }
 
   // Tile t + d (buffer d): scores, refill K with tile t + d + DEPTH, P*V, refill V.  refill is a
@@ -960,6 +982,44 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
 
   l_part += __shfl_xor(l_part, 16);
   l_part += __shfl_xor(l_part, 32);
+  if constexpr (PAIR) {
+    // Columns li < 2G; a column's rows are its own kv head's half of the 128 (lg / 2 = 0 for
+    // li < G, 1 above: real head_dim elements 32 (lg % 2) + 8 rr + dt); the other half's rows
+    // mixed this column's probabilities with the other kv head's V and are dropped.
+    static_assert(!GROUP && HD == 128, "pairs of 64-wide kv heads, range layout only");
+    const int upper = li >= G ? 1 : 0;
+    if (li >= 2 * G) return;
+    const int h = kvh * G + li;
+    const int64_t row = rec * a.num_q_heads + h;
+    if (!full && lg == 2 * upper) {
+      a.ws_m[row] = m_run;
+      a.ws_l[row] = l_part;
+    }
+    if ((lg >> 1) != upper) return;
+    const int d0 = 32 * (lg & 1);
+    if (full) {
+      const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh + upper], 1e-6f) : 1.0f;
+      const float inv = l_part > 0.0f ? vscale / l_part : 0.0f;
+      char* op = a.out + (b * a.o_sb + (int64_t)h * a.o_sh) * esize<QT>();
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        float o[8];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[dt] = acc[dt][rr] * inv;
+        store_n<QT, 8>(op + (d0 + 8 * rr) * esize<QT>(), o);
+      }
+    } else {
+      char* pp = reinterpret_cast<char*>(a.ws_acc + row * 64);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        float o[8];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[dt] = acc[dt][rr];
+        store_n<kF32, 8>(pp + (d0 + 8 * rr) * 4, o);
+      }
+    }
+    return;
+  }
   if (li >= G) return;
   if constexpr (GROUP) {
 #pragma unroll
@@ -1014,13 +1074,14 @@ constexpr int decode_waves_per_eu() {
   return (DEPTH > 2 || CACHE != kI8 || HD > 128) ? 1 : 2;
 }
 
-template <int CACHE, int QT, bool NT, bool QQ, int HALVES, int HD, int DEPTH>
+template <int CACHE, int QT, bool NT, bool QQ, int HALVES, int HD, int DEPTH, bool PAIR = false>
 __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<CACHE, DEPTH, HD>()))) void decode_kernel(DecodeArgs a) {
   __shared__ int32_t s_ids[HALVES * kMaxWavesPerWG][kChunkTiles * tile_blocks<CACHE>()];
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int W = blockDim.x / (HALVES * kWave);  // kv heads per workgroup
-  const int kvh = blockIdx.y * W + (HALVES == 1 ? wave : wave % W);
+  const int kvh = blockIdx.y * W + (HALVES == 1 ? wave : wave % W);  // the wave's (pair of) kv heads
+  const int kv0 = PAIR ? 2 * kvh : kvh;  // first kv head of the wave
   const int half = HALVES == 1 ? 0 : wave / W;
 
   const int64_t L0 = seq_len_of(a, lane);
@@ -1063,7 +1124,12 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(de
       while (zmask) {
         const int j = __builtin_ctzll(zmask);
         zmask &= zmask - 1;
-        write_zero_rows<QT, HD>(a, base + j, kvh, lane);
+        if constexpr (PAIR) {
+          write_zero_rows<QT, 64>(a, base + j, kv0, lane);
+          write_zero_rows<QT, 64>(a, base + j, kv0 + 1, lane);
+        } else {
+          write_zero_rows<QT, HD>(a, base + j, kvh, lane);
+        }
       }
       // Sequences whose tiles (units past the start cost) meet [u0, u1).
       uint64_t mask = __ballot(n > 0 && incl > u0 && excl + a.seq_cost < u1);
@@ -1081,8 +1147,8 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(de
           a.ws_cut[4 * r] = base + j;
           a.ws_cut[4 * r + 1] = first + nb - 1;
         }
-        run_segment<CACHE, QT, NT, QQ, HD, DEPTH>(a, s_ids[wave], base + j, Lb, kvh, ta, te, full,
-                               2 * r + cut_slot(ta), lane);
+        run_segment<CACHE, QT, NT, QQ, HD, DEPTH, false, PAIR>(a, s_ids[wave], base + j, Lb, kv0, ta,
+                                                               te, full, 2 * r + cut_slot(ta), lane);
       }
     }
     if (chunk_end >= u1 && !last_range) break;
@@ -1464,6 +1530,14 @@ bool use_per_sequence(bool int8_cache, int64_t batch, int32_t num_kv_heads, int6
   return wgs >= (need < cu / 2 ? need : cu / 2);
 }
 
+// head_dim 64 with an even kv-head count and GQA groups of at most 8: a wave can take two kv
+// heads as one 128-wide head (their rows sit side by side in the cache when the head stride is
+// head_dim), 2 G <= 16 query heads in the MFMA columns.  Loads then have HD = 128's shape
+// (32-byte K runs, 8-byte V pieces per lane and token row) instead of 16- and 4-byte ones.
+bool kv_pair_shape(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim) {
+  return head_dim == 64 && num_kv_heads % 2 == 0 && num_q_heads / num_kv_heads <= 8;
+}
+
 int32_t auto_ranges(int32_t num_kv_heads, int64_t cu) {
   const int64_t p = cu * kWavesPerCU / num_kv_heads;
   return (int32_t)(p < 1 ? 1 : (p > kMaxRangesLimit ? kMaxRangesLimit : p));
@@ -1494,27 +1568,48 @@ bool shape_ok(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32
          block_size_ok(block_size);
 }
 
-template <int CACHE, int QT, bool NT, bool QQ, int HD>
+template <int CACHE, int QT, bool NT, bool QQ, int HD, bool PAIR = false>
 void launch_main(const DecodeArgs& a, dim3 grid, int W, hipStream_t s) {
   if constexpr (CACHE == kI8 && HD <= 128) {  // HD 256: one range per workgroup, two tiles
     if (a.halves == 2) {
-      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 2, HD, 2>), grid, dim3(2 * W * kWave), 0,
+      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 2, HD, 2, PAIR>), grid, dim3(2 * W * kWave), 0,
                          s, a);
       return;
     }
     // Four tiles in flight leave no registers for an fp32 query's lo operands: two for those.
     if (a.depth == 4 && QT != kF32) {
-      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 4>), grid, dim3(W * kWave), 0, s,
+      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 4, PAIR>), grid, dim3(W * kWave), 0, s,
                          a);
       return;
     }
   }
-  hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 2>), grid, dim3(W * kWave), 0, s, a);
+  hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 2, PAIR>), grid, dim3(W * kWave), 0, s, a);
+}
+
+// The range decode kernel for one call: kv-head pairs at head_dim 64 run the HD = 128 kernel
+// with PAIR (see DecodeArgs::kv_pair).
+template <int CACHE, int QT, int HD, bool PAIR>
+void launch_ranges(const DecodeArgs& a, dim3 grid, int W, bool nt, hipStream_t s) {
+  constexpr int KH = PAIR ? 128 : HD;
+  // INT8 caches: non-temporal loads for large pools, int8 scores for a quantised query.
+  if constexpr (CACHE == kI8) {
+    if (nt && a.quantize_q)
+      launch_main<CACHE, QT, true, true, KH, PAIR>(a, grid, W, s);
+    else if (nt)
+      launch_main<CACHE, QT, true, false, KH, PAIR>(a, grid, W, s);
+    else if (a.quantize_q)
+      launch_main<CACHE, QT, false, true, KH, PAIR>(a, grid, W, s);
+    else
+      launch_main<CACHE, QT, false, false, KH, PAIR>(a, grid, W, s);
+  } else {
+    launch_main<CACHE, QT, false, false, KH, PAIR>(a, grid, W, s);
+  }
 }
 
 template <int CACHE, int QT, int HD>
 int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
-  const int W = waves_per_wg(a.num_kv_heads);
+  const int32_t hv = a.kv_pair ? a.num_kv_heads / 2 : a.num_kv_heads;  // kv heads (pairs) per range
+  const int W = waves_per_wg(a.group_mode ? a.num_kv_heads : hv);
   if (a.group_mode) {  // one kernel; nothing to merge afterwards
     // Not at head_dim 256: the 8 waves' states would need 128 KB of LDS (decode_entry rejects
     // the flag there and the automatic choice skips the layout).
@@ -1536,19 +1631,14 @@ int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
     }
   }
   if (flags & INT8KV_DECODE_MAIN) {
-    dim3 grid((unsigned)((a.max_ranges + a.halves - 1) / a.halves), (unsigned)(a.num_kv_heads / W));
-    // INT8 caches: non-temporal loads for large pools, int8 scores for a quantised query.
-    if constexpr (CACHE == kI8) {
-      if (nt && a.quantize_q)
-        launch_main<CACHE, QT, true, true, HD>(a, grid, W, s);
-      else if (nt)
-        launch_main<CACHE, QT, true, false, HD>(a, grid, W, s);
-      else if (a.quantize_q)
-        launch_main<CACHE, QT, false, true, HD>(a, grid, W, s);
+    dim3 grid((unsigned)((a.max_ranges + a.halves - 1) / a.halves), (unsigned)(hv / W));
+    if constexpr (HD == 64) {
+      if (a.kv_pair)
+        launch_ranges<CACHE, QT, HD, true>(a, grid, W, nt, s);
       else
-        launch_main<CACHE, QT, false, false, HD>(a, grid, W, s);
+        launch_ranges<CACHE, QT, HD, false>(a, grid, W, nt, s);
     } else {
-      launch_main<CACHE, QT, false, false, HD>(a, grid, W, s);
+      launch_ranges<CACHE, QT, HD, false>(a, grid, W, nt, s);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
@@ -1620,7 +1710,10 @@ extern "C" size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num
   if (!shape_ok(num_q_heads, num_kv_heads, head_dim, block_size) || num_ranges < 0 ||
       num_ranges > kMaxRangesLimit)
     return 0;
-  if (num_ranges == 0) num_ranges = auto_ranges(num_kv_heads, cu_count());
+  if (num_ranges == 0)
+    num_ranges = auto_ranges(
+        kv_pair_shape(num_q_heads, num_kv_heads, head_dim) ? num_kv_heads / 2 : num_kv_heads,
+        cu_count());
   return workspace_bytes(num_q_heads, num_ranges, head_dim);
 }
 
@@ -1710,7 +1803,10 @@ int decode_entry(
 
   const bool automatic = num_ranges == 0 && min_tiles == 0;
   const int64_t cus = cu_count();
-  if (num_ranges == 0) num_ranges = auto_ranges(num_kv_heads, cus);
+  const bool kv_pair_ok = kv_pair_shape(num_q_heads, num_kv_heads, head_dim) &&
+                          key_cache_strides[2] == head_dim && value_cache_strides[2] == head_dim;
+  const int32_t wave_heads = kv_pair_ok ? num_kv_heads / 2 : num_kv_heads;  // per range
+  if (num_ranges == 0) num_ranges = auto_ranges(wave_heads, cus);
   if (min_tiles == 0) min_tiles = auto_min_tiles(batch, table_width, block_size, num_ranges);
   const size_t need = workspace_bytes(num_q_heads, num_ranges, head_dim);
   if (from_scratch) {
@@ -1765,6 +1861,7 @@ int decode_entry(
                   use_per_sequence(cache_dtype == INT8KV_I8, batch, num_kv_heads, table_width,
                                    block_size, cus));
   if (a.group_mode && head_dim > 128) return INT8KV_E_SHAPE;
+  a.kv_pair = kv_pair_ok && !a.group_mode;
   a.block_shift = __builtin_ctz((unsigned)block_size);
   a.tile_tokens = kRows * (cache_dtype == INT8KV_I8 ? tile_blocks<kI8>() : tile_blocks<kBF16>());
   a.bt_is64 = table_dtype == INT8KV_I64;
@@ -1777,7 +1874,7 @@ int decode_entry(
     // and that can fill it: P >= pair_min needs at least pair_min * min_tiles units, bounded
     // here by batch x (longest possible sequence).  16-bit caches (1 % slower paired) keep one
     // range per workgroup.
-    const int64_t wgs_y = num_kv_heads / waves_per_wg(num_kv_heads);  // workgroups per range
+    const int64_t wgs_y = wave_heads / waves_per_wg(wave_heads);  // workgroups per range
     const int64_t pair_min = (2LL * cus + wgs_y - 1) / wgs_y;
     const double units_max =
         (double)batch * (std::ceil((double)table_width * block_size / a.tile_tokens) + a.seq_cost);
@@ -1789,7 +1886,7 @@ int decode_entry(
     // One wave per SIMD at most (every range's waves resident at once) and long ranges: INT8
     // waves keep four tiles in flight instead of two, the bytes in flight of two waves.
     a.depth = cache_dtype == INT8KV_I8 && !paired && head_dim <= 128 &&
-                      (int64_t)num_ranges * num_kv_heads <= 4LL * cus &&
+                      (int64_t)num_ranges * wave_heads <= 4LL * cus &&
                       units_max >= (double)kDeepMinUnits * num_ranges
                   ? 4
                   : 2;
