@@ -171,11 +171,13 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *                 one sequence into more than 128 ranges; decided from batch, table width and
  *                 block size only).
  *                 With num_ranges = 0 and min_tiles = 0, short calls take the per-sequence layout
- *                 below instead (decided from batch, num_kv_heads, table width and block size
- *                 only: at most one workgroup per compute unit; for an INT8 cache sequences of at
- *                 most 768 tokens, or of at most 2048 when there are (tiles per wave - 3) x
- *                 CUs / 8 workgroups (at most CUs / 2); for a 16-bit cache at most 512 tokens, or
- *                 1024 when the workgroups fill half the compute units).
+ *                 below instead (decided from head_dim, batch, num_kv_heads, table width and
+ *                 block size only, with tokens = table width x block size and W = batch x
+ *                 num_kv_heads workgroups; head_dim 128, INT8 cache: W <= CUs, and tokens <= 768,
+ *                 or tokens <= 2048 with W >= (tiles per wave - 3) x CUs / 8, at most CUs / 2;
+ *                 head_dim 128, 16-bit cache: W <= 3 CUs, and tokens <= 512, or tokens <= 1024
+ *                 with W >= CUs / 2; head_dim 64: W <= 4 CUs, and for an INT8 cache tokens <=
+ *                 1536, or tokens <= 2048 with W >= CUs / 8; for a 16-bit cache tokens <= 1024).
  *   flags:        INT8KV_DECODE_ALL normally; MAIN and MERGE separately let a caller time the
  *                 two kernels on their own (MERGE must follow MAIN with identical arguments).
  *                 OR INT8KV_DECODE_QUANTIZE_Q to quantise each (sequence, query head) row of q

@@ -1514,16 +1514,29 @@ int32_t auto_min_tiles(int64_t batch, int64_t table_width, int32_t block_size, i
 // to 16); with 4 from 32 workgroups on (ctx 1024: B = 8 11.77 vs 11.89, B = 16 11.84 vs 13.22,
 // B = 24 12.27 vs 14.44 us; B = 1-4 lose 0.3-0.45 us); with 6 from ~96 (ctx 1536: B = 24 15.58 vs
 // 16.54 us, B = 16 loses 0.9 us); with 8 from 128 (ctx 2048 B = 32 even, B = 16 loses 2.1 us).
-// So an INT8 call needs (tiles per wave - 3) x CUs / 8 workgroups, at most CUs / 2.  BF16 tiles
-// hold twice the bytes: up to 2 tiles per wave at any count, up to 4 from CUs / 2 workgroups.
-// At most one workgroup per CU (its LDS holds the 8 waves' states).
-bool use_per_sequence(bool int8_cache, int64_t batch, int32_t num_kv_heads, int64_t table_width,
-                      int32_t block_size, int64_t cu) {
+// So an INT8 call needs (tiles per wave - 3) x CUs / 8 workgroups, at most CUs / 2, and past one
+// workgroup per CU the two layouts trade places by +-3 us (B = 32-192, 28/4 and 32/8 heads), so
+// it stops there.  BF16 tiles hold twice the bytes: up to 2 tiles per wave at any count, up to 4
+// from CUs / 2 workgroups, and it keeps winning up to 3 workgroups per CU (28/4 heads: B = 128 x
+// 512 25.8 vs 29.9 us, B = 192 x 1024 78.3 vs 82.4; at 4 per CU it loses, 50.9 vs 46.7).
+// At head_dim 64 the workgroup's LDS state is half as large and the range layout's 64-wide loads
+// are shorter (32/8 heads): INT8 wins up to 6 tiles per wave at any count (B = 1 x 1536 10.6 vs
+// 12.5 us), up to 8 from CUs / 8 workgroups (B = 4 x 2048 12.9 vs 13.3, B = 128 x 2048 45.5 vs
+// 56.8), and up to 4 workgroups per CU (B = 128 x 1024 26.4 vs 32.6; at 6 per CU with 4 tiles
+// per wave 54.3 vs 45.0, at 8 per CU it loses at every length); BF16 wins up to 4 tiles per wave
+// at any count (B = 8 x 1024 9.5 vs 12.8 us) and loses from 6 on.
+bool use_per_sequence(bool int8_cache, int32_t head_dim, int64_t batch, int32_t num_kv_heads,
+                      int64_t table_width, int32_t block_size, int64_t cu) {
   const int64_t wgs = batch * num_kv_heads;
-  if (wgs > cu) return false;
   const double tiles = std::ceil((double)table_width * block_size / 32.0);  // longest sequence
   const int64_t per_wave = (int64_t)std::ceil(tiles / kGroupWaves);
-  if (!int8_cache) return per_wave <= 2 || (per_wave <= 4 && 2 * wgs >= cu);
+  if (head_dim == 64) {
+    if (wgs > 4 * cu) return false;
+    if (!int8_cache) return per_wave <= 4;
+    return per_wave <= 6 || (per_wave <= 8 && wgs >= cu / 8);
+  }
+  if (!int8_cache) return wgs <= 3 * cu && (per_wave <= 2 || (per_wave <= 4 && 2 * wgs >= cu));
+  if (wgs > cu) return false;
   if (per_wave <= 3) return true;
   if (per_wave > 8) return false;
   const int64_t need = (per_wave - 3) * cu / 8;
@@ -1858,8 +1871,8 @@ int decode_entry(
   a.quantize_q = (flags & INT8KV_DECODE_QUANTIZE_Q) != 0;
   a.group_mode = (flags & INT8KV_DECODE_PER_SEQUENCE) != 0 ||
                  (automatic && head_dim <= 128 &&
-                  use_per_sequence(cache_dtype == INT8KV_I8, batch, num_kv_heads, table_width,
-                                   block_size, cus));
+                  use_per_sequence(cache_dtype == INT8KV_I8, head_dim, batch, num_kv_heads,
+                                   table_width, block_size, cus));
   if (a.group_mode && head_dim > 128) return INT8KV_E_SHAPE;
   a.kv_pair = kv_pair_ok && !a.group_mode;
   a.block_shift = __builtin_ctz((unsigned)block_size);

@@ -649,3 +649,54 @@ def test_paired_ranges_with_the_range_indexed_merge(cuda):
     out_q = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs, num_splits=splits, quantize_q=True)
     torch.cuda.synchronize()
     _check(out_q, ref_q, "paired quantize_q, merge by range")
+
+
+# (head_dim, q heads, kv heads, cache, batch, table width in 16-token blocks, per-sequence?) on a
+# 256-CU MI355X: the automatic choice's thresholds on both sides.
+AUTO_LAYOUT_POINTS = [
+    (64, 32, 8, "int8", 96, 64, True),      # 3 workgroups per CU, 4 tiles per wave
+    (64, 32, 8, "int8", 160, 64, False),    # 5 per CU: past the 4-per-CU cap
+    (64, 32, 8, "int8", 1, 96, True),       # 6 tiles per wave at any count
+    (64, 32, 8, "int8", 2, 128, False),     # 8 tiles per wave: needs CUs / 8 = 32 workgroups
+    (64, 32, 8, "int8", 4, 128, True),
+    (64, 32, 8, "int8", 64, 160, False),    # 10 tiles per wave
+    (64, 32, 8, "bf16", 8, 64, True),       # 16-bit cache: up to 4 tiles per wave
+    (64, 32, 8, "bf16", 8, 96, False),
+    (128, 28, 4, "bf16", 128, 32, True),    # 16-bit cache at 128: up to 3 workgroups per CU
+    (128, 28, 4, "bf16", 200, 32, False),
+    (128, 28, 4, "int8", 96, 32, False),    # INT8 at 128: at most one workgroup per CU
+    (128, 28, 4, "int8", 48, 32, True),
+]
+
+
+@pytest.mark.parametrize("d,hq,hkv,cache,batch,width,per_seq", AUTO_LAYOUT_POINTS)
+def test_automatic_layout_choice(cuda, d, hq, hkv, cache, batch, width, per_seq):
+    """The automatic call (num_ranges = 0, min_tiles = 0) takes the per-sequence layout exactly
+    where the rule says: its output is then bit-identical to the forced per-sequence layout's
+    (and differs from it otherwise, the range layout summing in another order); both match the
+    oracle.  Ragged lengths up to the table width, one empty sequence."""
+    if torch.cuda.get_device_properties(cuda).multi_processor_count != 256:
+        pytest.skip("the thresholds are stated for 256 compute units")
+    g = torch.Generator().manual_seed(batch * width + d)
+    lens = torch.randint(1, width * 16 + 1, (batch,), generator=g).tolist()
+    lens[0] = width * 16
+    if batch > 2:
+        lens[batch // 2] = 0
+    c = decode_case(lens, seed=batch + width, hq=hq, hkv=hkv, head_dim=d, width=width,
+                    extra_blocks=3)
+    assert c.block_tables.shape[1] == width
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    if cache == "int8":
+        ref = oracle_int8(c)
+        auto = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs)
+    else:
+        k16, v16 = bf16_caches(c)
+        ref = O.paged_attention_ref(c.query.float().numpy(), k16.float().numpy(),
+                                    v16.float().numpy(), c.block_tables.numpy(), c.seq_lens.numpy())
+        kc, vc, ks, vs = k16.to(cuda), v16.to(cuda), None, None
+        auto = int8kv.bf16_paged_attention(q, kc, vc, bt, sl)
+    forced = _group(q, kc, vc, bt, sl, ks, vs)
+    torch.cuda.synchronize()
+    _check(auto, ref, f"automatic {cache} d={d} B={batch} width={width}")
+    _check(forced, ref, f"per-sequence {cache} d={d} B={batch} width={width}")
+    assert torch.equal(auto, forced) == per_seq
