@@ -5,8 +5,8 @@ a GQA shape (group 1-16, including one kv head), head_dim 64 or 128, a cache blo
 tokens, the query dtype, the table and length dtypes, the split count, ``impl`` and
 ``quantize_q``, then checks ``int8_paged_attention`` (and, for a third of the cases,
 ``bf16_paged_attention`` on the same K/V in a 16-bit cache) against the fp32 oracle at the
-usual bar (max |diff| <= 2e-2, cosine >= 0.9999; empty sequences exactly zero).  A second set repeats
-the draws at head_dim 256.  The seeds are fixed, so a failure names a reproducible case.
+usual bar (max |diff| <= 2e-2, cosine >= 0.9999; empty sequences exactly zero).  Two more sets repeat
+the draws at head_dim 256 and at head_dim 64.  The seeds are fixed, so a failure names a reproducible case.
 """
 
 from __future__ import annotations
@@ -54,9 +54,7 @@ def _check(out, ref, lens, what):
     assert err <= MAX_ABS and cos >= MIN_COS, f"{what}: max|diff|={err} cos={cos}"
 
 
-@pytest.mark.parametrize("seed", range(24))
-def test_random_configuration(cuda, seed):
-    p = _draw(seed)
+def _run(cuda, p, seed):
     what = f"seed {seed}: {p}"
     c = decode_case(p["lens"], seed=seed, hq=p["hq"], hkv=p["hkv"], head_dim=p["d"],
                     block_size=p["bs"], randn_kv=p["randn"], extra_blocks=5)
@@ -84,6 +82,11 @@ def test_random_configuration(cuda, seed):
         _check(out16, ref16, p["lens"], "bf16 " + what)
 
 
+@pytest.mark.parametrize("seed", range(24))
+def test_random_configuration(cuda, seed):
+    _run(cuda, _draw(seed), seed)
+
+
 @pytest.mark.parametrize("seed", range(100, 110))
 def test_random_configuration_head_dim_256(cuda, seed):
     """The same random draws at head_dim 256 (GQA groups 1-8 as the Gemma family uses; 16-bit
@@ -94,27 +97,15 @@ def test_random_configuration_head_dim_256(cuda, seed):
     if p["qdtype"] == torch.float32 and p["bf16"]:
         p["qdtype"] = torch.bfloat16
     p["lens"] = [min(n, 4000) for n in p["lens"]]
-    what = f"seed {seed}: {p}"
-    c = decode_case(p["lens"], seed=seed, hq=hq, hkv=hkv, head_dim=256, block_size=p["bs"],
-                    randn_kv=p["randn"], extra_blocks=5)
-    q = c.query.to(p["qdtype"])
-    _, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
-    if p["bt64"]:
-        bt = bt.to(torch.int64)
-    if p["sl64"]:
-        sl = sl.to(torch.int64)
-    out = int8kv.int8_paged_attention(q.to(cuda), kc, vc, bt, sl, ks, vs, quantize_q=p["qq"],
-                                      impl=p["impl"], num_splits=p["splits"])
-    torch.cuda.synchronize()
-    ref = O.paged_attention_ref(q.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
-                                c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
-                                quantize_q=p["qq"])
-    _check(out, ref, p["lens"], "int8 " + what)
-    if p["bf16"]:
-        k16, v16 = bf16_caches(c)
-        out16 = int8kv.bf16_paged_attention(q.to(cuda), k16.to(cuda), v16.to(cuda), bt, sl,
-                                            num_splits=p["splits"])
-        torch.cuda.synchronize()
-        ref16 = O.paged_attention_ref(q.float().numpy(), k16.float().numpy(), v16.float().numpy(),
-                                      c.block_tables.numpy(), c.seq_lens.numpy())
-        _check(out16, ref16, p["lens"], "bf16 " + what)
+    _run(cuda, p, seed)
+
+
+@pytest.mark.parametrize("seed", range(200, 212))
+def test_random_configuration_head_dim_64(cuda, seed):
+    """The random draws at head_dim 64: even kv-head counts with groups up to 8 take kv heads in
+    pairs in the range layout (32/8 as Llama-3.2-1B, 24/8 as Llama-3.2-3B, 16/2, 8/8), odd ones
+    and group 12 do not (12/3, 24/2); short calls take the per-sequence layout."""
+    p = _draw(seed)
+    hq, hkv = [(32, 8), (24, 8), (16, 2), (8, 8), (12, 3), (24, 2)][seed % 6]
+    p.update(hq=hq, hkv=hkv, d=64)
+    _run(cuda, p, seed)
