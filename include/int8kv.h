@@ -177,7 +177,10 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *                 or tokens <= 2048 with W >= (tiles per wave - 3) x CUs / 8, at most CUs / 2;
  *                 head_dim 128, 16-bit cache: W <= 3 CUs, and tokens <= 512, or tokens <= 1024
  *                 with W >= CUs / 2; head_dim 64: W <= 4 CUs, and for an INT8 cache tokens <=
- *                 1536, or tokens <= 2048 with W >= CUs / 8; for a 16-bit cache tokens <= 1024).
+ *                 1536, or tokens <= 2048 with W >= CUs / 8; for a 16-bit cache tokens <= 1024;
+ *                 head_dim 256: W <= 3 CUs, and for an INT8 cache tokens <= 512, or tokens <=
+ *                 1024 with CUs / 2 <= W <= CUs; for a 16-bit cache tokens <= 256, or tokens <=
+ *                 512 with W >= CUs / 2).
  *   flags:        INT8KV_DECODE_ALL normally; MAIN and MERGE separately let a caller time the
  *                 two kernels on their own (MERGE must follow MAIN with identical arguments).
  *                 OR INT8KV_DECODE_QUANTIZE_Q to quantise each (sequence, query head) row of q
@@ -190,7 +193,7 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *                 does nothing.  Suited to short sequences (each workgroup streams its whole
  *                 sequence on one compute unit).
  *
- * Supported sizes: head_dim 64, 128 or 256 (256 without INT8KV_DECODE_PER_SEQUENCE), block_size
+ * Supported sizes: head_dim 64, 128 or 256, block_size
  * a power of two in [16, 65536] (16 and 32 are vLLM's usual values), group = num_q_heads /
  * num_kv_heads in [1, 16].  Other sizes return INT8KV_E_SHAPE.
  */

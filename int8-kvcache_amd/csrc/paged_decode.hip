@@ -1157,14 +1157,19 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(de
 }
 
 // Short sequences, one workgroup per (sequence b = blockIdx.x, kv head blockIdx.y): its
-// kGroupWaves waves take equal shares of the sequence's tiles, leave their softmax states in LDS,
-// and wave 0 merges them into the output rows.  No partial records and no merge kernel: a call
-// costs one launch and the dependent loads of one segment.
-constexpr int kGroupWaves = 8;
+// group_waves<HD>() waves take equal shares of the sequence's tiles, leave their softmax states in
+// LDS, and waves 0-3 merge them into the output rows.  No partial records and no merge kernel: a
+// call costs one launch and the dependent loads of one segment.  Eight waves (two per SIMD) up
+// to head_dim 128; four at 256, one per SIMD as its registers need, whose states then take
+// 64 KB of LDS (eight would need 128 KB and spill).
+template <int HD>
+constexpr int group_waves() {
+  return HD > 128 ? 4 : 8;
+}
 
 template <int CACHE, int QT, bool QQ, int HD>
-__global__ __launch_bounds__(kGroupWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void group_kernel(DecodeArgs a) {
-  constexpr int NW = kGroupWaves;
+__global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves_per_eu(HD > 128 ? 1 : 2))) void group_kernel(DecodeArgs a) {
+  constexpr int NW = group_waves<HD>();
   __shared__ int32_t s_ids[NW][kChunkTiles * tile_blocks<CACHE>()];
   __shared__ float s_acc[NW][HD / 4 * kWave];
   __shared__ float s_m[NW][16];
@@ -1524,12 +1529,23 @@ int32_t auto_min_tiles(int64_t batch, int64_t table_width, int32_t block_size, i
 // 12.5 us), up to 8 from CUs / 8 workgroups (B = 4 x 2048 12.9 vs 13.3, B = 128 x 2048 45.5 vs
 // 56.8), and up to 4 workgroups per CU (B = 128 x 1024 26.4 vs 32.6; at 6 per CU with 4 tiles
 // per wave 54.3 vs 45.0, at 8 per CU it loses at every length); BF16 wins up to 4 tiles per wave
-// at any count (B = 8 x 1024 9.5 vs 12.8 us) and loses from 6 on.
+// at any count (B = 8 x 1024 9.5 vs 12.8 us) and loses from 6 on.  At head_dim 256 (16/8 heads,
+// four waves per workgroup): INT8 wins up to 4 tiles per wave at any count up to 3 workgroups
+// per CU (B = 1 x 256 10.2 vs 14.2 us, B = 32 x 512 17.8 vs 22.8, B = 96 x 512 42.7 vs 47.1; at
+// 4 per CU 44.0 vs 29.5), with 8 from CUs / 2 to CUs workgroups (B = 32 x 1024 27.4 vs 32.4;
+// B = 1 and 8 x 1024 lose 4.1 and 0.6); 16-bit caches up to 2 tiles per wave (B = 1 x 256 10.9
+// vs 14.6), 4 from CUs / 2 workgroups (B = 16 x 512 18.3 vs 22.4; B = 1-8 lose 0.7-0.8).
 bool use_per_sequence(bool int8_cache, int32_t head_dim, int64_t batch, int32_t num_kv_heads,
                       int64_t table_width, int32_t block_size, int64_t cu) {
   const int64_t wgs = batch * num_kv_heads;
   const double tiles = std::ceil((double)table_width * block_size / 32.0);  // longest sequence
-  const int64_t per_wave = (int64_t)std::ceil(tiles / kGroupWaves);
+  const int nw = head_dim > 128 ? group_waves<256>() : group_waves<128>();
+  const int64_t per_wave = (int64_t)std::ceil(tiles / nw);
+  if (head_dim > 128) {  // four waves per workgroup, so twice the tiles per wave
+    if (wgs > 3 * cu) return false;
+    if (!int8_cache) return per_wave <= 2 || (per_wave <= 4 && 2 * wgs >= cu);
+    return per_wave <= 4 || (per_wave <= 8 && 2 * wgs >= cu && wgs <= cu);
+  }
   if (head_dim == 64) {
     if (wgs > 4 * cu) return false;
     if (!int8_cache) return per_wave <= 4;
@@ -1624,24 +1640,17 @@ int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
   const int32_t hv = a.kv_pair ? a.num_kv_heads / 2 : a.num_kv_heads;  // kv heads (pairs) per range
   const int W = waves_per_wg(a.group_mode ? a.num_kv_heads : hv);
   if (a.group_mode) {  // one kernel; nothing to merge afterwards
-    // Not at head_dim 256: the 8 waves' states would need 128 KB of LDS (decode_entry rejects
-    // the flag there and the automatic choice skips the layout).
-    if constexpr (HD > 128) {
-      return INT8KV_E_SHAPE;
-    } else {
-      if (flags & INT8KV_DECODE_MAIN) {
-        dim3 grid((unsigned)a.batch, (unsigned)a.num_kv_heads);
-        if (a.quantize_q)
-          hipLaunchKernelGGL((group_kernel<CACHE, QT, true, HD>), grid, dim3(kGroupWaves * kWave),
-                             0, s, a);
-        else
-          hipLaunchKernelGGL((group_kernel<CACHE, QT, false, HD>), grid, dim3(kGroupWaves * kWave),
-                             0, s, a);
-        hipError_t e = hipGetLastError();
-        return e == hipSuccess ? INT8KV_OK : (int)e;
-      }
-      return INT8KV_OK;
+    if (flags & INT8KV_DECODE_MAIN) {
+      dim3 grid((unsigned)a.batch, (unsigned)a.num_kv_heads);
+      const dim3 block(group_waves<HD>() * kWave);
+      if (a.quantize_q)
+        hipLaunchKernelGGL((group_kernel<CACHE, QT, true, HD>), grid, block, 0, s, a);
+      else
+        hipLaunchKernelGGL((group_kernel<CACHE, QT, false, HD>), grid, block, 0, s, a);
+      hipError_t e = hipGetLastError();
+      return e == hipSuccess ? INT8KV_OK : (int)e;
     }
+    return INT8KV_OK;
   }
   if (flags & INT8KV_DECODE_MAIN) {
     dim3 grid((unsigned)((a.max_ranges + a.halves - 1) / a.halves), (unsigned)(hv / W));
@@ -1870,10 +1879,9 @@ int decode_entry(
   a.seq_cost = kSeqStartCost;
   a.quantize_q = (flags & INT8KV_DECODE_QUANTIZE_Q) != 0;
   a.group_mode = (flags & INT8KV_DECODE_PER_SEQUENCE) != 0 ||
-                 (automatic && head_dim <= 128 &&
+                 (automatic &&
                   use_per_sequence(cache_dtype == INT8KV_I8, head_dim, batch, num_kv_heads,
                                    table_width, block_size, cus));
-  if (a.group_mode && head_dim > 128) return INT8KV_E_SHAPE;
   a.kv_pair = kv_pair_ok && !a.group_mode;
   a.block_shift = __builtin_ctz((unsigned)block_size);
   a.tile_tokens = kRows * (cache_dtype == INT8KV_I8 ? tile_blocks<kI8>() : tile_blocks<kBF16>());

@@ -554,7 +554,8 @@ def _group(q, kc, vc, bt, sl, ks, vs, extra_flags=0):
     return out
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(28, 4, 128), (14, 2, 64), (8, 8, 128)])
+@pytest.mark.parametrize("hq,hkv,d", [(28, 4, 128), (14, 2, 64), (8, 8, 128), (16, 8, 256),
+                                    (8, 1, 256)])
 def test_per_sequence_mode(cuda, hq, hkv, d):
     """One workgroup per (sequence, kv head) whose waves merge their states in LDS
     (INT8KV_DECODE_PER_SEQUENCE): against the oracle for INT8 (fp32 query too) and quantize_q,
@@ -666,6 +667,13 @@ AUTO_LAYOUT_POINTS = [
     (128, 28, 4, "bf16", 200, 32, False),
     (128, 28, 4, "int8", 96, 32, False),    # INT8 at 128: at most one workgroup per CU
     (128, 28, 4, "int8", 48, 32, True),
+    (256, 16, 8, "int8", 32, 32, True),     # 256: four waves per workgroup, 4 tiles per wave
+    (256, 16, 8, "int8", 128, 16, False),   # 4 workgroups per CU: past the 3-per-CU cap
+    (256, 16, 8, "int8", 8, 64, False),     # 8 tiles per wave: needs CUs / 2 workgroups
+    (256, 16, 8, "int8", 32, 64, True),
+    (256, 16, 8, "bf16", 1, 16, True),      # 16-bit cache: 2 tiles per wave at any count
+    (256, 16, 8, "bf16", 4, 32, False),     # 4 tiles per wave: needs CUs / 2 workgroups
+    (256, 16, 8, "bf16", 16, 32, True),
 ]
 
 

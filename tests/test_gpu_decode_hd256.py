@@ -7,8 +7,8 @@ its 4 token rows, the waves take one SIMD each with two tiles in flight, and the
 one range slot of 64 float4 columns.  Cases: GQA groups 2, 1 and 8 (Gemma-2-9B 16/8, Gemma-7B
 16/16, Gemma-2B 8/1), lengths at tile, block and chunk boundaries with empty and one-token
 sequences, bf16 / fp16 / fp32 queries, quantize_q (int8 scores), forced splits, both merge grids,
-BF16 and FP16 caches, and the write-then-decode path.  The per-sequence layout is not offered at
-256 (its LDS state would need 128 KB) and is rejected with an error.
+BF16 and FP16 caches, the write-then-decode path, and the per-sequence layout (four waves per
+workgroup at 256).
 """
 
 from __future__ import annotations
@@ -117,16 +117,22 @@ def test_write_then_decode(cuda):
     _check(out, ref, "write then decode")
 
 
-def test_per_sequence_layout_is_rejected(cuda):
+def test_per_sequence_layout(cuda):
+    """The per-sequence layout at 256 (four waves, one per SIMD, their states in 64 KB of LDS):
+    forced, against the oracle for short and tile-boundary lengths, and the automatic choice on
+    the same call agrees with it."""
     from int8kv import _decode, _lib
 
-    c = decode_case([40, 7], seed=3, hq=8, hkv=2, head_dim=256, extra_blocks=2)
+    c = decode_case([40, 7, 0, 32, 33, 129, 511], seed=3, hq=8, hkv=2, head_dim=256,
+                    extra_blocks=2)
     q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    ref = oracle_int8(c)
     out = torch.empty_like(q)
-    with pytest.raises(RuntimeError, match="E_SHAPE"):
-        _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, out, 0,
-                             _lib.DECODE_ALL | _lib.DECODE_PER_SEQUENCE)
-    # the automatic choice never takes it at 256 (a call this short would take it at 128)
+    _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, out, 0,
+                         _lib.DECODE_ALL | _lib.DECODE_PER_SEQUENCE)
+    torch.cuda.synchronize()
+    assert (out[2] == 0).all()
+    _check(out, ref, "per-sequence layout")
     auto = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs)
     torch.cuda.synchronize()
-    _check(auto, oracle_int8(c), "short call, automatic layout")
+    _check(auto, ref, "short call, automatic layout")
