@@ -4,7 +4,7 @@ It must give exactly what int8kv_paged_decode gives with a caller's workspace (s
 same plan, partials in the library's fixed scratch array instead).  Two calls in a row on the
 same GPU, the second with a smaller input, both bit-identical to the workspace entry point and
 within the oracle bar; then the INT8 x BF16-cache and forced-range variants, the merge indexed by
-range and head_dim 256.
+range, head_dim 256, and head_dim 64 (kv-head pairs, per-sequence layout).
 """
 
 from __future__ import annotations
@@ -89,6 +89,22 @@ def test_range_indexed_merge_and_head_dim_256(cuda):
                        (decode_case([700, 3, 2500, 64], seed=36, hq=16, hkv=8, head_dim=256,
                                     extra_blocks=3), "head_dim 256")):
         print(f"noalloc: {what}", flush=True)
+        q, kc, vc, bt, sl, ks, vs = to_dev(case, cuda)
+        want = _with_workspace(q, kc, vc, bt, sl, ks, vs)
+        got = _noalloc(q, kc, vc, bt, sl, ks, vs, torch.full_like(q, float("nan")))
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"{what}: outputs differ from int8kv_paged_decode"
+        err, cos, _ = metrics(got.float().cpu().numpy(), oracle_int8(case))
+        assert err <= MAX_ABS and cos >= MIN_COS, (what, err, cos)
+
+
+def test_head_dim_64_pairs_and_per_sequence(cuda):
+    """head_dim 64 with kv heads taken in pairs (twice the automatic range count, sized by the
+    entry point from the pairs), then a short call that takes the per-sequence layout."""
+    for lens, seed, what in (([5000, 1, 3000, 0, 4100, 77], 37, "head_dim 64 pairs"),
+                             ([300, 12, 512], 38, "head_dim 64 per-sequence")):
+        print(f"noalloc: {what}", flush=True)
+        case = decode_case(lens, seed=seed, hq=32, hkv=8, head_dim=64, extra_blocks=3)
         q, kc, vc, bt, sl, ks, vs = to_dev(case, cuda)
         want = _with_workspace(q, kc, vc, bt, sl, ks, vs)
         got = _noalloc(q, kc, vc, bt, sl, ks, vs, torch.full_like(q, float("nan")))
