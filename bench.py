@@ -701,29 +701,46 @@ def main() -> int:
 
     settle(int8_q_call, batch=10, min_ms=30.0)
     ms_q = time_loop(int8_q_call, args.steps, args.warmup)
-    # Host cost of one eager call: the wall time of enqueueing `steps` calls without waiting (each
-    # call's ~190 us of device work keeps the device behind the host), through the torch
-    # extension (the default path) and through the ctypes binding of the same C ABI.
+    # Host cost of one eager call, through the torch extension (the default path) and through the
+    # ctypes binding of the same C ABI: the wall time of one call made when the device has caught
+    # up (median of 50), and the wall time per call of enqueueing 50 calls without waiting (median
+    # of five batches after one untimed), where each call's ~190 us of device work keeps the device
+    # ever further behind the host: the HIP runtime's launches then cost ~3.5 us more per call
+    # (MI355X, ROCm 7.2; 5.5 us per call with 20-us calls queued, 9 us with 190-us ones).
     from int8kv import _ext
 
-    def enqueue_us():
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
+    def call_us(calls=50):
+        per_call = []
+        for _ in range(calls + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
             int8_call()
-        us = (time.perf_counter() - t0) * 1e6 / args.steps
+            per_call.append((time.perf_counter() - t0) * 1e6)
         torch.cuda.synchronize()
-        return us
+        return statistics.median(per_call[1:])
 
-    host_us = enqueue_us()
+    def enqueue_us(batches=5, calls=50):
+        per_call = []
+        for rep in range(batches + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(calls):
+                int8_call()
+            if rep:
+                per_call.append((time.perf_counter() - t0) * 1e6 / calls)
+        torch.cuda.synchronize()
+        return statistics.median(per_call)
+
+    host_us, host_us_queued = call_us(), enqueue_us()
     with _ext.use_ctypes():
-        host_us_ctypes = enqueue_us()
+        host_us_ctypes, host_us_ctypes_queued = call_us(), enqueue_us()
     value = nbytes8 / (ms * 1e-3) / 1e9
     achieved = nbytes8 / (ms_main * 1e-3) / 1e9
     log(f"int8 op: {ms * 1e3:.1f} us/call ({value:.0f} GB/s); decode kernel {ms_main * 1e3:.1f} us "
         f"({achieved:.0f} GB/s); merge kernel {ms_merge * 1e3:.1f} us; bf16 op {ms16 * 1e3:.1f} us "
         f"({nbytes16 / (ms16 * 1e-3) / 1e9:.0f} GB/s); int8 quantize_q op {ms_q * 1e3:.1f} us; "
-        f"host enqueue {host_us:.1f} us/call (ctypes path {host_us_ctypes:.1f})")
+        f"host enqueue {host_us:.1f} us/call, {host_us_queued:.1f} queued (ctypes path "
+        f"{host_us_ctypes:.1f}, {host_us_ctypes_queued:.1f})")
 
     result = {
         "metric": METRIC,
@@ -756,6 +773,8 @@ def main() -> int:
             "frac_of_hbm_peak_whole_call": round(value / HBM_PEAK_GBS, 4),
             "host_enqueue_us_per_call": round(host_us, 2),
             "host_enqueue_us_per_call_ctypes": round(host_us_ctypes, 2),
+            "host_enqueue_us_per_call_queued": round(host_us_queued, 2),
+            "host_enqueue_us_per_call_ctypes_queued": round(host_us_ctypes_queued, 2),
             "host_path": "torch extension" if _ext.module() is not None else "ctypes",
             "settle": st,
         },

@@ -15,7 +15,9 @@
 #include <c10/hip/HIPStream.h>
 
 #include <cmath>
+#include <map>
 #include <string>
+#include <utility>
 
 #include "int8kv.h"
 
@@ -105,9 +107,25 @@ int32_t ranges_for(int64_t batch, const c10::optional<int64_t>& num_splits) {
   return (int32_t)std::max<int64_t>(1, std::min<int64_t>(kMaxRanges, r));
 }
 
+// Workspace of an eager call, kept per (device, stream) for the calling host thread: a call's
+// partial records are read only by its own merge launch on the same stream, so the next call on
+// that stream can reuse the buffer in stream order, while other streams and threads get their
+// own.  Saves a caching-allocator round trip per call (~1.3 us of host time on MI355X).  Under
+// graph capture it comes from torch's allocator instead (the graph's pool), so a replay never
+// shares memory with eager calls.  The tensors are released when the thread ends.
+at::Tensor workspace_for(const at::Tensor& like, hipStream_t stream, size_t need) {
+  const int64_t bytes = (int64_t)std::max<size_t>(need, 16);
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone)
+    return at::empty({bytes}, like.options().dtype(at::kByte));
+  thread_local std::map<std::pair<int, uintptr_t>, at::Tensor> cache;
+  at::Tensor& ws = cache[{(int)like.device().index(), reinterpret_cast<uintptr_t>(stream)}];
+  if (!ws.defined() || ws.numel() < bytes) ws = at::empty({bytes}, like.options().dtype(at::kByte));
+  return ws;
+}
+
 // Launches int8kv_paged_decode into `out`; the workspace comes from `workspace` when it is large
-// enough, else from torch's caching allocator (stream-ordered, so under graph capture it comes
-// from the graph's pool).
+// enough, else from workspace_for.
 at::Tensor decode_into(at::Tensor query, const at::Tensor& key_cache, const at::Tensor& value_cache,
                        const at::Tensor& block_tables, at::Tensor seq_lens,
                        const c10::optional<at::Tensor>& k_scale,
@@ -121,12 +139,10 @@ at::Tensor decode_into(at::Tensor query, const at::Tensor& key_cache, const at::
   if (!seq_lens.is_contiguous()) seq_lens = seq_lens.contiguous();
   const size_t need = int8kv_decode_workspace_bytes((int32_t)Hq, (int32_t)Hkv, (int32_t)D,
                                                     (int32_t)BS, (int32_t)num_ranges);
-  at::Tensor ws;
-  if (workspace.has_value() && (size_t)workspace->numel() >= need) {
-    ws = *workspace;
-  } else {
-    ws = at::empty({(int64_t)std::max<size_t>(need, 16)}, query.options().dtype(at::kByte));
-  }
+  const hipStream_t stream = current_stream(query);
+  const at::Tensor ws = (workspace.has_value() && (size_t)workspace->numel() >= need)
+                            ? *workspace
+                            : workspace_for(query, stream, need);
   const int st = int8kv_paged_decode(
       query.data_ptr(), dtype_code(query.scalar_type()), B, (int32_t)Hq, (int32_t)D,
       query.strides().data(), key_cache.data_ptr(), value_cache.data_ptr(),
@@ -137,7 +153,7 @@ at::Tensor decode_into(at::Tensor query, const at::Tensor& key_cache, const at::
       k_scale.has_value() ? k_scale->data_ptr<float>() : nullptr,
       v_scale.has_value() ? v_scale->data_ptr<float>() : nullptr, (float)(1.0 / std::sqrt((double)D)),
       out.data_ptr(), out.strides().data(), ws.data_ptr(), (size_t)ws.numel(), (int32_t)num_ranges,
-      (int32_t)min_tiles, (uint32_t)flags, current_stream(query));
+      (int32_t)min_tiles, (uint32_t)flags, stream);
   check_status(st, "int8kv_paged_decode");
   return out;
 }
