@@ -62,6 +62,7 @@ enum int8kv_dtype {
 #define INT8KV_DECODE_ALL 3u
 #define INT8KV_DECODE_QUANTIZE_Q 4u  /* quantise q to int8 per (sequence, head) first */
 #define INT8KV_DECODE_PER_SEQUENCE 8u  /* one workgroup per (sequence, kv head), no merge */
+#define INT8KV_DECODE_SPLIT_SEQUENCES 16u  /* several workgroups per (sequence, kv head) */
 
 /*
  * Static per-head INT8 quantisation of K and V plus the slot_mapping scatter into the paged
@@ -192,6 +193,15 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *                 softmax states on chip; one kernel, the workspace is not touched and MERGE
  *                 does nothing.  Suited to short sequences (each workgroup streams its whole
  *                 sequence on one compute unit).
+ *                 OR INT8KV_DECODE_SPLIT_SEQUENCES for the split per-sequence layout: Z =
+ *                 min(CUs / (batch x num_kv_heads), 64, 2 x num_ranges / batch) such workgroups
+ *                 per (sequence, kv head), each over 1/Z of the sequence's tiles, leave one
+ *                 partial record per query head in the workspace, and MERGE combines the Z
+ *                 records (below Z = 2 it is the plain per-sequence layout).  Suited to a few
+ *                 long sequences.  The automatic choice (num_ranges = 0, min_tiles = 0, when the
+ *                 per-sequence layout is not taken) uses it when batch x num_kv_heads <= CUs / 8
+ *                 and each wave then holds at most 4 tiles of 32 tokens (2 at head_dim 64) of
+ *                 the longest possible sequence (table width x block size).
  *
  * Supported sizes: head_dim 64, 128 or 256, block_size
  * a power of two in [16, 65536] (16 and 32 are vLLM's usual values), group = num_q_heads /

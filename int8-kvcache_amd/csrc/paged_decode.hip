@@ -121,6 +121,8 @@ struct DecodeArgs {
   int32_t scan32;       // a 64-sequence chunk's units fit 32 bits (see units_scan)
   int32_t cut_desc;     // write ws_cut (merge_by_range_kernel follows)
   int32_t kv_pair;      // head_dim 64: each wave takes kv heads 2k and 2k + 1 as one 128-wide head
+  int32_t split;        // per-sequence layout over `split` workgroups per (sequence, kv head), whose
+                        // records merge_split_kernel combines (0: one workgroup, no records)
 };
 
 // ------------------------------------------------------------------------ wave utilities
@@ -1171,12 +1173,16 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(de
 // call costs one launch and the dependent loads of one segment.  Eight waves (two per SIMD) up
 // to head_dim 128; four at 256, one per SIMD as its registers need, whose states then take
 // 64 KB of LDS (eight would need 128 KB and spill).
+// SPLIT (few long sequences): gridDim.z workgroups per (sequence, kv head), workgroup z taking
+// tiles [z n / Z, (z + 1) n / Z) of the sequence's n; each leaves one record per query head
+// (row (b Z + z) Hq + h, the layout of the range records) for merge_split_kernel, and an empty
+// sequence leaves none (that kernel writes its zero rows).
 template <int HD>
 constexpr int group_waves() {
   return HD > 128 ? 4 : 8;
 }
 
-template <int CACHE, int QT, bool QQ, int HD>
+template <int CACHE, int QT, bool QQ, int HD, bool SPLIT>
 __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves_per_eu(HD > 128 ? 1 : 2))) void group_kernel(DecodeArgs a) {
   constexpr int NW = group_waves<HD>();
   __shared__ int32_t s_ids[NW][kChunkTiles * tile_blocks<CACHE>()];
@@ -1193,11 +1199,16 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
   const int64_t L = seq_len_of(a, b);
   const int64_t n = tiles_of(a, L);
   if (n == 0) {  // uniform over the workgroup: every wave leaves before the barrier
-    if (wave == 0) write_zero_rows<QT, HD>(a, b, kvh, lane);
+    if (!SPLIT && wave == 0) write_zero_rows<QT, HD>(a, b, kvh, lane);
     return;
   }
-  const int64_t ta = wave * n / NW;
-  const int64_t tb = (wave + 1) * n / NW;
+  int64_t t0 = 0, span = n;  // this workgroup's tiles of the sequence
+  if constexpr (SPLIT) {
+    t0 = (int64_t)blockIdx.z * n / gridDim.z;
+    span = ((int64_t)blockIdx.z + 1) * n / gridDim.z - t0;
+  }
+  const int64_t ta = t0 + wave * span / NW;
+  const int64_t tb = t0 + (wave + 1) * span / NW;
   if (ta < tb) {
     run_segment<CACHE, QT, false, QQ, HD, 2, true>(a, s_ids[wave], b, L, kvh, ta, tb, false, 0,
                                                    lane, s_acc[wave], s_m[wave], s_l[wave]);
@@ -1241,6 +1252,15 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
       M = Mn;
     }
   }
+  if constexpr (SPLIT) {
+    const int64_t row = ((int64_t)b * gridDim.z + blockIdx.z) * a.num_q_heads + kvh * G + li;
+    store_n<kF32, HD / 16>(reinterpret_cast<char*>(a.ws_acc + row * HD) + (HD / 4 * lg + HD / 16 * rr) * 4, O);
+    if (rr == 0 && lg == 0) {
+      a.ws_m[row] = M;
+      a.ws_l[row] = Ls;
+    }
+    return;
+  }
   const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
   const float inv = Ls > 0.0f ? vscale / Ls : 0.0f;
   char* op = a.out + (b * a.o_sb + (int64_t)(kvh * G + li) * a.o_sh) * esize<QT>();
@@ -1248,6 +1268,85 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
 #pragma unroll
   for (int dt = 0; dt < HD / 16; ++dt) o[dt] = O[dt] * inv;
   store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), o);
+}
+
+// Merge of the split per-sequence layout's records: a.split = Z <= 64 records per (sequence b =
+// blockIdx.x, query head h = blockIdx.y), one wave.  Every record load is issued at entry (in
+// chunks of 16 records, each chunk taken only when Z reaches it, the index clamped into [0, Z)):
+// lane z < Z reads record z's running max and sum and each lane HD / 64 accumulator elements of
+// every record, so the call waits for one memory latency.  The wave then reduces the maxima and
+// the weighted sums, and each lane combines its elements over the Z records.  A record without
+// a finite maximum is weighted 1 when no record has one, so a NaN still reaches the output, as
+// in merge_in.
+template <int CACHE, int QT, int HD>
+__global__ __launch_bounds__(64) void merge_split_kernel(DecodeArgs a) {
+  constexpr int D = HD / 64;  // accumulator elements per lane
+  constexpr int kChunk = 16, kChunks = 64 / kChunk;
+  const int lane = threadIdx.x;
+  const int64_t b = blockIdx.x;
+  const int h = blockIdx.y;
+  const int Z = a.split;
+  char* op = a.out + (b * a.o_sb + (int64_t)h * a.o_sh + D * lane) * esize<QT>();
+  float O[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) O[j] = 0.0f;
+  float inv = 0.0f;
+  if (seq_len_of(a, b) > 0) {  // uniform: an empty sequence left no records (zero rows)
+    const int64_t row0 = b * Z * a.num_q_heads + h;  // record z: row0 + z Hq
+    const int64_t stride = (int64_t)a.num_q_heads * HD;
+    const float* acc = a.ws_acc + row0 * HD + D * lane;
+    float A[kChunks][kChunk][D];
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      if (c * kChunk < Z) {
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+          const int z = c * kChunk + k < Z ? c * kChunk + k : Z - 1;
+#pragma unroll
+          for (int j = 0; j < D; ++j) A[c][k][j] = acc[z * stride + j];
+        }
+      }
+    }
+    const int64_t rz = row0 + (int64_t)(lane < Z ? lane : 0) * a.num_q_heads;
+    float m = a.ws_m[rz];
+    float l = a.ws_l[rz];
+    if (lane >= Z) {
+      m = -INFINITY;
+      l = 0.0f;
+    }
+    float M = m;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    const float w = lane < Z ? (M == -INFINITY ? 1.0f : exp2_fast(m - M)) : 0.0f;
+    float Lw = l * w;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) Lw += __shfl_xor(Lw, o);
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      if (c * kChunk < Z) {
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+          const float wk = __shfl(w, c * kChunk + k);
+          if (c * kChunk + k < Z) {
+#pragma unroll
+            for (int j = 0; j < D; ++j) O[j] += wk * A[c][k][j];
+          }
+        }
+      }
+    }
+    const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[h / a.group], 1e-6f) : 1.0f;
+    inv = Lw > 0.0f ? vscale / Lw : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    const float v = O[j] * inv;
+    if constexpr (QT == kF32)
+      reinterpret_cast<float*>(op)[j] = v;
+    else if constexpr (QT == kF16)
+      reinterpret_cast<_Float16*>(op)[j] = (_Float16)v;
+    else
+      reinterpret_cast<__bf16*>(op)[j] = (__bf16)v;
+  }
 }
 
 // Stores 4 consecutive fp32 values as DT (aligned to 4 elements).
@@ -1568,6 +1667,39 @@ bool use_per_sequence(bool int8_cache, int32_t head_dim, int64_t batch, int32_t 
   return wgs >= (need < cu / 2 ? need : cu / 2);
 }
 
+// Workgroups per (sequence, kv head) of the split per-sequence layout: one on every CU, at most
+// 64 (one merge lane each) and at most 2 x num_ranges / batch (the records use the range-record
+// rows of the workspace, 2 x num_ranges per query head).  Below 2 it is the plain layout.
+int32_t split_count(int64_t batch, int32_t num_kv_heads, int32_t num_ranges, int64_t cu) {
+  int64_t z = cu / (batch * num_kv_heads);
+  z = std::min<int64_t>(z, 64);
+  z = std::min<int64_t>(z, 2 * (int64_t)num_ranges / batch);
+  return z >= 2 ? (int32_t)z : 0;
+}
+
+// The automatic choice of the split per-sequence layout, for few long sequences (when the
+// per-sequence layout itself is not taken): the range layout cuts such a sequence into up to 256
+// ranges per kv head, whose records the merge then reads on one CU per query head (one 32k-token
+// sequence: 133 KB per query head, ~5.8 us of its 7 us), while the split layout leaves Z <= 64
+// records, already combined over eight waves in LDS.  Taken with at least 8 workgroups per
+// (sequence, kv head) and at most 4 tiles per wave (2 at head_dim 64, whose 64-wide loads lose to
+// the range layout's paired kv heads beyond that).  Measured on MI355X (HIP-graph replays, op
+// time, automatic range layout vs split, us): 28/4 heads at head_dim 128, INT8: B = 1 x 32768
+// 18.7 vs 15.3, 1 x 16384 15.2 vs 13.2, 1 x 8192 13.5 vs 12.2, 1 x 65536 23.4 vs 22.4, 2 x 8192
+// 14.5 vs 11.8, 4 x 4096 13.2 vs 11.1, 8 x 8192 21.4 vs 20.6 (1 x 4096 loses 0.3); 8 tiles per
+// wave or more lose (8 x 32768 53.2 vs 53.9, 4 workgroups: 16 x 8192 29.9 vs 31.6); BF16 cache
+// 1 x 8192 15.0 vs 11.9; 16/8 heads at 256: 1 x 16384 26.5 vs 22.4; 32/8 heads at 64: 1 x 8192
+// 15.1 vs 9.6, 4 tiles per wave ties (1 x 32768 18.7 vs 19.0) and 8 lose (4 x 16384 21.3 vs 28.7).
+bool use_split(int32_t head_dim, int64_t batch, int32_t num_kv_heads, int64_t table_width,
+               int32_t block_size, int64_t cu) {
+  const int64_t wgs = batch * num_kv_heads;
+  if (8 * wgs > cu) return false;
+  const int64_t z = std::min<int64_t>(cu / wgs, 64);
+  const double tiles = std::ceil((double)table_width * block_size / 32.0);  // longest sequence
+  const int nw = head_dim > 128 ? group_waves<256>() : group_waves<128>();
+  return tiles / (double)(z * nw) <= (head_dim == 64 ? 2.0 : 4.0);
+}
+
 // head_dim 64 with an even kv-head count and GQA groups of at most 8: a wave can take two kv
 // heads as one 128-wide head (their rows sit side by side in the cache when the head stride is
 // head_dim), 2 G <= 16 query heads in the MFMA columns.  Loads then have HD = 128's shape
@@ -1648,16 +1780,29 @@ template <int CACHE, int QT, int HD>
 int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
   const int32_t hv = a.kv_pair ? a.num_kv_heads / 2 : a.num_kv_heads;  // kv heads (pairs) per range
   const int W = waves_per_wg(a.group_mode ? a.num_kv_heads : hv);
-  if (a.group_mode) {  // one kernel; nothing to merge afterwards
+  if (a.group_mode) {  // one kernel, plus merge_split_kernel when split
     if (flags & INT8KV_DECODE_MAIN) {
-      dim3 grid((unsigned)a.batch, (unsigned)a.num_kv_heads);
+      dim3 grid((unsigned)a.batch, (unsigned)a.num_kv_heads, (unsigned)(a.split > 0 ? a.split : 1));
       const dim3 block(group_waves<HD>() * kWave);
-      if (a.quantize_q)
-        hipLaunchKernelGGL((group_kernel<CACHE, QT, true, HD>), grid, block, 0, s, a);
-      else
-        hipLaunchKernelGGL((group_kernel<CACHE, QT, false, HD>), grid, block, 0, s, a);
+      if (a.split > 0) {
+        if (a.quantize_q)
+          hipLaunchKernelGGL((group_kernel<CACHE, QT, true, HD, true>), grid, block, 0, s, a);
+        else
+          hipLaunchKernelGGL((group_kernel<CACHE, QT, false, HD, true>), grid, block, 0, s, a);
+      } else {
+        if (a.quantize_q)
+          hipLaunchKernelGGL((group_kernel<CACHE, QT, true, HD, false>), grid, block, 0, s, a);
+        else
+          hipLaunchKernelGGL((group_kernel<CACHE, QT, false, HD, false>), grid, block, 0, s, a);
+      }
       hipError_t e = hipGetLastError();
-      return e == hipSuccess ? INT8KV_OK : (int)e;
+      if (e != hipSuccess) return (int)e;
+    }
+    if (a.split > 0 && (flags & INT8KV_DECODE_MERGE)) {
+      dim3 grid((unsigned)a.batch, (unsigned)a.num_q_heads);
+      hipLaunchKernelGGL((merge_split_kernel<CACHE, QT, HD>), grid, dim3(kWave), 0, s, a);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return (int)e;
     }
     return INT8KV_OK;
   }
@@ -1891,6 +2036,13 @@ int decode_entry(
                  (automatic &&
                   use_per_sequence(cache_dtype == INT8KV_I8, head_dim, batch, num_kv_heads,
                                    table_width, block_size, cus));
+  a.split = 0;
+  if ((flags & INT8KV_DECODE_SPLIT_SEQUENCES) != 0 ||
+      (automatic && !a.group_mode &&
+       use_split(head_dim, batch, num_kv_heads, table_width, block_size, cus))) {
+    a.group_mode = true;
+    a.split = split_count(batch, num_kv_heads, num_ranges, cus);
+  }
   a.kv_pair = kv_pair_ok && !a.group_mode;
   a.block_shift = __builtin_ctz((unsigned)block_size);
   a.tile_tokens = kRows * (cache_dtype == INT8KV_I8 ? tile_blocks<kI8>() : tile_blocks<kBF16>());

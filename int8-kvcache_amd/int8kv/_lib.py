@@ -27,6 +27,7 @@ DTYPE_CODE = {
 
 DECODE_MAIN, DECODE_MERGE, DECODE_ALL, DECODE_QUANTIZE_Q = 1, 2, 3, 4
 DECODE_PER_SEQUENCE = 8
+DECODE_SPLIT_SEQUENCES = 16
 
 ERRORS = {
     -1: "INT8KV_E_NULL (a required pointer is NULL)",

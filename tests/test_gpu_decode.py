@@ -708,3 +708,75 @@ def test_automatic_layout_choice(cuda, d, hq, hkv, cache, batch, width, per_seq)
     _check(auto, ref, f"automatic {cache} d={d} B={batch} width={width}")
     _check(forced, ref, f"per-sequence {cache} d={d} B={batch} width={width}")
     assert torch.equal(auto, forced) == per_seq
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(28, 4, 128), (32, 8, 64), (16, 8, 256), (8, 1, 128)])
+def test_split_sequences_layout(cuda, hq, hkv, d):
+    """INT8KV_DECODE_SPLIT_SEQUENCES: several per-sequence workgroups per (sequence, kv head),
+    each leaving one record per query head, combined by merge_split_kernel.  Few long sequences
+    with an empty one and one shorter than the split count (workgroups without tiles leave
+    neutral records); INT8 with bf16 and fp32 queries, quantize_q, a BF16 cache."""
+    from int8kv import _decode, _lib
+
+    lens = [9000, 0, 5, 30000] if d < 256 else [9000, 0, 5, 12000]
+    c = decode_case(lens, seed=hq + d + 5, hq=hq, hkv=hkv, head_dim=d, extra_blocks=4)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    flags = _lib.DECODE_ALL | _lib.DECODE_SPLIT_SEQUENCES
+
+    def run(qq, k, v, kscale, vscale, extra=0):
+        out = torch.full_like(qq, float("nan"))
+        _decode.paged_decode(qq, k, v, bt, sl, kscale, vscale, out, 0, flags | extra)
+        torch.cuda.synchronize()
+        return out
+
+    ref = oracle_int8(c)
+    out = run(q, kc, vc, ks, vs)
+    assert (out[1] == 0).all()
+    _check(out, ref, f"split int8 {hq}/{hkv}/{d}")
+    err, _, _ = metrics(run(q.float(), kc, vc, ks, vs).cpu().numpy(), ref)
+    assert err <= 1e-3, err
+    ref_q = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                  c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
+                                  quantize_q=True)
+    _check(run(q, kc, vc, ks, vs, _lib.DECODE_QUANTIZE_Q), ref_q, f"split quantize_q {hq}/{hkv}/{d}")
+    k16, v16 = bf16_caches(c)
+    ref16 = O.paged_attention_ref(c.query.float().numpy(), k16.float().numpy(), v16.float().numpy(),
+                                  c.block_tables.numpy(), c.seq_lens.numpy())
+    _check(run(q, k16.to(cuda), v16.to(cuda), None, None), ref16, f"split bf16 {hq}/{hkv}/{d}")
+
+
+# (head_dim, q heads, kv heads, batch, table width in 16-token blocks, split?) on 256 CUs.
+AUTO_SPLIT_POINTS = [
+    (128, 28, 4, 1, 2048, True),     # 64 workgroups per kv head, 2 tiles per wave
+    (128, 28, 4, 8, 2048, False),    # 8 workgroups per kv head, 16 tiles per wave
+    (64, 32, 8, 1, 256, True),       # head_dim 64: 32 workgroups, under one tile per wave
+    (64, 32, 8, 4, 1024, False),     # head_dim 64: 8 tiles per wave (paired range layout)
+    (256, 16, 8, 1, 1024, True),     # head_dim 256: four waves, 4 tiles per wave
+    (128, 28, 4, 16, 512, False),    # 4 workgroups per (sequence, kv head)
+]
+
+
+@pytest.mark.parametrize("d,hq,hkv,batch,width,split", AUTO_SPLIT_POINTS)
+def test_automatic_split_choice(cuda, d, hq, hkv, batch, width, split):
+    """The automatic call takes the split per-sequence layout exactly where the rule says: its
+    output is then bit-identical to the forced INT8KV_DECODE_SPLIT_SEQUENCES call's (and differs
+    otherwise); both match the oracle."""
+    from int8kv import _decode, _lib
+
+    if torch.cuda.get_device_properties(cuda).multi_processor_count != 256:
+        pytest.skip("the thresholds are stated for 256 compute units")
+    g = torch.Generator().manual_seed(batch * width + d + 1)
+    lens = torch.randint(1, width * 16 + 1, (batch,), generator=g).tolist()
+    lens[0] = width * 16
+    c = decode_case(lens, seed=batch + width + 1, hq=hq, hkv=hkv, head_dim=d, width=width,
+                    extra_blocks=3)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    auto = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs)
+    forced = torch.empty_like(q)
+    _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, forced, 0,
+                         _lib.DECODE_ALL | _lib.DECODE_SPLIT_SEQUENCES)
+    torch.cuda.synchronize()
+    ref = oracle_int8(c)
+    _check(auto, ref, f"automatic d={d} B={batch} width={width}")
+    _check(forced, ref, f"split d={d} B={batch} width={width}")
+    assert torch.equal(auto, forced) == split
