@@ -185,12 +185,15 @@ def test_graph_replays_of_the_range_indexed_merge(cuda, host_path):
 
 
 def test_graph_replays_at_head_dims_64_and_256(cuda, host_path):
-    """Graphs holding the head_dim-64 paired range decode (kv heads two per wave, merge) and the
-    head_dim-256 per-sequence decode (four-wave workgroups, one kernel), replayed between eager
-    calls of the other on the same stream; every output bit-identical to the call made alone."""
+    """Graphs holding the head_dim-64 paired range decode (kv heads two per wave, merge), the
+    head_dim-256 per-sequence decode (four-wave workgroups, one kernel) and the split
+    per-sequence decode of one long sequence (records and merge_split_kernel), each replayed
+    between eager calls of another on the same stream; every output bit-identical to the call
+    made alone."""
     cases = []
     for lens, seed, hq, hkv, d in (([4000, 17, 2600, 0, 900], 81, 32, 8, 64),
-                                   ([300, 5, 512, 64], 82, 16, 8, 256)):
+                                   ([300, 5, 512, 64], 82, 16, 8, 256),
+                                   ([20000, 0], 83, 28, 4, 128)):
         c = decode_case(lens, seed=seed, hq=hq, hkv=hkv, head_dim=d, extra_blocks=3)
         q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
         cases.append(lambda q=q, kc=kc, vc=vc, bt=bt, sl=sl, ks=ks, vs=vs:
@@ -213,9 +216,10 @@ def test_graph_replays_at_head_dims_64_and_256(cuda, host_path):
         for rep in range(4):
             for i, (g, out) in enumerate(zip(graphs, captured)):
                 out[0].zero_()
-                other = cases[1 - i]()
+                j = (i + 1) % len(cases)
+                other = cases[j]()
                 g.replay()
                 s.synchronize()
                 _check(out, refs[i], f"graph {i} replay {rep}")
-                _check(other, refs[1 - i], f"eager call beside graph {i}, replay {rep}")
+                _check(other, refs[j], f"eager call beside graph {i}, replay {rep}")
                 _ = (other[0].float() * 2).sum().item()  # eager work and a sync between replays

@@ -4,7 +4,8 @@ It must give exactly what int8kv_paged_decode gives with a caller's workspace (s
 same plan, partials in the library's fixed scratch array instead).  Two calls in a row on the
 same GPU, the second with a smaller input, both bit-identical to the workspace entry point and
 within the oracle bar; then the INT8 x BF16-cache and forced-range variants, the merge indexed by
-range, head_dim 256, and head_dim 64 (kv-head pairs, per-sequence layout).
+range, head_dim 256, head_dim 64 (kv-head pairs, per-sequence layout) and the split
+per-sequence layout.
 """
 
 from __future__ import annotations
@@ -98,13 +99,16 @@ def test_range_indexed_merge_and_head_dim_256(cuda):
         assert err <= MAX_ABS and cos >= MIN_COS, (what, err, cos)
 
 
-def test_head_dim_64_pairs_and_per_sequence(cuda):
+def test_head_dim_64_and_split_layouts(cuda):
     """head_dim 64 with kv heads taken in pairs (twice the automatic range count, sized by the
-    entry point from the pairs), then a short call that takes the per-sequence layout."""
-    for lens, seed, what in (([5000, 1, 3000, 0, 4100, 77], 37, "head_dim 64 pairs"),
-                             ([300, 12, 512], 38, "head_dim 64 per-sequence")):
+    entry point from the pairs), a short call that takes the per-sequence layout, then one long
+    sequence in the split per-sequence layout (its records in the scratch array)."""
+    for lens, seed, hq, hkv, d, what in (
+            ([5000, 1, 3000, 0, 4100, 77], 37, 32, 8, 64, "head_dim 64 pairs"),
+            ([300, 12, 512], 38, 32, 8, 64, "head_dim 64 per-sequence"),
+            ([30000], 39, 28, 4, 128, "one long sequence, split per-sequence layout")):
         print(f"noalloc: {what}", flush=True)
-        case = decode_case(lens, seed=seed, hq=32, hkv=8, head_dim=64, extra_blocks=3)
+        case = decode_case(lens, seed=seed, hq=hq, hkv=hkv, head_dim=d, extra_blocks=3)
         q, kc, vc, bt, sl, ks, vs = to_dev(case, cuda)
         want = _with_workspace(q, kc, vc, bt, sl, ks, vs)
         got = _noalloc(q, kc, vc, bt, sl, ks, vs, torch.full_like(q, float("nan")))
