@@ -175,7 +175,9 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *                 below instead (decided from head_dim, batch, num_kv_heads, table width and
  *                 block size only, with tokens = table width x block size and W = batch x
  *                 num_kv_heads workgroups; head_dim 128, INT8 cache: W <= CUs, and tokens <= 768,
- *                 or tokens <= 2048 with W >= (tiles per wave - 3) x CUs / 8, at most CUs / 2;
+ *                 or tokens <= 2048 with W >= (tiles per wave - 3) x CUs / 8, at most CUs / 2,
+ *                 except with W <= CUs / 8, 3 or more tiles per wave and W x tiles >= CUs (then
+ *                 the split layout below);
  *                 head_dim 128, 16-bit cache: W <= 3 CUs, and tokens <= 512, or tokens <= 1024
  *                 with W >= CUs / 2; head_dim 64: W <= 4 CUs, and for an INT8 cache tokens <=
  *                 1536, or tokens <= 2048 with W >= CUs / 8; for a 16-bit cache tokens <= 1024;

@@ -1202,6 +1202,8 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
     if (!SPLIT && wave == 0) write_zero_rows<QT, HD>(a, b, kvh, lane);
     return;
   }
+  // Loaded before the tile loop: after the barrier it would add a memory latency to every call.
+  const float vscale = (CACHE == kI8 && !SPLIT) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
   int64_t t0 = 0, span = n;  // this workgroup's tiles of the sequence
   if constexpr (SPLIT) {
     t0 = (int64_t)blockIdx.z * n / gridDim.z;
@@ -1261,7 +1263,6 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
     }
     return;
   }
-  const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
   const float inv = Ls > 0.0f ? vscale / Ls : 0.0f;
   char* op = a.out + (b * a.o_sb + (int64_t)(kvh * G + li) * a.o_sh) * esize<QT>();
   float o[HD / 16];
@@ -1292,6 +1293,7 @@ __global__ __launch_bounds__(64) void merge_split_kernel(DecodeArgs a) {
   for (int j = 0; j < D; ++j) O[j] = 0.0f;
   float inv = 0.0f;
   if (seq_len_of(a, b) > 0) {  // uniform: an empty sequence left no records (zero rows)
+    const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[h / a.group], 1e-6f) : 1.0f;
     const int64_t row0 = b * Z * a.num_q_heads + h;  // record z: row0 + z Hq
     const int64_t stride = (int64_t)a.num_q_heads * HD;
     const float* acc = a.ws_acc + row0 * HD + D * lane;
@@ -1334,7 +1336,6 @@ __global__ __launch_bounds__(64) void merge_split_kernel(DecodeArgs a) {
         }
       }
     }
-    const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[h / a.group], 1e-6f) : 1.0f;
     inv = Lw > 0.0f ? vscale / Lw : 0.0f;
   }
 #pragma unroll
@@ -1401,6 +1402,8 @@ __device__ __forceinline__ void merge_records(const DecodeArgs& a, int64_t b, in
   __shared__ float s_l[RS * MW][C4];
   __shared__ f32x4 s_o[RS * MW][C4];
   const int kvh = h / a.group;
+  // Loaded at entry: after the barrier below it would add a memory latency to every merge.
+  const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int rs = lane / C4;  // range slot of this lane within the wave
@@ -1443,7 +1446,6 @@ __device__ __forceinline__ void merge_records(const DecodeArgs& a, int64_t b, in
   O = (f32x4)(0.0f);
 #pragma unroll
   for (int k = 0; k < kStride; ++k) merge_in(M, L, O, s_m[k][c4], s_l[k][c4], s_o[k][c4]);
-  const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
   const float inv = L > 0.0f ? vscale / L : 0.0f;
   store4<QT>(a.out + (b * a.o_sb + (int64_t)h * a.o_sh + 4 * c4) * esize<QT>(), O * inv);
 }
@@ -1661,6 +1663,10 @@ bool use_per_sequence(bool int8_cache, int32_t head_dim, int64_t batch, int32_t 
   }
   if (!int8_cache) return wgs <= 3 * cu && (per_wave <= 2 || (per_wave <= 4 && 2 * wgs >= cu));
   if (wgs > cu) return false;
+  // Few workgroups with 3 or more tiles per wave: the split layout (use_split) spreads them over
+  // every CU once each of its workgroups gets a tile (B = 8 x 1024 11.7 -> 9.8 us, 8 x 768 10.5
+  // -> 8.9, 4 x 768 10.3 -> 9.6; B = 1 x 768, under a tile per split workgroup, 10.3 vs 10.9).
+  if (8 * wgs <= cu && per_wave >= 3 && tiles * (double)wgs >= (double)cu) return false;
   if (per_wave <= 3) return true;
   if (per_wave > 8) return false;
   const int64_t need = (per_wave - 3) * cu / 8;

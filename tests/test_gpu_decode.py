@@ -667,6 +667,8 @@ AUTO_LAYOUT_POINTS = [
     (128, 28, 4, "bf16", 200, 32, False),
     (128, 28, 4, "int8", 96, 32, False),    # INT8 at 128: at most one workgroup per CU
     (128, 28, 4, "int8", 48, 32, True),
+    (128, 28, 4, "int8", 8, 64, False),     # few workgroups, 4 tiles per wave: the split layout
+    (128, 28, 4, "int8", 1, 48, True),      # under a tile per split workgroup: per-sequence
     (256, 16, 8, "int8", 32, 32, True),     # 256: four waves per workgroup, 4 tiles per wave
     (256, 16, 8, "int8", 128, 16, False),   # 4 workgroups per CU: past the 3-per-CU cap
     (256, 16, 8, "int8", 8, 64, False),     # 8 tiles per wave: needs CUs / 2 workgroups
@@ -694,6 +696,7 @@ def test_automatic_layout_choice(cuda, d, hq, hkv, cache, batch, width, per_seq)
                     extra_blocks=3)
     assert c.block_tables.shape[1] == width
     q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    q = q.float()  # fp32 outputs: a bf16 rounding could hide a different summation order
     if cache == "int8":
         ref = oracle_int8(c)
         auto = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs)
@@ -753,6 +756,8 @@ AUTO_SPLIT_POINTS = [
     (64, 32, 8, 4, 1024, False),     # head_dim 64: 8 tiles per wave (paired range layout)
     (256, 16, 8, 1, 1024, True),     # head_dim 256: four waves, 4 tiles per wave
     (128, 28, 4, 16, 512, False),    # 4 workgroups per (sequence, kv head)
+    (128, 28, 4, 8, 64, True),       # preferred to the per-sequence layout: 4 tiles per wave there
+    (128, 28, 4, 1, 48, False),      # per-sequence layout: under a tile per split workgroup
 ]
 
 
@@ -771,6 +776,7 @@ def test_automatic_split_choice(cuda, d, hq, hkv, batch, width, split):
     c = decode_case(lens, seed=batch + width + 1, hq=hq, hkv=hkv, head_dim=d, width=width,
                     extra_blocks=3)
     q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    q = q.float()  # fp32 outputs: a bf16 rounding could hide a different summation order
     auto = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs)
     forced = torch.empty_like(q)
     _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, forced, 0,
