@@ -1687,7 +1687,7 @@ int32_t split_count(int64_t batch, int32_t num_kv_heads, int32_t num_ranges, int
 // per-sequence layout itself is not taken): the range layout cuts such a sequence into up to 256
 // ranges per kv head, whose records the merge then reads on one CU per query head (one 32k-token
 // sequence: 133 KB per query head, ~5.8 us of its 7 us), while the split layout leaves Z <= 64
-// records, already combined over eight waves in LDS.  Taken with at least 8 workgroups per
+// records, already combined over the workgroup's waves in LDS.  Taken with at least 8 workgroups per
 // (sequence, kv head) and at most 4 tiles per wave (2 at head_dim 64, whose 64-wide loads lose to
 // the range layout's paired kv heads beyond that).  Measured on MI355X (HIP-graph replays, op
 // time, automatic range layout vs split, us): 28/4 heads at head_dim 128, INT8: B = 1 x 32768
