@@ -740,7 +740,10 @@ __device__ __forceinline__ float round_half_away(float x) {
 //     137-146, :798-802); the operand is q8 and q_scale joins the score factor.  With QQ the
 //     q8 values are packed as int8 operands instead (q8op[ks] byte e of lane (li, lg) =
 //     lane element 16 ks + e of q8, matching the int8 K bytes the lane holds).
-template <int CACHE, int QT, bool QQ, int HD, bool PAIR = false>
+//   HEADWISE: the 2^e scale per query head (the 4 lanes holding a head's elements, whose score
+//   column is the same lane's), two lane exchanges instead of six; the per-sequence kernels use
+//   it (their short calls wait on every exchange: ~0.15 us of a 6.5 us kernel on MI355X).
+template <int CACHE, int QT, bool QQ, int HD, bool PAIR = false, bool HEADWISE = false>
 __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRaw<QT, HD>& raw,
                                               int kvh, typename MfmaOp<CACHE>::T (&qop)[HD / 32],
                                               typename MfmaOp<CACHE>::T (&qlo)[HD / 32],
@@ -800,10 +803,12 @@ __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRa
   }
   float qmul = 1.0f;
   if constexpr (CACHE != kBF16) {
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
-    amax = fmaxf(amax, __shfl_xor(amax, 4));
-    amax = fmaxf(amax, __shfl_xor(amax, 8));
+    if constexpr (!HEADWISE) {
+      amax = fmaxf(amax, __shfl_xor(amax, 1));
+      amax = fmaxf(amax, __shfl_xor(amax, 2));
+      amax = fmaxf(amax, __shfl_xor(amax, 4));
+      amax = fmaxf(amax, __shfl_xor(amax, 8));
+    }
     amax = fmaxf(amax, __shfl_xor(amax, 16));
     amax = fmaxf(amax, __shfl_xor(amax, 32));
     if (amax > 0.0f && amax < INFINITY) {
@@ -938,7 +943,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     QueryRaw<QT, HD> qraw;
     issue_query<QT, HD, PAIR>(a, b, kvh, li, lg, qraw);
     chunk_prologue();
-    s_scale = finish_query<CACHE, QT, QQ, HD, PAIR>(a, qraw, kvh, qop, qlo, q8op);
+    s_scale = finish_query<CACHE, QT, QQ, HD, PAIR, GROUP>(a, qraw, kvh, qop, qlo, q8op);
   }
 
   // Tile t + d (buffer d): scores, refill K with tile t + d + DEPTH, P*V, refill V.  refill is a
