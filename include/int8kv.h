@@ -181,8 +181,9 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *                 head_dim 128, 16-bit cache: W <= 3 CUs, and tokens <= 512, or tokens <= 1024
  *                 with W >= CUs / 2; head_dim 64: W <= 4 CUs, and for an INT8 cache tokens <=
  *                 1536, or tokens <= 2048 with W >= CUs / 8; for a 16-bit cache tokens <= 1024;
- *                 head_dim 256: W <= 3 CUs, and for an INT8 cache tokens <= 512, or tokens <=
- *                 1024 with CUs / 2 <= W <= CUs; for a 16-bit cache tokens <= 256, or tokens <=
+ *                 head_dim 256: W <= 3 CUs, and for an INT8 cache tokens <= 512 (not with W <=
+ *                 CUs / 8 above 256 tokens: the split layout below), or tokens <= 1024 with
+ *                 CUs / 2 <= W <= CUs; for a 16-bit cache tokens <= 256, or tokens <=
  *                 512 with W >= CUs / 2).
  *   flags:        INT8KV_DECODE_ALL normally; MAIN and MERGE separately let a caller time the
  *                 two kernels on their own (MERGE must follow MAIN with identical arguments).

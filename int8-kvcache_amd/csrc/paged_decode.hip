@@ -1659,6 +1659,9 @@ bool use_per_sequence(bool int8_cache, int32_t head_dim, int64_t batch, int32_t 
   if (head_dim > 128) {  // four waves per workgroup, so twice the tiles per wave
     if (wgs > 3 * cu) return false;
     if (!int8_cache) return per_wave <= 2 || (per_wave <= 4 && 2 * wgs >= cu);
+    // Few workgroups with 3 or more tiles per wave: the split layout (use_split) spreads them
+    // over every CU (B = 1 / 2 / 4 x 512: 13.1 / 13.1 / 13.3 -> 11.2 / 10.5 / 11.2 us).
+    if (8 * wgs <= cu && per_wave >= 3) return false;
     return per_wave <= 4 || (per_wave <= 8 && 2 * wgs >= cu && wgs <= cu);
   }
   if (head_dim == 64) {

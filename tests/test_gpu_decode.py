@@ -670,6 +670,7 @@ AUTO_LAYOUT_POINTS = [
     (128, 28, 4, "int8", 8, 64, False),     # few workgroups, 4 tiles per wave: the split layout
     (128, 28, 4, "int8", 1, 48, True),      # under a tile per split workgroup: per-sequence
     (256, 16, 8, "int8", 32, 32, True),     # 256: four waves per workgroup, 4 tiles per wave
+    (256, 16, 8, "int8", 2, 32, False),     # few workgroups with 4 tiles per wave: the split layout
     (256, 16, 8, "int8", 128, 16, False),   # 4 workgroups per CU: past the 3-per-CU cap
     (256, 16, 8, "int8", 8, 64, False),     # 8 tiles per wave: needs CUs / 2 workgroups
     (256, 16, 8, "int8", 32, 64, True),
@@ -758,6 +759,7 @@ AUTO_SPLIT_POINTS = [
     (128, 28, 4, 16, 512, False),    # 4 workgroups per (sequence, kv head)
     (128, 28, 4, 8, 64, True),       # preferred to the per-sequence layout: 4 tiles per wave there
     (128, 28, 4, 1, 48, False),      # per-sequence layout: under a tile per split workgroup
+    (256, 16, 8, 2, 32, True),       # preferred to the four-wave per-sequence layout at 256
 ]
 
 
