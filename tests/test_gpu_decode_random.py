@@ -5,8 +5,9 @@ a GQA shape (group 1-16, including one kv head), head_dim 64 or 128, a cache blo
 tokens, the query dtype, the table and length dtypes, the split count, ``impl`` and
 ``quantize_q``, then checks ``int8_paged_attention`` (and, for a third of the cases,
 ``bf16_paged_attention`` on the same K/V in a 16-bit cache) against the fp32 oracle at the
-usual bar (max |diff| <= 2e-2, cosine >= 0.9999; empty sequences exactly zero).  Two more sets repeat
-the draws at head_dim 256 and at head_dim 64.  The seeds are fixed, so a failure names a reproducible case.
+usual bar (max |diff| <= 2e-2, cosine >= 0.9999; empty sequences exactly zero).  Three more sets
+repeat the draws at head_dim 256, at head_dim 64, and forced into the split per-sequence layout.  The
+seeds are fixed, so a failure names a reproducible case.
 """
 
 from __future__ import annotations
@@ -109,3 +110,45 @@ def test_random_configuration_head_dim_64(cuda, seed):
     hq, hkv = [(32, 8), (24, 8), (16, 2), (8, 8), (12, 3), (24, 2)][seed % 6]
     p.update(hq=hq, hkv=hkv, d=64)
     _run(cuda, p, seed)
+
+
+@pytest.mark.parametrize("seed", range(300, 310))
+def test_random_configuration_split_layout(cuda, seed):
+    """The random draws forced into the split per-sequence layout (INT8KV_DECODE_SPLIT_SEQUENCES:
+    several per-sequence workgroups per sequence and kv head, records merged per query head) at
+    head_dim 64, 128 and 256, with the drawn block size, table / length dtypes, query dtype and
+    quantize_q; a 16-bit cache for a third of them."""
+    from int8kv import _decode, _lib
+
+    p = _draw(seed)
+    d = (64, 128, 256)[seed % 3]
+    hq, hkv = [(28, 4), (32, 8), (16, 8), (8, 1), (14, 2)][seed % 5]
+    p.update(hq=hq, hkv=hkv, d=d)
+    lens = p["lens"][:6]
+    c = decode_case(lens, seed=seed, hq=hq, hkv=hkv, head_dim=d, block_size=p["bs"],
+                    randn_kv=p["randn"], extra_blocks=5)
+    q = c.query.to(p["qdtype"]).to(cuda)
+    _, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    if p["bt64"]:
+        bt = bt.to(torch.int64)
+    if p["sl64"]:
+        sl = sl.to(torch.int64)
+    flags = _lib.DECODE_ALL | _lib.DECODE_SPLIT_SEQUENCES | (_lib.DECODE_QUANTIZE_Q if p["qq"] else 0)
+    out = torch.full_like(q, float("nan"))
+    _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, out, 0, flags)
+    torch.cuda.synchronize()
+    what = f"seed {seed}: d={d} {hq}/{hkv} lens={lens} bs={p['bs']} {p['qdtype']} qq={p['qq']}"
+    ref = O.paged_attention_ref(q.float().cpu().numpy(), c.kc, c.vc, c.block_tables.numpy(),
+                                c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
+                                quantize_q=p["qq"])
+    _check(out, ref, lens, "split int8 " + what)
+    if p["bf16"]:
+        k16, v16 = bf16_caches(c)
+        out16 = torch.full_like(q, float("nan"))
+        _decode.paged_decode(q, k16.to(cuda), v16.to(cuda), bt, sl, None, None, out16, 0,
+                             _lib.DECODE_ALL | _lib.DECODE_SPLIT_SEQUENCES)
+        torch.cuda.synchronize()
+        ref16 = O.paged_attention_ref(q.float().cpu().numpy(), k16.float().numpy(),
+                                      v16.float().numpy(), c.block_tables.numpy(),
+                                      c.seq_lens.numpy())
+        _check(out16, ref16, lens, "split bf16 " + what)
