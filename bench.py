@@ -461,6 +461,78 @@ MIDSIZE_CASES = (("B32x8256", 32, 8256, False), ("B32xU16k", 32, 16384, True),
                  ("B256xU2k", 256, 2048, True))
 
 
+# Short and few-sequence decode calls across head_dim and cache type, for the host's choice of
+# layout: (head_dim, q heads, kv heads, cache, batch, uniform length).  Qwen2.5-7B (28/4) at 128,
+# Llama-3.2-1B (32/8) at 64, Gemma-2-9B (16/8) at 256.
+LAYOUT_CASES = (
+    (128, 28, 4, "int8", 1, 512), (128, 28, 4, "int8", 8, 1024), (128, 28, 4, "int8", 4, 768),
+    (128, 28, 4, "int8", 1, 32768), (128, 28, 4, "int8", 2, 8192), (128, 28, 4, "int8", 16, 8192),
+    (128, 28, 4, "bf16", 1, 8192), (128, 28, 4, "bf16", 128, 512),
+    (64, 32, 8, "int8", 1, 1024), (64, 32, 8, "int8", 128, 2048), (64, 32, 8, "int8", 1, 8192),
+    (64, 32, 8, "int8", 4, 16384), (64, 32, 8, "bf16", 8, 1024),
+    (256, 16, 8, "int8", 1, 256), (256, 16, 8, "int8", 2, 512), (256, 16, 8, "int8", 32, 512),
+    (256, 16, 8, "int8", 1, 16384), (256, 16, 8, "bf16", 16, 512),
+)
+
+
+def layout_legs(dev, out_path: str | None) -> dict:
+    """Per case: the automatic call against each layout forced (per-sequence, split per-sequence,
+    and the range layout with the automatic range count and 2-tile minimum), op time per call from
+    HIP-graph replays (median of three); random K/V in a shuffled pool of exactly the needed
+    blocks plus 16."""
+    import torch
+
+    from int8kv import _decode, _lib
+
+    lib = _lib.load()
+    rows = []
+    for d, hq, hkv, cache, B, ctx in LAYOUT_CASES:
+        per = 2 * hq * (d + 2) * 4 + 32
+        ws_bytes = lib.int8kv_decode_workspace_bytes(hq, hkv, d, 16, 0)
+        auto_ranges = ws_bytes // per
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        g = torch.Generator().manual_seed(B * ctx + d)
+        width = (ctx + 15) // 16
+        nb = B * width + 16
+        bt = torch.randperm(nb, generator=g)[: B * width].view(B, width).to(torch.int32).to(dev)
+        sl = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+        if cache == "int8":
+            kc = torch.randint(-127, 128, (nb, 16, hkv, d), dtype=torch.int8, device=dev)
+            vc = torch.randint(-127, 128, (nb, 16, hkv, d), dtype=torch.int8, device=dev)
+            ks = torch.full((hkv,), 0.05, device=dev)
+            vs = torch.full((hkv,), 0.01, device=dev)
+        else:
+            kc = torch.randn(nb, 16, hkv, d, device=dev).to(torch.bfloat16)
+            vc = torch.randn(nb, 16, hkv, d, device=dev).to(torch.bfloat16)
+            ks = vs = None
+        q = torch.randn(B, hq, d, device=dev).to(torch.bfloat16)
+        out = torch.empty_like(q)
+        row = {"head_dim": d, "heads": f"{hq}/{hkv}", "cache": cache, "B": B, "ctx": ctx}
+        for name, ranges, min_tiles, flags in (
+                ("auto", 0, 0, _lib.DECODE_ALL),
+                ("per_sequence", 0, 0, _lib.DECODE_ALL | _lib.DECODE_PER_SEQUENCE),
+                ("split", 0, 0, _lib.DECODE_ALL | _lib.DECODE_SPLIT_SEQUENCES),
+                ("range", int(auto_ranges), 2, _lib.DECODE_ALL)):
+            def call():
+                _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, out, ranges, flags, ws, min_tiles)
+            if d > 128 and name == "per_sequence" and ctx > 4096:
+                row[name + "_us"] = None  # a whole long sequence on one four-wave workgroup
+                continue
+            call()
+            torch.cuda.synchronize()
+            row[name + "_us"] = round(sorted(time_graph(call, settle_ms=10.0) * 1e3
+                                             for _ in range(3))[1], 2)
+        rows.append(row)
+        log(f"layouts d={d} {hq}/{hkv} {cache} B={B} ctx={ctx}: " +
+            ", ".join(f"{k[:-3]} {v}" for k, v in row.items() if k.endswith("_us")))
+        del kc, vc, q, out, ws
+    res = {"layouts": rows}
+    if out_path:
+        Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+        Path(out_path).write_text(json.dumps(res, indent=1))
+    return res
+
+
 def midsize_legs(dev, out_path: str | None) -> dict:
     """INT8 decode at the mid sizes above (random int8 K/V in a pool just larger than the batch
     needs, shuffled block tables, Qwen2.5-7B attention shape).  Per case: the decode kernel alone
@@ -608,6 +680,9 @@ def main() -> int:
                          "for rocprofv3 counter passes) and print their JSON")
     ap.add_argument("--midsize", metavar="JSON", default=None,
                     help="only the mid-size INT8 decode cases (B=32 x 8256 ...), results to JSON")
+    ap.add_argument("--layouts", metavar="JSON", default=None,
+                    help="only the layout comparison (automatic vs each forced layout over head_dim "
+                         "64/128/256 short and few-sequence calls), results to JSON")
     ap.add_argument("--sweep", metavar="JSON", default=None,
                     help="also measure the config-2 decode sweep, written to JSON")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -647,6 +722,9 @@ def main() -> int:
         return 0
     if args.midsize:
         midsize_legs(dev, args.midsize)
+        return 0
+    if args.layouts:
+        layout_legs(dev, args.layouts)
         return 0
     if args.writes_only:
         res = write_legs(dev, cfg1_graph=False)
