@@ -490,7 +490,7 @@ def layout_legs(dev, out_path: str | None) -> dict:
         per = 2 * hq * (d + 2) * 4 + 32
         ws_bytes = lib.int8kv_decode_workspace_bytes(hq, hkv, d, 16, 0)
         auto_ranges = ws_bytes // per
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
         g = torch.Generator().manual_seed(B * ctx + d)
         width = (ctx + 15) // 16
         nb = B * width + 16
@@ -557,32 +557,195 @@ def midsize_legs(dev, out_path: str | None) -> dict:
         vs = torch.full((4,), 0.01, device=dev)
         sl = lens.to(torch.int32).to(dev)
         out = torch.empty_like(q)
-        ws = torch.empty(_lib.load().int8kv_decode_workspace_bytes(28, 4, 128, 16, 0),
+        ws = torch.zeros(_lib.load().int8kv_decode_workspace_bytes(28, 4, 128, 16, 0),
                          dtype=torch.uint8, device=dev)
 
         def call(flags):
             return lambda: _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, out, 0, flags, ws, 0)
 
+        plan = _lib.decode_plan(q.dtype, kc.dtype, B, 28, 4, 128, nb, 16, bt.shape[1])
         settle(call(_lib.DECODE_ALL), batch=20, min_ms=30.0)
         ms_main = time_events(call(_lib.DECODE_MAIN), 50, 10)
         ms_op = time_graph(call(_lib.DECODE_ALL))
-        ms_merge = time_graph(call(_lib.DECODE_MERGE))
+        # A second (merge) kernel only in the layouts that have one.
+        ms_merge = time_graph(call(_lib.DECODE_MERGE)) if plan["kernels"] == 2 else None
         nbytes = roofline.decode_bytes(lens.numpy(), 4, 128, 1, B, 28)
         row = {"case": name, "batch": B, "tokens": int(lens.sum()), "bytes": nbytes,
+               "layout": plan["layout"], "merge": plan["merge"], "kernels": plan["kernels"],
                "decode_kernel_us": round(ms_main * 1e3, 2),
                "decode_kernel_TBps": round(nbytes / ms_main / 1e9, 3),
-               "merge_graph_us": round(ms_merge * 1e3, 2), "op_graph_us": round(ms_op * 1e3, 2),
-               "op_TBps": round(nbytes / ms_op / 1e9, 3)}
+               "merge_graph_us": None if ms_merge is None else round(ms_merge * 1e3, 2),
+               "op_graph_us": round(ms_op * 1e3, 2), "op_TBps": round(nbytes / ms_op / 1e9, 3)}
         rows.append(row)
-        log(f"midsize {name}: decode kernel {row['decode_kernel_us']} us "
+        log(f"midsize {name}: first kernel {row['decode_kernel_us']} us "
             f"({row['decode_kernel_TBps']} TB/s), op {row['op_graph_us']} us ({row['op_TBps']} TB/s), "
-            f"merge {row['merge_graph_us']} us")
+            f"{plan['layout']} layout, merge {plan['merge']} {row['merge_graph_us']}")
         del kc, vc
     res = {"midsize": rows}
     if out_path:
         Path(out_path).parent.mkdir(parents=True, exist_ok=True)
         Path(out_path).write_text(json.dumps(res, indent=1))
     return res
+
+
+def graph_us(fns, replays: int = 10, settle_ms: float = 30.0) -> float:
+    """Device time (us) of one replay of a HIP graph that captures ``fns`` once each, in order."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for fn in fns:
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for fn in fns:
+            fn()
+    torch.cuda.synchronize()
+    settle(graph.replay, batch=1, min_ms=settle_ms, max_ms=4 * settle_ms)
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(replays):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / replays
+
+
+# Config 4's attention call as the decode loop makes it: B = 32 sequences at one decode step of
+# the 8192-token prompts (8193 tokens), each sequence owning its blocks of a shuffled pool of
+# B x 520 blocks (tables 520 wide), one pool per layer in one [layers, blocks, 16, 4, 128] tensor.
+COLD_CASE = dict(batch=32, length=8193, width=520, layers=28)
+
+
+class ColdSetup:
+    """Config 4's per-layer attention inputs (28 layer pools of random int8 K/V) and, for the
+    "between layers" traffic, the decode step's four per-layer GEMMs on random bf16 weights of
+    Qwen2.5-7B's shapes (qkv 3584 -> 4608, o 3584 -> 3584, gate_up 3584 -> 37888, down 18944 ->
+    3584; 0.5 GB per layer, 13.9 GB in all) with M = 32 rows, as the decode step runs them."""
+
+    def __init__(self, dev):
+        import torch
+
+        from int8kv import _lib, roofline
+
+        c = COLD_CASE
+        B, L, W, NL = c["batch"], c["length"], c["width"], c["layers"]
+        self.B, self.L, self.NL = B, L, NL
+        nb = B * W
+        g = torch.Generator().manual_seed(2)
+        self.bt = torch.randperm(nb, generator=g).to(torch.int32).view(B, W).to(dev)
+        gd = torch.Generator(device=dev).manual_seed(3)
+        self.kc = torch.randint(-127, 128, (NL, nb, 16, 4, 128), dtype=torch.int8, device=dev, generator=gd)
+        self.vc = torch.randint(-127, 128, (NL, nb, 16, 4, 128), dtype=torch.int8, device=dev, generator=gd)
+        self.q = torch.randn(B, 28, 128, device=dev, generator=gd).to(torch.bfloat16)
+        self.ks = torch.full((NL, 4), 0.02, device=dev)
+        self.vs = torch.full((NL, 4), 0.01, device=dev)
+        self.sl = torch.full((B,), L, dtype=torch.int32, device=dev)
+        self.out = torch.empty_like(self.q)
+        self.ws = torch.zeros(_lib.load().int8kv_decode_workspace_bytes(28, 4, 128, 16, 0),
+                              dtype=torch.uint8, device=dev)
+        self.nbytes = roofline.decode_bytes([L] * B, 4, 128, 1, B, 28)
+
+        def w(n, k):
+            return (torch.randn(NL, n, k, device=dev, generator=gd) * 0.02).to(torch.bfloat16)
+
+        self.wqkv, self.wo, self.wgu, self.wdown = w(4608, 3584), w(3584, 3584), w(37888, 3584), w(3584, 18944)
+        self.x = torch.randn(B, 3584, device=dev, generator=gd).to(torch.bfloat16)
+        self.act = torch.randn(B, 18944, device=dev, generator=gd).to(torch.bfloat16)
+        self.y = [torch.empty(B, n, device=dev, dtype=torch.bfloat16) for n in (4608, 3584, 37888, 3584)]
+        self.weight_bytes = sum(t[0].numel() * 2 for t in (self.wqkv, self.wo, self.wgu, self.wdown))
+
+    def op(self, layer, flags=None):
+        from int8kv import _decode, _lib
+
+        fl = _lib.DECODE_ALL if flags is None else flags
+        return lambda: _decode.paged_decode(self.q, self.kc[layer], self.vc[layer], self.bt, self.sl,
+                                            self.ks[layer], self.vs[layer], self.out, 0, fl, self.ws, 0)
+
+    def gemms(self, layer):
+        import torch
+
+        def run():
+            torch.mm(self.x, self.wqkv[layer].t(), out=self.y[0])
+            torch.mm(self.x, self.wo[layer].t(), out=self.y[1])
+            torch.mm(self.x, self.wgu[layer].t(), out=self.y[2])
+            torch.mm(self.act, self.wdown[layer].t(), out=self.y[3])
+        return run
+
+
+def cold_legs(dev, out_path: str | None) -> dict:
+    """The decode op (decode + merge) at config 4's per-layer shape with warm and cold caches.
+
+    * rotate_N: one HIP graph of 28 calls over N distinct layer pools (layer i % N), per call.
+      N = 1 repeats one 272 MB pool (the midsize figure), N = 28 touches each pool once per
+      replay, as the decode step does.
+    * between_gemms: 28 x (layer i's four GEMMs, then the call on layer i's pool), minus the same
+      graph without the calls: the attention call in the decode step's traffic (0.5 GB of
+      weights streamed between two layers' calls).  Also for the decode kernel alone.
+    Kernel durations inside each graph come from a kernel trace of this same leg."""
+    import torch
+
+    from int8kv import _lib
+
+    cs = ColdSetup(dev)
+    NL, nbytes = cs.NL, cs.nbytes
+    res = {"case": {**COLD_CASE, "tokens": cs.B * cs.L, "bytes_per_call": nbytes,
+                    "weight_bytes_per_layer": cs.weight_bytes}}
+    for n in (1, 28):
+        us = graph_us([cs.op(i % n) for i in range(NL)]) / NL
+        res[f"rotate_{n}_op_us"] = round(us, 2)
+        res[f"rotate_{n}_op_TBps"] = round(nbytes / us / 1e6, 3)
+        log(f"cold: rotate over {n} pools: op {us:.2f} us ({nbytes / us / 1e6:.2f} TB/s)")
+    base = graph_us([cs.gemms(i) for i in range(NL)])
+    for name, flags in (("op", _lib.DECODE_ALL), ("decode", _lib.DECODE_MAIN)):
+        fns = []
+        for i in range(NL):
+            fns += [cs.gemms(i), cs.op(i, flags)]
+        us = (graph_us(fns) - base) / NL
+        res[f"between_gemms_{name}_us"] = round(us, 2)
+        res[f"between_gemms_{name}_TBps"] = round(nbytes / us / 1e6, 3)
+        log(f"cold: between the GEMMs: {name} {us:.2f} us ({nbytes / us / 1e6:.2f} TB/s)")
+    res["gemms_per_layer_us"] = round(base / NL, 2)
+    del cs
+    torch.cuda.empty_cache()
+    if out_path:
+        Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+        Path(out_path).write_text(json.dumps({"cold": res}, indent=1))
+    return res
+
+
+def counter_run(dev, mode: str) -> None:
+    """Eager calls for a rocprofv3 counter pass (the profiler serialises counted dispatches, so
+    graphs are not used): "warm" = 40 calls on one layer pool; "cold" = 2 x 28 layers of (the
+    layer's GEMMs, the call on its pool); "cfg3" = 10 INT8 and 10 BF16 calls of the headline
+    workload."""
+    import torch
+
+    if mode == "cfg3":
+        import int8kv
+
+        w = build_workload(dev)
+        for _ in range(10):
+            int8kv.int8_paged_attention(w["q"], w["kc"], w["vc"], w["bt"], w["sl"], w["ks"], w["vs"])
+        for _ in range(10):
+            int8kv.bf16_paged_attention(w["q"], w["kc16"], w["vc16"], w["bt"], w["sl"])
+        torch.cuda.synchronize()
+        return
+    cs = ColdSetup(dev)
+    if mode == "warm":
+        for _ in range(40):
+            cs.op(0)()
+    else:
+        for _ in range(2):
+            for i in range(cs.NL):
+                cs.gemms(i)()
+                cs.op(i)()
+    torch.cuda.synchronize()
+    log(f"counter run {mode}: done")
 
 
 def tpot_config4(dev, out_path: str | None, batch: int = 32, context: int = 8192,
@@ -680,6 +843,12 @@ def main() -> int:
                          "for rocprofv3 counter passes) and print their JSON")
     ap.add_argument("--midsize", metavar="JSON", default=None,
                     help="only the mid-size INT8 decode cases (B=32 x 8256 ...), results to JSON")
+    ap.add_argument("--cold", metavar="JSON", default=None,
+                    help="only config 4's per-layer decode call with warm and cold caches (28 "
+                         "layer pools rotated, and between the decode step's GEMMs), results to JSON")
+    ap.add_argument("--counter-run", choices=("warm", "cold", "cfg3"), default=None,
+                    help="only eager decode calls for a rocprofv3 counter pass (config 4's call on "
+                         "a warm pool or between the step's GEMMs, or the headline workload)")
     ap.add_argument("--layouts", metavar="JSON", default=None,
                     help="only the layout comparison (automatic vs each forced layout over head_dim "
                          "64/128/256 short and few-sequence calls), results to JSON")
@@ -726,6 +895,12 @@ def main() -> int:
     if args.layouts:
         layout_legs(dev, args.layouts)
         return 0
+    if args.cold:
+        cold_legs(dev, args.cold)
+        return 0
+    if args.counter_run:
+        counter_run(dev, args.counter_run)
+        return 0
     if args.writes_only:
         res = write_legs(dev, cfg1_graph=False)
         if args.calibrate_copy:
@@ -748,7 +923,7 @@ def main() -> int:
     # Decode kernel alone (no merge), same arguments as int8_call, workspace preallocated.
     chunk = 0
     need = _lib.load().int8kv_decode_workspace_bytes(28, 4, 128, 16, chunk)
-    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(max(need, 16), dtype=torch.uint8, device=dev)
     out_main = torch.empty_like(w["q"])
 
     def main_kernel():
@@ -765,9 +940,11 @@ def main() -> int:
     log(f"settle: {st}")
     ms = time_loop(int8_call, args.steps, args.warmup)
     ms_main = time_events(main_kernel, args.steps, args.warmup)
-    # The merge kernel takes a few microseconds, less than the host's cost of one call: HIP-graph
-    # replays give its device time.
-    ms_merge = time_graph(merge_kernel)
+    plan = _lib.decode_plan(w["q"].dtype, w["kc"].dtype, 64, 28, 4, 128, w["num_blocks"], 16,
+                            w["bt"].shape[1])
+    # A separate merge kernel (when the layout has one) takes a few microseconds, less than the
+    # host's cost of one call: HIP-graph replays give its device time.
+    ms_merge = time_graph(merge_kernel) if plan["kernels"] == 2 else None
     # Each later op gets a short settle of its own: switching from one sustained load to another
     # (the BF16 op after the INT8 one) showed the same kind of dip for a few ms.
     settle(bf16_call, batch=10, min_ms=30.0)
@@ -815,7 +992,8 @@ def main() -> int:
     value = nbytes8 / (ms * 1e-3) / 1e9
     achieved = nbytes8 / (ms_main * 1e-3) / 1e9
     log(f"int8 op: {ms * 1e3:.1f} us/call ({value:.0f} GB/s); decode kernel {ms_main * 1e3:.1f} us "
-        f"({achieved:.0f} GB/s); merge kernel {ms_merge * 1e3:.1f} us; bf16 op {ms16 * 1e3:.1f} us "
+        f"({achieved:.0f} GB/s); merge kernel {ms_merge and round(ms_merge * 1e3, 1)} us; "
+        f"bf16 op {ms16 * 1e3:.1f} us "
         f"({nbytes16 / (ms16 * 1e-3) / 1e9:.0f} GB/s); int8 quantize_q op {ms_q * 1e3:.1f} us; "
         f"host enqueue {host_us:.1f} us/call, {host_us_queued:.1f} queued (ctypes path "
         f"{host_us_ctypes:.1f}, {host_us_ctypes_queued:.1f})")
@@ -846,7 +1024,8 @@ def main() -> int:
             "bf16_algorithmic_bytes_per_call": int(nbytes16),
             "int8_speedup_vs_bf16": round(ms16 / ms, 3),
             "decode_kernel_us": round(ms_main * 1e3, 2),
-            "merge_kernel_us_graph_replay": round(ms_merge * 1e3, 2),
+            "merge_kernel_us_graph_replay": None if ms_merge is None else round(ms_merge * 1e3, 2),
+            "plan": plan,
             "int8_quantize_q_us_per_call": round(ms_q * 1e3, 2),
             "frac_of_hbm_peak_whole_call": round(value / HBM_PEAK_GBS, 4),
             "host_enqueue_us_per_call": round(host_us, 2),

@@ -26,6 +26,8 @@
  *                           src/triton_ops/int8_paged_attention.py:594-603
  *   int8kv_decode_auto_ranges <- the split-count heuristic _choose_num_splits,
  *                           src/triton_ops/int8_paged_attention.py:39-49
+ *   int8kv_decode_plan   <- the dispatcher's host-side choices, _choose_num_splits and _auto_impl
+ *                           (src/triton_ops/int8_paged_attention.py:39-58, used at :726-763)
  */
 #ifndef INT8KV_H
 #define INT8KV_H
@@ -137,6 +139,53 @@ int32_t int8kv_decode_auto_ranges(int32_t num_kv_heads);
 size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                                      int32_t block_size, int32_t num_ranges);
 
+/* Layouts and merge kernels reported by int8kv_decode_plan. */
+#define INT8KV_LAYOUT_RANGES 0       /* equal ranges of the batch's token stream */
+#define INT8KV_LAYOUT_PER_SEQUENCE 1 /* one workgroup per (sequence, kv head), no merge */
+#define INT8KV_LAYOUT_SPLIT 2        /* `split` workgroups per (sequence, kv head) + merge */
+#define INT8KV_MERGE_NONE 0
+#define INT8KV_MERGE_BY_SEQUENCE 1   /* one workgroup per (sequence, query head) */
+#define INT8KV_MERGE_BY_RANGE 2      /* one wave per (range, query head) */
+#define INT8KV_MERGE_SPLIT 3         /* the split layout's records, one wave per (sequence, q head) */
+
+/* What int8kv_paged_decode does for given sizes (int8kv_decode_plan). */
+typedef struct int8kv_decode_plan_t {
+  int32_t layout;               /* INT8KV_LAYOUT_* */
+  int32_t kernels;              /* kernel launches of a call with INT8KV_DECODE_ALL (0 for batch 0) */
+  int32_t num_ranges;           /* ranges layout: most ranges the token stream is cut into; every
+                                   layout: the range count the workspace is sized by */
+  int32_t min_tiles;            /* ranges layout: smallest range, in 32-token tiles */
+  int32_t seq_cost;             /* ranges layout: stream units charged per sequence start */
+  int32_t ranges_per_workgroup; /* ranges layout: 1, or 2 (paired ranges); 0 otherwise */
+  int32_t depth;                /* 32-token tiles of K/V loads in flight per wave */
+  int32_t kv_pair;              /* 1: head_dim 64, two kv heads per wave as one 128-wide head */
+  int32_t split;                /* split layout: workgroups per (sequence, kv head); else 0 */
+  int32_t non_temporal;         /* 1: K/V loads carry the non-temporal hint */
+  int32_t merge;                /* INT8KV_MERGE_* (the second kernel) */
+  int32_t merge_waves;          /* waves per merge workgroup (0 without a merge) */
+  int32_t merge_fold;           /* merge by sequence: records per lane slot and round */
+  int32_t compute_units;        /* compute units the plan was made for */
+  uint64_t workspace_bytes;     /* workspace the call needs */
+} int8kv_decode_plan_t;
+
+/*
+ * The plan int8kv_paged_decode (no_alloc = 0) or int8kv_paged_decode_noalloc (no_alloc = 1)
+ * follows for these sizes, without launching, allocating or reading device memory.  The
+ * arguments mean what they mean there; key_head_stride / value_head_stride are the caches'
+ * strides between kv heads in elements (key_cache_strides[2] / value_cache_strides[2]: head_dim
+ * 64 takes kv heads in pairs only when both equal head_dim).  compute_units: the device's CU
+ * count (256 on MI355X), or 0 for the current device (the only case that makes a HIP call).
+ * Returns 0 and fills *plan, or the negative code int8kv_paged_decode returns for these sizes.
+ * (The reference decides its split count and kernel on the host as well,
+ * src/triton_ops/int8_paged_attention.py:39-58.)
+ */
+int int8kv_decode_plan(int query_dtype, int cache_dtype, int64_t batch, int32_t num_q_heads,
+                       int32_t num_kv_heads, int32_t head_dim, int64_t num_blocks,
+                       int32_t block_size, int64_t table_width, int64_t key_head_stride,
+                       int64_t value_head_stride, int32_t num_ranges, int32_t min_tiles,
+                       uint32_t flags, int32_t compute_units, int32_t no_alloc,
+                       int8kv_decode_plan_t* plan);
+
 /*
  * Paged decode attention, one query token per sequence, GQA group = num_q_heads / num_kv_heads
  * (replaces int8_paged_attention, src/triton_ops/int8_paged_attention.py:683-769, and
@@ -159,7 +208,7 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *   out:          [batch, num_q_heads, head_dim] of query_dtype, innermost stride 1, rows
  *                 16-byte aligned.
  *   workspace:    at least int8kv_decode_workspace_bytes(...) bytes, 16-byte aligned; it needs
- *                 no initialisation.
+ *                 no initialisation.  Calls that share a workspace must not overlap.
  *   num_ranges:   the 32-token tiles of all sequences (each non-empty sequence also charged
  *                 a fixed start cost) form one stream per kv head, cut into
  *                 P = min(num_ranges, ceil(units / min_tiles)) equal ranges, one workgroup
@@ -196,12 +245,13 @@ size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num_kv_heads, 
  *                 softmax states on chip; one kernel, the workspace is not touched and MERGE
  *                 does nothing.  Suited to short sequences (each workgroup streams its whole
  *                 sequence on one compute unit).
- *                 OR INT8KV_DECODE_SPLIT_SEQUENCES for the split per-sequence layout: Z =
- *                 min(CUs / (batch x num_kv_heads), 64, 2 x num_ranges / batch) such workgroups
- *                 per (sequence, kv head), each over 1/Z of the sequence's tiles, leave one
- *                 partial record per query head in the workspace, and MERGE combines the Z
- *                 records (below Z = 2 it is the plain per-sequence layout).  Suited to a few
- *                 long sequences.  The automatic choice (num_ranges = 0, min_tiles = 0, when the
+ *                 OR INT8KV_DECODE_SPLIT_SEQUENCES for the split per-sequence layout: Z such
+ *                 workgroups per (sequence, kv head), each over 1/Z of the sequence's tiles,
+ *                 leave one partial record per query head in the workspace, and MERGE combines
+ *                 the Z records (below Z = 2 it is the plain per-sequence layout); Z =
+ *                 min(num_ranges / batch, 64) for a given num_ranges (S splits per sequence:
+ *                 num_ranges = S x batch), else min(CUs / (batch x num_kv_heads), 64,
+ *                 2 x automatic ranges / batch).  Suited to a few long sequences.  The automatic choice (num_ranges = 0, min_tiles = 0, when the
  *                 per-sequence layout is not taken) uses it when batch x num_kv_heads <= CUs / 8
  *                 and each wave then holds at most 4 tiles of 32 tokens (2 at head_dim 64) of
  *                 the longest possible sequence (table width x block size).
@@ -230,10 +280,13 @@ int int8kv_paged_decode(const void* query, int query_dtype, int64_t batch, int32
  * the process ends) instead of a caller's workspace.  It calls no allocator.
  *
  *   - The array belongs to the current device (hipGetDevice); `stream` must be on it.
- *   - A call whose partials need more than INT8KV_DECODE_SCRATCH_BYTES
+ *   - With num_ranges = 0 the automatic range count is lowered, if need be, to the most ranges
+ *     whose partials fit INT8KV_DECODE_SCRATCH_BYTES (16 MiB: the full automatic count of 256
+ *     ranges at 4 kv heads for a GQA group of up to 15 query heads per kv head at head_dim
+ *     128, 7 at 256; larger groups get fewer, longer ranges; int8kv_decode_plan(..., no_alloc
+ *     = 1, ...) reports the count).  A given num_ranges whose partials exceed the array
  *     (int8kv_decode_workspace_bytes(...) > INT8KV_DECODE_SCRATCH_BYTES) returns
- *     INT8KV_E_SCRATCH and launches nothing.  16 MiB holds the automatic range count for up to
- *     60 query heads at head_dim 128.
+ *     INT8KV_E_SCRATCH and launches nothing.
  *   - Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams,
  *     two threads) race and must be serialised by the caller.  The array keeps the last call's
  *     contents; the kernels need no clearing between calls.

@@ -53,1503 +53,15 @@
 //   * A running max is only moved when a tile's max exceeds it by more than 8 (log2 units), so
 //     most tiles skip the accumulator rescale; probabilities are then <= 2^8 (fits fp16/bf16).
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <mutex>
-#include <type_traits>
 
-#include "int8kv_common.h"
-
-namespace int8kv {
-
-// head_dim: 64, 128 or 256 (template parameter HD of the kernels).
-constexpr int kRows = 16;           // tokens per MFMA row group (half a tile)
-constexpr int kMaxGroup = 16;       // query heads per kv head (MFMA column count)
-constexpr int kChunkTiles = 256;    // tiles whose block ids a wave stages in LDS at a time
-constexpr int kMaxWavesPerWG = 4;
-
-// 16-token row groups per wave iteration ("tile"): 32 tokens, one MFMA k-step of P*V.
-template <int CACHE>
-constexpr int tile_blocks() {
-  return 2;
-}
-constexpr float kLazyRescale = 8.0f;
-constexpr float kLog2e = 1.4426950408889634f;
-
-struct DecodeArgs {
-  const char* q;
-  int64_t q_sb, q_sh;  // element strides
-  const char* kc;
-  const char* vc;
-  int64_t kc_sb, kc_ss, kc_sh;  // byte strides
-  int64_t vc_sb, vc_ss, vc_sh;
-  const void* bt;
-  int64_t bt_sb, bt_sl;  // element strides
-  const void* sl;
-  const float* k_scale;
-  const float* v_scale;
-  char* out;
-  int64_t o_sb, o_sh;  // element strides
-  float* ws_acc;       // [max_ranges * 2][num_q_heads][head_dim]
-  float* ws_m;         // [max_ranges * 2][num_q_heads]
-  float* ws_l;         // [max_ranges * 2][num_q_heads]
-  int64_t* ws_cut;     // [max_ranges][4]: (sequence, unit of its last tile) of the cut sequence a
-                       // range starts (its tile 0 lies in the range and its tiles run past it;
-                       // sequence -1 when the range starts none), then the plan (U; P, share,
-                       // paired packed), from which the merge finds the sequence's last range
-  int64_t num_blocks;
-  int64_t batch;
-  int32_t num_kv_heads;
-  int32_t num_q_heads;
-  int32_t group;
-  int32_t width;       // block-table width in blocks
-  int32_t max_ranges;  // P upper bound (= grid.x of decode_kernel)
-  int32_t min_tiles;   // P <= ceil(U / min_tiles)
-  int32_t seq_cost;    // stream units charged for starting a sequence (see make_plan)
-  int32_t quantize_q;  // quantise q per (sequence, head) to int8 first (the reference's option)
-  int32_t tile_tokens;  // 16 * tile_blocks<CACHE>()
-  int32_t block_shift;  // log2(cache block size); the block size is a power of two >= 16
-  int32_t bt_is64;
-  int32_t sl_is64;
-  float sm_scale_log2e;
-  int32_t first_share;  // of a range pair's units, the first range's share in 1/256
-  int32_t pair_min;     // ranges are paired when P >= pair_min (every CU gets a whole pair)
-  int32_t halves;       // ranges per workgroup (1, or 2 with the paired layout)
-  int32_t depth;        // tiles of K/V loads in flight per wave (2, or 4: INT8, one range per WG)
-  int32_t group_mode;   // one workgroup per (sequence, kv head), states merged in LDS
-  int32_t head_dim;     // 64, 128 or 256
-  int32_t scan32;       // a 64-sequence chunk's units fit 32 bits (see units_scan)
-  int32_t cut_desc;     // write ws_cut (merge_by_range_kernel follows)
-  int32_t kv_pair;      // head_dim 64: each wave takes kv heads 2k and 2k + 1 as one 128-wide head
-  int32_t split;        // per-sequence layout over `split` workgroups per (sequence, kv head), whose
-                        // records merge_split_kernel combines (0: one workgroup, no records)
-};
-
-// ------------------------------------------------------------------------ wave utilities
-__device__ __forceinline__ int64_t wave_sum(int64_t x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
-
-__device__ __forceinline__ int64_t wave_inclusive_scan(int64_t x, int lane) {
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int64_t y = __shfl_up(x, (unsigned)o);
-    if (lane >= o) x += y;
-  }
-  return x;
-}
-
-// Inclusive prefix sum of a 32-bit value over the wave (all 64 lanes active): DPP row shifts
-// by 1, 2, 4, 8 inside each 16-lane row, then the totals of the rows below (lanes 15, 31, 47,
-// read before they change) added to each row.  A few dozen VALU cycles, against six
-// dependent LDS permutes per 32-bit word for a __shfl_up / __shfl_xor ladder.
-__device__ __forceinline__ int32_t wave_scan32(int32_t x, int lane) {
-  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
-  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
-  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
-  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
-  const int32_t r0 = __builtin_amdgcn_readlane(x, 15);
-  const int32_t r1 = __builtin_amdgcn_readlane(x, 31);
-  const int32_t r2 = __builtin_amdgcn_readlane(x, 47);
-  const int row = lane >> 4;
-  return x + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
-}
-
-__device__ __forceinline__ int64_t readlane64(int64_t x, int lane) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, lane);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)x >> 32), lane);
-  return (int64_t)(((uint64_t)hi << 32) | lo);
-}
-
-// ------------------------------------------------------------------------ work plan
-// Sequence b's token count L_b = clamp(seq_lens[b], 0, width * 16) and tile count
-// n_b = ceil(L_b / tile_tokens).  The batch becomes a stream of units: a non-empty sequence
-// contributes seq_cost "start" units (the latency of its first block ids and tiles, which a
-// range pays again for every sequence it starts) followed by its n_b tiles.  With U units in
-// all, P = clamp(ceil(U / min_tiles), 1, max_ranges) and the uniform bounds are b_r = r U / P,
-// so every range costs the same whatever the lengths.  When P >= pair_min (enough ranges for a
-// pair on every CU), ranges come in pairs (2k, 2k + 1), the two halves of one workgroup, and
-// the bound between them moves from b_{2k+1} to first_share / 256 of the pair's units (an
-// unpaired last range keeps its bounds): the first half, which streams faster on a shared
-// SIMD, gets the larger share.
-__device__ __forceinline__ int64_t seq_len_of(const DecodeArgs& a, int64_t b) {
-  if (b >= a.batch) return 0;
-  int64_t L = load_index(a.sl, b, a.sl_is64);
-  const int64_t cap = (int64_t)a.width << a.block_shift;
-  return L < 0 ? 0 : (L > cap ? cap : L);
-}
-
-// Lengths (as seq_len_of) of sequences (c0 + k) 64 + lane, k < K, with all K loads issued before
-// any is used (the index clamped into the batch, 0 past it): seq_len_of's bounds test around
-// each load made every chunk wait for the previous one.
-template <int K>
-__device__ __forceinline__ void seq_len_chunks(const DecodeArgs& a, int64_t c0, int lane,
-                                               int64_t (&L)[K]) {
-  const int64_t last = a.batch - 1;
-  if (a.sl_is64) {
-    const int64_t* t = reinterpret_cast<const int64_t*>(a.sl);
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int64_t i = (c0 + k) * kWave + lane;
-      L[k] = t[i < last ? i : last];
-    }
-  } else {
-    const int32_t* t = reinterpret_cast<const int32_t*>(a.sl);
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int64_t i = (c0 + k) * kWave + lane;
-      L[k] = t[i < last ? i : last];
-    }
-  }
-  const int64_t cap = (int64_t)a.width << a.block_shift;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    const int64_t x = L[k] < 0 ? 0 : (L[k] > cap ? cap : L[k]);
-    L[k] = (c0 + k) * kWave + lane <= last ? x : 0;
-  }
-}
-
-__device__ __forceinline__ int64_t tiles_of(const DecodeArgs& a, int64_t L) {
-  static_assert(tile_blocks<kI8>() == 2 && tile_blocks<kBF16>() == 2, "32-token tiles");
-  return (L + 2 * kRows - 1) / (2 * kRows);
-}
-
-__device__ __forceinline__ int64_t units_of(const DecodeArgs& a, int64_t n) {
-  return n > 0 ? n + a.seq_cost : 0;
-}
-
-// Inclusive scan / total of the lanes' unit counts over one 64-sequence chunk.  32-bit DPP
-// scan when the host has bounded a chunk's units below 2^31 (scan32: no sequence can exceed
-// 2^25 tiles), else the 64-bit permute ladder.
-__device__ __forceinline__ int64_t units_scan(const DecodeArgs& a, int64_t u, int lane) {
-  if (a.scan32) return (int64_t)wave_scan32((int32_t)u, lane);
-  return wave_inclusive_scan(u, lane);
-}
-
-__device__ __forceinline__ int64_t units_sum(const DecodeArgs& a, int64_t u, int lane) {
-  if (a.scan32) return (int64_t)__builtin_amdgcn_readlane(wave_scan32((int32_t)u, lane), kWave - 1);
-  return wave_sum(u);
-}
-
-// a / b for a >= 0, b > 0, with a 32-bit divide when both fit (the plan's bounds always do in
-// practice; the 64-bit divide is a long instruction sequence on the GPU).
-__device__ __forceinline__ int64_t udiv(int64_t a, int64_t b) {
-  if ((((uint64_t)a | (uint64_t)b) >> 32) == 0) return (int64_t)((uint32_t)a / (uint32_t)b);
-  return a / b;
-}
-
-// Ranges are paired only when they average at least this many units: short ranges are
-// latency-bound, and shifting a unit or two between them costs more than the balance gains.
-constexpr int kPairMinUnits = 16;
-
-struct Plan {
-  int64_t U;
-  int64_t P;
-  int32_t share;  // first_share
-  bool paired;
-};
-
-// A plan's P, share and paired in one word (P < 2^31, share < 2^8), and back, with U.
-__device__ __forceinline__ int64_t pack_plan(const Plan& p) {
-  return p.P | ((int64_t)p.share << 32) | ((int64_t)p.paired << 40);
-}
-
-__device__ __forceinline__ Plan unpack_plan(int64_t U, int64_t w) {
-  return {U, w & 0x7fffffff, (int32_t)((w >> 32) & 0xff), ((w >> 40) & 1) != 0};
-}
-
-// The plan of a batch of U units.
-__device__ __forceinline__ Plan plan_of_units(const DecodeArgs& a, int64_t U) {
-  int64_t P = udiv(U + a.min_tiles - 1, a.min_tiles);
-  P = P < 1 ? 1 : (P > a.max_ranges ? a.max_ranges : P);
-  return {U, P, a.first_share, P >= a.pair_min && U >= (int64_t)kPairMinUnits * P};
-}
-
-// L0: this lane's seq_len_of(a, lane), the first 64 sequences' lengths, which the caller keeps
-// in a register for its own walk over the batch (most batches have at most 64 sequences).
-__device__ __forceinline__ Plan make_plan(const DecodeArgs& a, int lane, int64_t L0) {
-  int64_t U = units_sum(a, units_of(a, tiles_of(a, L0)), lane);
-  for (int64_t base = kWave; base < a.batch; base += kWave)
-    U += units_sum(a, units_of(a, tiles_of(a, seq_len_of(a, base + lane))), lane);
-  return plan_of_units(a, U);
-}
-
-// Bound between the ranges of pair k (2k + 1 < P): first_share of the pair's units, at least
-// one unit on each side (P <= U keeps every uniform range non-empty).
-__device__ __forceinline__ int64_t pair_split(const Plan& p, int64_t k) {
-  const int64_t ps = udiv(2 * k * p.U, p.P);
-  const int64_t pe = udiv((2 * k + 2) * p.U, p.P);
-  int64_t h = ((pe - ps) * p.share) >> 8;
-  h = h < 1 ? 1 : (h > pe - ps - 1 ? pe - ps - 1 : h);
-  return ps + h;
-}
-
-__device__ __forceinline__ int64_t range_start(const Plan& p, int64_t r) {
-  if (p.paired && (r & 1) && r < p.P) return pair_split(p, r >> 1);
-  return udiv(r * p.U, p.P);
-}
-
-// The range holding stream unit x (0 <= x < U): the largest r with range_start(r) <= x.
-__device__ __forceinline__ int64_t range_of(const Plan& p, int64_t x) {
-  const int64_t r0 = udiv((x + 1) * p.P - 1, p.U);  // uniform range
-  const int64_t k = r0 >> 1;
-  if (!p.paired || 2 * k + 1 >= p.P) return r0;  // uniform, or the unpaired last range
-  return 2 * k + (x >= pair_split(p, k) ? 1 : 0);
-}
-
-// Partial-record slot of a sequence cut by a range: 0 if it started in an earlier range, 1 if
-// it starts in this range and continues after it.  A range cuts at most one sequence of each
-// kind (its first and its last), so the two slots never collide.
-__device__ __forceinline__ int64_t cut_slot(int64_t first_tile) { return first_tile > 0 ? 0 : 1; }
-
-// ------------------------------------------------------------------------ tile registers
-// Registers holding the K or the V half of one tile (NB 16-token row groups) for one lane, for
-// head_dim HD (64, 128 or 256).
-//   K: lane (i = lane % 16, g = lane / 16) holds token i of row group s, head_dim elements
-//      [HD/4 g, HD/4 (g + 1)): HD/4 elements, HD E / 64 16-byte pieces.
-//   V: lane (i, g) holds tokens 4g + r (r = 0..3) of row group s, head_dim elements
-//      [HD/16 i, HD/16 (i + 1)): HD E / 64 dwords per token row.
-template <int CACHE, int HD>
-constexpr int k_pieces() {
-  return HD * (CACHE == kI8 ? 1 : 2) / 64;
-}
-template <int CACHE, int HD>
-constexpr int v_dwords() {
-  return HD * (CACHE == kI8 ? 1 : 2) / 64;
-}
-template <int CACHE, int NB, int HD>
-struct KTile {
-  u32x4 k[NB][k_pieces<CACHE, HD>()];
-};
-template <int CACHE, int NB, int HD>
-struct VTile {
-  uint32_t v[NB][4][v_dwords<CACHE, HD>()];
-};
-
-template <int CACHE>
-struct MfmaOp;
-template <>
-struct MfmaOp<kI8> {
-  typedef f16x8 T;
-  typedef _Float16 E;
-};
-template <>
-struct MfmaOp<kF16> {
-  typedef f16x8 T;
-  typedef _Float16 E;
-};
-template <>
-struct MfmaOp<kBF16> {
-  typedef bf16x8 T;
-  typedef __bf16 E;
-};
-
-__device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-
-// Exact int8 x int8 -> int32 product of a 16x64 and a 64x16 tile (lane (i, g): row/column i,
-// 16 k-slots of group g).
-__device__ __forceinline__ i32x4 mfma_i8(u32x4 a, i32x4 b, i32x4 c) {
-  return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// Byte permute: result byte k = byte sel_k of the 8-byte value {hi, lo} (0-3 from lo).
-__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
-  return __builtin_amdgcn_perm(hi, lo, sel);
-}
-
-constexpr uint32_t kMagic = 0x64646464u;     // fp16 exponent byte of 1024.0
-constexpr uint32_t kSignFlip = 0x80808080u;  // int8 -> offset binary (x + 128)
-constexpr uint32_t kSelLo = 0x04010400u;     // [b0, 0x64, b1, 0x64]
-constexpr uint32_t kSelHi = 0x04030402u;     // [b2, 0x64, b3, 0x64]
-
-// Four offset-binary bytes of d0 and four of d1 -> 8 exact fp16 values of the signed bytes.
-__device__ __forceinline__ f16x8 i8x8_to_f16(uint32_t d0, uint32_t d1) {
-  u32x4 w;
-  w[0] = perm(kMagic, d0, kSelLo);
-  w[1] = perm(kMagic, d0, kSelHi);
-  w[2] = perm(kMagic, d1, kSelLo);
-  w[3] = perm(kMagic, d1, kSelHi);
-  return __builtin_bit_cast(f16x8, w) - (f16x8)(_Float16)1152.0f;
-}
-
-template <int DT>
-constexpr int esize() {
-  return DT == kF32 ? 4 : (DT == kI8 ? 1 : 2);
-}
-
-// Stores 8 consecutive fp32 values as DT (16-byte aligned destination).
-template <int DT>
-__device__ __forceinline__ void store8(char* p, const float (&x)[8]) {
-  if constexpr (DT == kF32) {
-    f32x4* q = reinterpret_cast<f32x4*>(p);
-    q[0] = f32x4{x[0], x[1], x[2], x[3]};
-    q[1] = f32x4{x[4], x[5], x[6], x[7]};
-  } else if constexpr (DT == kF16) {
-    f16x8 h;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = (_Float16)x[i];
-    *reinterpret_cast<f16x8*>(p) = h;
-  } else {
-    bf16x8 h;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = (__bf16)x[i];
-    *reinterpret_cast<bf16x8*>(p) = h;
-  }
-}
-
-// Stores N (4, 8 or 16) consecutive fp32 values as DT (aligned to min(N, 8) elements).
-template <int DT, int N>
-__device__ __forceinline__ void store_n(char* p, const float (&x)[N]) {
-  static_assert(N == 4 || N == 8 || N == 16, "4, 8 or 16 elements");
-  if constexpr (N == 16) {
-    const float lo[8] = {x[0], x[1], x[2], x[3], x[4], x[5], x[6], x[7]};
-    const float hi[8] = {x[8], x[9], x[10], x[11], x[12], x[13], x[14], x[15]};
-    store8<DT>(p, lo);
-    store8<DT>(p + 8 * esize<DT>(), hi);
-  } else if constexpr (N == 8) {
-    store8<DT>(p, x);
-  } else if constexpr (DT == kF32) {
-    *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
-  } else if constexpr (DT == kF16) {
-    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-    *reinterpret_cast<f16x4*>(p) = f16x4{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
-  } else {
-    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-    *reinterpret_cast<bf16x4*>(p) = bf16x4{(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]};
-  }
-}
-
-// Cache-stream load.  NT (chosen per call by the host, INT8 caches only): the non-temporal hint,
-// +10 % delivered bandwidth on MI355X when the call streams more K/V than the Infinity Cache
-// holds; a small pool that the cache keeps between calls is read faster without it.  16-bit
-// caches always use plain loads: their wider per-lane rows (64 B of K per lane) measured ~12 %
-// slower with the hint.
-template <int CACHE, bool NT, typename T>
-__device__ __forceinline__ T stream_load(const T* p) {
-  if constexpr (CACHE == kI8 && NT)
-    return __builtin_nontemporal_load(p);
-  else
-    return *p;
-}
-
-// Where each 16-token row group of a tile starts: its cache block and its first row in the block.
-template <int NB>
-struct TileRows {
-  int32_t id[NB];
-  int32_t row[NB];
-};
-
-// The lane's HD/4 K elements of its token: one contiguous run [HD/4 lg, HD/4 (lg + 1)) up to
-// head_dim 128; at 256 two runs of HD/8, [HD/8 lg, ...) and [HD/2 + HD/8 lg, ...), so that an
-// INT8 lane reads 32 contiguous bytes per run as at 128 (the order the lane's elements are held
-// in, run 0 then run 1, is the order issue_query loads the query in, so the products pair the
-// same elements).
-template <int HD>
-__device__ __forceinline__ constexpr int k_run(int run, int lg) {
-  return HD > 128 ? run * (HD / 2) + lg * (HD / 8) : lg * (HD / 4);
-}
-
-template <int CACHE, int NB, bool NT, int HD>
-__device__ __forceinline__ void issue_k(KTile<CACHE, NB, HD>& r, const char* kb,
-                                        const TileRows<NB>& ph, const DecodeArgs& a, int li,
-                                        int lg) {
-  constexpr int E = esize<CACHE>();
-  constexpr int kRuns = HD > 128 ? 2 : 1;
-  constexpr int PR = k_pieces<CACHE, HD>() / kRuns;  // 16-byte pieces per run
-#pragma unroll
-  for (int s = 0; s < NB; ++s) {
-    const char* row = kb + ph.id[s] * a.kc_sb + (ph.row[s] + li) * a.kc_ss;
-#pragma unroll
-    for (int run = 0; run < kRuns; ++run) {
-      const u32x4* k4 = reinterpret_cast<const u32x4*>(row + k_run<HD>(run, lg) * E);
-#pragma unroll
-      for (int i = 0; i < PR; ++i) r.k[s][run * PR + i] = stream_load<CACHE, NT>(&k4[i]);
-    }
-  }
-}
-
-template <int CACHE, int NB, bool NT, int HD>
-__device__ __forceinline__ void issue_v(VTile<CACHE, NB, HD>& r, const char* vb,
-                                        const TileRows<NB>& ph, const DecodeArgs& a, int li,
-                                        int lg) {
-  constexpr int E = esize<CACHE>();
-  constexpr int DW = v_dwords<CACHE, HD>();
-#pragma unroll
-  for (int s = 0; s < NB; ++s) {
-    const char* vp = vb + ph.id[s] * a.vc_sb + (ph.row[s] + 4 * lg) * a.vc_ss + li * (HD / 16 * E);
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const char* rp = vp + rr * a.vc_ss;
-      if constexpr (DW == 1) {
-        r.v[s][rr][0] = stream_load<CACHE, NT>(reinterpret_cast<const uint32_t*>(rp));
-      } else if constexpr (DW == 2) {
-        const u32x2 x = stream_load<CACHE, NT>(reinterpret_cast<const u32x2*>(rp));
-        r.v[s][rr][0] = x[0];
-        r.v[s][rr][1] = x[1];
-      } else {
-        static_assert(DW % 4 == 0, "whole 16-byte pieces");
-#pragma unroll
-        for (int h = 0; h < DW / 4; ++h) {
-          const u32x4 x = stream_load<CACHE, NT>(reinterpret_cast<const u32x4*>(rp) + h);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) r.v[s][rr][4 * h + k] = x[k];
-        }
-      }
-    }
-  }
-}
-
-// Scores of one tile (NB row groups) and the online-softmax update: rescales acc/l_part when
-// the running max moves and returns the P^T operands (one per MFMA k-step of 32 tokens) as a
-// hi + lo pair of 16-bit values (p = hi + lo to about 2^-22 relative), so that P*V on the
-// 16-bit matrix cores keeps fp32 accuracy: the rounding of p would otherwise dominate the error
-// (2^-12 relative for fp16, 2^-9 for bf16).
-//   valid: number of tokens of this tile inside the sequence (1..16 NB).
-//   QSPLIT (an fp32 query): q is held as 16-bit hi + lo operands and each k-step takes two MFMAs,
-//   so the scores keep ~2^-22 (fp16) / 2^-16 (bf16) relative accuracy instead of one rounding of q.
-//   QQ (INT8 cache with a quantised query): the scores are the exact integer products of the
-//   int8 K rows and q8 on the int8 matrix cores (2 k-steps of 64, no K conversion); otherwise
-//   K is converted to 16-bit operands (4 k-steps of 32).
-template <int CACHE, int NB, bool QQ, int HD, bool QSPLIT>
-__device__ __forceinline__ void tile_scores(const KTile<CACHE, NB, HD>& r,
-                                            const typename MfmaOp<CACHE>::T (&qop)[HD / 32],
-                                            const typename MfmaOp<CACHE>::T (&qlo)[HD / 32],
-                                            const i32x4 (&q8op)[HD / 64], f32x4 (&acc)[HD / 16],
-                                            float& m_run, float& l_part, int valid, int lg,
-                                            float s_scale,
-                                            typename MfmaOp<CACHE>::T (&pop)[NB / 2][2]) {
-  typedef typename MfmaOp<CACHE>::T OpT;
-  constexpr int kTileTokens = NB * kRows;
-  // ---- scores S^T[token][head] for each row group of the tile ----
-  f32x4 S[NB];
-#pragma unroll
-  for (int s = 0; s < NB; ++s) {
-    if constexpr (QQ) {
-      i32x4 si = (i32x4)(0);
-#pragma unroll
-      for (int ks = 0; ks < HD / 64; ++ks) si = mfma_i8(r.k[s][ks], q8op[ks], si);
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) S[s][rr] = (float)si[rr];
-      continue;
-    }
-    S[s] = (f32x4)(0.0f);
-#pragma unroll
-    for (int ks = 0; ks < HD / 32; ++ks) {
-      OpT kop;
-      if constexpr (CACHE == kI8) {
-        const uint32_t d0 = r.k[s][ks >> 1][(ks & 1) * 2] ^ kSignFlip;
-        const uint32_t d1 = r.k[s][ks >> 1][(ks & 1) * 2 + 1] ^ kSignFlip;
-        kop = i8x8_to_f16(d0, d1);
-      } else {
-        kop = __builtin_bit_cast(OpT, r.k[s][ks]);
-      }
-      S[s] = mfma(kop, qop[ks], S[s]);
-      if constexpr (QSPLIT) S[s] = mfma(kop, qlo[ks], S[s]);
-    }
-  }
-
-  // ---- online softmax (exp2 domain); lane column = head, rows = tokens 16s + 4lg + r ----
-  float sv[4 * NB];
-#pragma unroll
-  for (int s = 0; s < NB; ++s)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) sv[4 * s + rr] = S[s][rr] * s_scale;
-  if (valid < kTileTokens) {
-#pragma unroll
-    for (int s = 0; s < NB; ++s)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        if (16 * s + 4 * lg + rr >= valid) sv[4 * s + rr] = -INFINITY;
-  }
-  float mx = sv[0];
-#pragma unroll
-  for (int e = 1; e < 4 * NB; ++e) mx = fmaxf(mx, sv[e]);
-  mx = fmaxf(mx, __shfl_xor(mx, 16));
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
-  const bool need = mx > m_run + kLazyRescale;
-  if (__any(need)) {
-    const float m_new = need ? mx : m_run;
-    const float alpha = exp2_fast(m_run - m_new);
-    m_run = m_new;
-    l_part *= alpha;
-#pragma unroll
-    for (int dt = 0; dt < HD / 16; ++dt) acc[dt] *= alpha;
-  }
-  typedef typename MfmaOp<CACHE>::E E;
-#pragma unroll
-  for (int e = 0; e < 4 * NB; ++e) {
-    const float pe = exp2_fast(sv[e] - m_run);
-    l_part += pe;
-    const E hi = (E)pe;
-    pop[e / 8][0][e % 8] = hi;
-    pop[e / 8][1][e % 8] = (E)(pe - (float)hi);
-  }
-}
-
-// out^T[dim][head] += V^T[dim][token] * P^T[token][head] for one tile.
-// MFMA row i of dim tile dt is head_dim element (HD/16) i + dt; k-slot e of lane group g in
-// k-step kst is token (row group 2 kst + e / 4, row 4g + e % 4), matching the P^T operands.
-template <int CACHE, int NB, int HD>
-__device__ __forceinline__ void tile_pv(VTile<CACHE, NB, HD>& r,
-                                        const typename MfmaOp<CACHE>::T (&pop)[NB / 2][2],
-                                        f32x4 (&acc)[HD / 16], int valid, int lg) {
-  typedef typename MfmaOp<CACHE>::T OpT;
-  constexpr int DW = v_dwords<CACHE, HD>();
-  if constexpr (CACHE != kI8) {
-    // 16-bit rows past the sequence end may hold non-finite garbage; 0 * NaN would leak.
-    if (valid < NB * kRows) {
-#pragma unroll
-      for (int s = 0; s < NB; ++s)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          if (16 * s + 4 * lg + rr >= valid) {
-#pragma unroll
-            for (int k = 0; k < DW; ++k) r.v[s][rr][k] = 0u;
-          }
-    }
-  }
-#pragma unroll
-  for (int kst = 0; kst < NB / 2; ++kst) {
-    const int s0 = 2 * kst;
-    if constexpr (CACHE == kI8) {
-      uint32_t pk[2][2][DW][2];  // [row group][token pair][row dword][byte pair 01/23]
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int rp = 0; rp < 2; ++rp)
-#pragma unroll
-          for (int hsel = 0; hsel < DW; ++hsel) {
-            const uint32_t a0 = r.v[s0 + s][2 * rp][hsel] ^ kSignFlip;
-            const uint32_t b0 = r.v[s0 + s][2 * rp + 1][hsel] ^ kSignFlip;
-            pk[s][rp][hsel][0] = perm(a0, b0, 0x01050004u);  // [a.b0, b.b0, a.b1, b.b1]
-            pk[s][rp][hsel][1] = perm(a0, b0, 0x03070206u);  // [a.b2, b.b2, a.b3, b.b3]
-          }
-#pragma unroll
-      for (int dt = 0; dt < HD / 16; ++dt) {
-        const int hsel = dt >> 2, bp = (dt >> 1) & 1;
-        const uint32_t sel = (dt & 1) ? kSelHi : kSelLo;
-        u32x4 w;
-        w[0] = perm(kMagic, pk[0][0][hsel][bp], sel);
-        w[1] = perm(kMagic, pk[0][1][hsel][bp], sel);
-        w[2] = perm(kMagic, pk[1][0][hsel][bp], sel);
-        w[3] = perm(kMagic, pk[1][1][hsel][bp], sel);
-        const f16x8 vop = __builtin_bit_cast(f16x8, w) - (f16x8)(_Float16)1152.0f;
-        acc[dt] = mfma(vop, pop[kst][0], acc[dt]);
-        acc[dt] = mfma(vop, pop[kst][1], acc[dt]);
-      }
-    } else {
-#pragma unroll
-      for (int dt = 0; dt < HD / 16; ++dt) {
-        const int wd = dt >> 1;
-        const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
-        u32x4 w;
-        w[0] = perm(r.v[s0][1][wd], r.v[s0][0][wd], sel);
-        w[1] = perm(r.v[s0][3][wd], r.v[s0][2][wd], sel);
-        w[2] = perm(r.v[s0 + 1][1][wd], r.v[s0 + 1][0][wd], sel);
-        w[3] = perm(r.v[s0 + 1][3][wd], r.v[s0 + 1][2][wd], sel);
-        const OpT vop = __builtin_bit_cast(OpT, w);
-        acc[dt] = mfma(vop, pop[kst][0], acc[dt]);
-        acc[dt] = mfma(vop, pop[kst][1], acc[dt]);
-      }
-    }
-  }
-}
-
-// Raw query row piece of one lane: head li, its HD/4 elements (the runs of k_run) as loaded.
-template <int QT, int HD>
-struct QueryRaw {
-  u32x4 w[HD / 32];  // HD/4 16-bit elements
-};
-template <int HD>
-struct QueryRaw<kF32, HD> {
-  f32x4 w[HD / 16];  // HD/4 fp32 elements
-};
-
-// Issues the query loads (no wait): lane (head li, group lg) fetches the HD/4 elements of
-// q[b, kvh * G + li] whose K elements it holds (the runs of k_run, in the same order); lanes of
-// padding heads (li >= G) hold zeros.
-//   PAIR (head_dim 64 as kv heads kvh, kvh + 1 side by side, HD = 128): column li < 2G is query
-//   head kvh G + li; its 64 elements go to the lanes of its own kv head's half (lg / 2 = 0 for
-//   li < G, 1 above) and the other half's lanes hold zeros, so each column's scores use only its
-//   own kv head's K elements.
-template <int QT, int HD, bool PAIR = false>
-__device__ __forceinline__ void issue_query(const DecodeArgs& a, int64_t b, int kvh, int li,
-                                            int lg, QueryRaw<QT, HD>& raw) {
-  constexpr int QE = esize<QT>();
-  typedef typename std::remove_reference<decltype(raw.w[0])>::type Vec;
-  constexpr int N = sizeof(raw.w) / sizeof(raw.w[0]);
-  constexpr int kRuns = HD > 128 ? 2 : 1;
-  if constexpr (PAIR) {
-    static_assert(HD == 128, "pairs of 64-wide kv heads");
-    if (li < 2 * a.group && (lg >> 1) == (li >= a.group ? 1 : 0)) {
-      const Vec* qp = reinterpret_cast<const Vec*>(
-          a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh + 32 * (lg & 1)) * QE);
-#pragma unroll
-      for (int i = 0; i < N; ++i) raw.w[i] = qp[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < N; ++i) raw.w[i] = (Vec)(0);
-    }
-    return;
-  }
-  // Up to head_dim 128 the lane's elements are one run and its address is one expression: built
-  // from a row pointer plus k_run's offset instead, hipcc's allocation of the depth-2 INT8
-  // kernel put a wait for the older loads before each V load of the tile loop (137 instead of
-  // 100 s_waitcnt), which cost 0.3-0.45 us per call at B = 1 x 32768 and B = 8 x 4096.
-  if (kRuns == 1 && li < a.group) {
-    const Vec* qp = reinterpret_cast<const Vec*>(
-        a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh + HD / 4 * lg) * QE);
-#pragma unroll
-    for (int i = 0; i < N; ++i) raw.w[i] = qp[i];
-  } else if (li < a.group) {
-    const char* qrow = a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh) * QE;
-#pragma unroll
-    for (int run = 0; run < kRuns; ++run) {
-      const Vec* qp = reinterpret_cast<const Vec*>(qrow + k_run<HD>(run, lg) * QE);
-#pragma unroll
-      for (int i = 0; i < N / kRuns; ++i) raw.w[run * (N / kRuns) + i] = qp[i];
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < N; ++i) raw.w[i] = (Vec)(0);
-  }
-}
-
-__device__ __forceinline__ float round_half_away(float x) {
-  return x >= 0.0f ? floorf(x + 0.5f) : -floorf(-x + 0.5f);
-}
-
-// Builds the Q^T operand (lane (li, lg) holds element 8 ks + e of its HD/4 query elements, in
-// k_run order: q[li][HD/4 lg + 8 ks + e] up to head_dim 128) from the raw loads and
-// returns the lane's fp32 factor turning MFMA scores into log2-domain logits.
-//   * default: q is scaled by 2^e so the largest |q| of the wave lands in [2^14, 2^15) for fp16
-//     operands (exact for bf16 input, never overflows); bf16 operands take q as is;
-//   * quantize_q: per (sequence, head) q_scale = max(absmax / 127, 1e-6) and
-//     q8 = clamp(round_half_away(q / q_scale), -127, 127) (src/triton_ops/int8_paged_attention.py:
-//     137-146, :798-802); the operand is q8 and q_scale joins the score factor.  With QQ the
-//     q8 values are packed as int8 operands instead (q8op[ks] byte e of lane (li, lg) =
-//     lane element 16 ks + e of q8, matching the int8 K bytes the lane holds).
-//   HEADWISE: the 2^e scale per query head (the 4 lanes holding a head's elements, whose score
-//   column is the same lane's), two lane exchanges instead of six; the per-sequence kernels use
-//   it (their short calls wait on every exchange: ~0.15 us of a 6.5 us kernel on MI355X).
-template <int CACHE, int QT, bool QQ, int HD, bool PAIR = false, bool HEADWISE = false>
-__device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRaw<QT, HD>& raw,
-                                              int kvh, typename MfmaOp<CACHE>::T (&qop)[HD / 32],
-                                              typename MfmaOp<CACHE>::T (&qlo)[HD / 32],
-                                              i32x4 (&q8op)[HD / 64]) {
-  constexpr int KS = HD / 32;  // 16-bit k-steps
-  float x[KS][8];
-  if constexpr (QT == kF32) {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[ks][e] = raw.w[2 * ks + e / 4][e % 4];
-  } else {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) unpack2<QT>(raw.w[ks][e], x[ks][2 * e], x[ks][2 * e + 1]);
-  }
-  float amax = 0.0f;
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[ks][e]));
-  float s_scale = a.sm_scale_log2e;
-  if constexpr (CACHE == kI8) {
-    // PAIR: the lane's column belongs to kv head kvh + 1 from column G on.
-    const int kv = PAIR ? kvh + ((int)(__lane_id() & 15) >= a.group ? 1 : 0) : kvh;
-    s_scale *= fmaxf(a.k_scale[kv], 1e-6f);
-  }
-  if (a.quantize_q) {
-    // absmax over the head's HD elements: the 4 lanes (li, lg = 0..3) of this head column
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
-    const float qs = fmaxf(amax / 127.0f, 1e-6f);
-    if constexpr (QQ) {
-#pragma unroll
-      for (int ks = 0; ks < HD / 64; ++ks)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          uint32_t word = 0;
-#pragma unroll
-          for (int bb = 0; bb < 4; ++bb) {
-            const int d = 16 * ks + 4 * w + bb;  // element of the lane's HD / 4
-            const float v = fminf(fmaxf(round_half_away(x[d / 8][d % 8] / qs), -127.0f), 127.0f);
-            word |= ((uint32_t)(int32_t)v & 0xffu) << (8 * bb);
-          }
-          q8op[ks][w] = (int32_t)word;
-        }
-      return s_scale * qs;
-    }
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        qop[ks][e] = (typename MfmaOp<CACHE>::E)fminf(fmaxf(round_half_away(x[ks][e] / qs), -127.0f),
-                                                      127.0f);
-    return s_scale * qs;
-  }
-  float qmul = 1.0f;
-  if constexpr (CACHE != kBF16) {
-    if constexpr (!HEADWISE) {
-      amax = fmaxf(amax, __shfl_xor(amax, 1));
-      amax = fmaxf(amax, __shfl_xor(amax, 2));
-      amax = fmaxf(amax, __shfl_xor(amax, 4));
-      amax = fmaxf(amax, __shfl_xor(amax, 8));
-    }
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
-    if (amax > 0.0f && amax < INFINITY) {
-      const int e = 14 - ilogbf(amax);
-      qmul = ldexpf(1.0f, e);
-      s_scale = ldexpf(s_scale, -e);
-    }
-  }
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float v = x[ks][e] * qmul;  // exact: a power of two
-      qop[ks][e] = (typename MfmaOp<CACHE>::E)v;
-      if constexpr (QT == kF32) qlo[ks][e] = (typename MfmaOp<CACHE>::E)(v - (float)qop[ks][e]);
-    }
-  return s_scale;
-}
-
-// Stages the physical block ids of tiles [c0, c1) of sequence b (nblk blocks) in this wave's
-// LDS slots, one per 16-token row group: ids[NB * (t - c0) + s] = the block holding row group s
-// of tile t (tokens 16 (NB t + s) .. + 15; consecutive row groups share a block when the block
-// size exceeds 16), 0 past the sequence's last block and clamped into [0, num_blocks) so every
-// access stays inside the caches.
-template <int NB>
-__device__ __forceinline__ void stage_block_ids(const DecodeArgs& a, int32_t* ids, int64_t b,
-                                                int64_t c0, int64_t c1, int64_t nblk, int lane) {
-  const int n = (int)(NB * (c1 - c0));
-  const int64_t hi = a.num_blocks - 1;
-  const int gshift = a.block_shift - 4;  // row groups per block = 2^gshift
-  for (int j = lane; j < n; j += kWave) {
-    const int64_t blk = (NB * c0 + j) >> gshift;
-    int64_t p = 0;
-    if (blk < nblk) p = load_index(a.bt, b * a.bt_sb + blk * a.bt_sl, a.bt_is64);
-    ids[j] = (int32_t)(p < 0 ? 0 : (p > hi ? hi : p));
-  }
-}
-
-// Output rows of an empty sequence: zeros for the kv head's query heads (one wave).
-template <int QT, int HD>
-__device__ __forceinline__ void write_zero_rows(const DecodeArgs& a, int64_t b, int kvh, int lane) {
-  const int li = lane & 15;
-  const int lg = lane >> 4;
-  if (li >= a.group) return;
-  char* op = a.out + (b * a.o_sb + (int64_t)(kvh * a.group + li) * a.o_sh) * esize<QT>();
-  float z[HD / 16];
-#pragma unroll
-  for (int i = 0; i < HD / 16; ++i) z[i] = 0.0f;
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr)
-    store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), z);
-}
-
-// Processes tiles [ta, tb) of sequence b (length L) for kv head kvh with one wave, then writes
-// either the final output (full == true) or a partial record.  ids: this wave's LDS slots.
-// DEPTH: tiles of K/V loads kept in flight (register buffers).  GROUP: leave the state
-// (running max, sum, accumulators) in this wave's LDS slot (g_acc [HD/4][64], g_m, g_l [16])
-// for the workgroup to merge, instead of an output row or a partial record.
-template <int CACHE, int QT, bool NT, bool QQ, int HD, int DEPTH, bool GROUP = false,
-          bool PAIR = false>
-__device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, int64_t b,
-                                            int64_t L, int kvh, int64_t ta, int64_t tb,
-                                            bool full, int64_t rec, int lane,
-                                            float* g_acc = nullptr, float* g_m = nullptr,
-                                            float* g_l = nullptr) {
-  typedef typename MfmaOp<CACHE>::T OpT;
-  const int li = lane & 15;
-  const int lg = lane >> 4;
-  const int G = a.group;
-
-  f32x4 acc[HD / 16];
-#pragma unroll
-  for (int dt = 0; dt < HD / 16; ++dt) acc[dt] = (f32x4)(0.0f);
-  float m_run = -INFINITY;
-  float l_part = 0.0f;
-
-  const char* kb = a.kc + (int64_t)kvh * a.kc_sh;
-  const char* vb = a.vc + (int64_t)kvh * a.vc_sh;
-  const int64_t nblk = (L + (1 << a.block_shift) - 1) >> a.block_shift;
-  constexpr int NB = tile_blocks<CACHE>();
-  constexpr int kTileTokens = NB * kRows;
-
-  auto valid_of = [&](int64_t t) -> int {
-    const int64_t v = L - t * kTileTokens;
-    return v >= kTileTokens ? kTileTokens : (int)v;
-  };
-
-  // The tiles are processed in chunks of at most kChunkTiles whose block ids are staged in LDS
-  // (read through the LDS counter, so the waits on tile loads below only ever count tile loads).
-  int64_t c0 = ta;
-  int64_t c1 = (tb - c0 > kChunkTiles) ? c0 + kChunkTiles : tb;
-  const int gmask = (1 << (a.block_shift - 4)) - 1;  // row group within its block
-  auto blocks_of = [&](int64_t t, TileRows<NB>& ph) {
-    const int j = NB * (int)(t - c0);
-#pragma unroll
-    for (int s = 0; s < NB; ++s) {
-      ph.id[s] = __builtin_amdgcn_readfirstlane(ids[j + s]);
-      ph.row[s] = (((int)t * NB + s) & gmask) * kRows;
-    }
-  };
-
-  // DEPTH K and DEPTH V register buffers, refilled as soon as they are consumed: K(t + DEPTH)
-  // is requested right after the scores of tile t, V(t + DEPTH) right after its P*V, so up to
-  // DEPTH tiles of loads are in flight while a tile is computed.  The main loop body handles
-  // DEPTH tiles as one straight-line block and every load in it is unconditional, so the
-  // compiler's wait counts are exact and no wait drains the pipeline; only the chunk's last
-  // full block refills conditionally (its waits may be coarser: the pipeline is ending there).
-  KTile<CACHE, NB, HD> kt[DEPTH];
-  VTile<CACHE, NB, HD> vt[DEPTH];
-  TileRows<NB> ph[DEPTH];
-  OpT pop[NB / 2][2];
-  auto chunk_prologue = [&]() {
-    stage_block_ids<NB>(a, ids, b, c0, c1, nblk, lane);
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      blocks_of(c0 + d < c1 ? c0 + d : c1 - 1, ph[d]);
-      issue_k<CACHE, NB, NT, HD>(kt[d], kb, ph[d], a, li, lg);
-      issue_v<CACHE, NB, NT, HD>(vt[d], vb, ph[d], a, li, lg);
-    }
-  };
-
-  // The query, the first chunk's block ids and its first DEPTH tiles are requested back to
-  // back; the query operand is built once they are all in flight (otherwise three memory
-  // latencies would line up at every segment start).
-  // An fp32 query keeps a lo part (QSPLIT); a quantised query is exact in one operand.
-  constexpr bool QSPLIT = QT == kF32 && !QQ;
-  OpT qop[HD / 32];
-  OpT qlo[HD / 32];  // unused (and removed by the compiler) unless QSPLIT
-  i32x4 q8op[HD / 64];
-  float s_scale;
-  {
-    QueryRaw<QT, HD> qraw;
-    issue_query<QT, HD, PAIR>(a, b, kvh, li, lg, qraw);
-    chunk_prologue();
-    s_scale = finish_query<CACHE, QT, QQ, HD, PAIR, GROUP>(a, qraw, kvh, qop, qlo, q8op);
-  }
-
-  // Tile t + d (buffer d): scores, refill K with tile t + d + DEPTH, P*V, refill V.  refill is a
-  // compile-time true inside the main loop; in the chunk's last full block it stops the refills
-  // at the chunk's end, so no request repeats a tile there (with non-temporal loads a repeated
-  // tile is read from HBM again: 1-4 tiles per segment, ~2 % of a large call's bytes).
-  // sched_barrier(0) keeps the compiler's scheduler from sinking the refills past the compute
-  // that follows them (which would shorten the prefetch distance).
-  auto tile_step = [&](int64_t t, int d, bool refill) {
-    const int valid = valid_of(t + d);
-    tile_scores<CACHE, NB, QQ, HD, QSPLIT>(kt[d], qop, qlo, q8op,
-                                           acc, m_run, l_part, valid, lg, s_scale, pop);
-    if (refill) {
-      blocks_of(t + d + DEPTH, ph[d]);
-      issue_k<CACHE, NB, NT, HD>(kt[d], kb, ph[d], a, li, lg);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    tile_pv<CACHE, NB, HD>(vt[d], pop, acc, valid, lg);
-    if (refill) issue_v<CACHE, NB, NT, HD>(vt[d], vb, ph[d], a, li, lg);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  while (true) {
-    int64_t t = c0;
-    // Every refill of these blocks lies inside the chunk.
-    for (; t + 2 * DEPTH - 1 < c1; t += DEPTH) {
-#pragma unroll
-      for (int d = 0; d < DEPTH; ++d) tile_step(t, d, true);
-    }
-    // The chunk's last full block refills only the tiles the chunk still has.
-    if (t + DEPTH - 1 < c1) {
-#pragma unroll
-      for (int d = 0; d < DEPTH; ++d) tile_step(t, d, t + d + DEPTH < c1);
-      t += DEPTH;
-    }
-    // The last c1 - t < DEPTH tiles of the chunk are in buffers 0, 1, ...
-#pragma unroll
-    for (int d = 0; d + 1 < DEPTH; ++d) {
-      if (t + d < c1) {
-        const int valid = valid_of(t + d);
-        tile_scores<CACHE, NB, QQ, HD, QSPLIT>(kt[d], qop, qlo,
-                                               q8op, acc, m_run, l_part, valid, lg, s_scale,
-                                       pop);
-        tile_pv<CACHE, NB, HD>(vt[d], pop, acc, valid, lg);
-      }
-    }
-    if (c1 >= tb) break;
-    c0 = c1;
-    c1 = (tb - c0 > kChunkTiles) ? c0 + kChunkTiles : tb;
-    chunk_prologue();
-  }
-
-  l_part += __shfl_xor(l_part, 16);
-  l_part += __shfl_xor(l_part, 32);
-  if constexpr (PAIR) {
-    // Columns li < 2G; a column's rows are its own kv head's half of the 128 (lg / 2 = 0 for
-    // li < G, 1 above: real head_dim elements 32 (lg % 2) + 8 rr + dt); the other half's rows
-    // mixed this column's probabilities with the other kv head's V and are dropped.
-    static_assert(!GROUP && HD == 128, "pairs of 64-wide kv heads, range layout only");
-    const int upper = li >= G ? 1 : 0;
-    if (li >= 2 * G) return;
-    const int h = kvh * G + li;
-    const int64_t row = rec * a.num_q_heads + h;
-    if (!full && lg == 2 * upper) {
-      a.ws_m[row] = m_run;
-      a.ws_l[row] = l_part;
-    }
-    if ((lg >> 1) != upper) return;
-    const int d0 = 32 * (lg & 1);
-    if (full) {
-      const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh + upper], 1e-6f) : 1.0f;
-      const float inv = l_part > 0.0f ? vscale / l_part : 0.0f;
-      char* op = a.out + (b * a.o_sb + (int64_t)h * a.o_sh) * esize<QT>();
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        float o[8];
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[dt] = acc[dt][rr] * inv;
-        store_n<QT, 8>(op + (d0 + 8 * rr) * esize<QT>(), o);
-      }
-    } else {
-      char* pp = reinterpret_cast<char*>(a.ws_acc + row * 64);
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        float o[8];
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[dt] = acc[dt][rr];
-        store_n<kF32, 8>(pp + (d0 + 8 * rr) * 4, o);
-      }
-    }
-    return;
-  }
-  if (li >= G) return;
-  if constexpr (GROUP) {
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr)
-#pragma unroll
-      for (int dt = 0; dt < HD / 16; ++dt) g_acc[(rr * (HD / 16) + dt) * kWave + lane] = acc[dt][rr];
-    if (lg == 0) {
-      g_m[li] = m_run;
-      g_l[li] = l_part;
-    }
-    return;
-  }
-  const int h = kvh * G + li;
-  if (full) {
-    const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
-    const float inv = l_part > 0.0f ? vscale / l_part : 0.0f;
-    char* op = a.out + (b * a.o_sb + (int64_t)h * a.o_sh) * esize<QT>();
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      float o[HD / 16];
-#pragma unroll
-      for (int dt = 0; dt < HD / 16; ++dt) o[dt] = acc[dt][rr] * inv;
-      store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), o);
-    }
-  } else {
-    const int64_t row = rec * a.num_q_heads + h;
-    char* pp = reinterpret_cast<char*>(a.ws_acc + row * HD);
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      float o[HD / 16];
-#pragma unroll
-      for (int dt = 0; dt < HD / 16; ++dt) o[dt] = acc[dt][rr];
-      store_n<kF32, HD / 16>(pp + (HD / 4 * lg + HD / 16 * rr) * 4, o);
-    }
-    if (lg == 0) {
-      a.ws_m[row] = m_run;
-      a.ws_l[row] = l_part;
-    }
-  }
-}
-
-// grid (ceil(max_ranges / HALVES), num_kv_heads / W), block HALVES * W waves; wave w of
-// workgroup (x, y) handles kv head y * W + w % W over stream range x (HALVES = 1), or, with two
-// ranges per workgroup, 2x + w / W (paired ranges) or x + (w / W) grid.x.  DEPTH: tiles in flight
-// per wave (4 only in the one-wave-per-SIMD layout, whose register budget allows it).
-// Register budget: one wave per SIMD (512 registers) for INT8 waves with four tiles in flight,
-// for head_dim 256 (twice the tile and accumulator registers) and for 16-bit caches, whose 16 KB
-// tiles spilled to scratch under the two-wave budget (their automatic range count is one wave
-// per SIMD anyway); two waves per SIMD otherwise.
-template <int CACHE, int DEPTH, int HD>
-constexpr int decode_waves_per_eu() {
-  return (DEPTH > 2 || CACHE != kI8 || HD > 128) ? 1 : 2;
-}
-
-template <int CACHE, int QT, bool NT, bool QQ, int HALVES, int HD, int DEPTH, bool PAIR = false>
-__global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<CACHE, DEPTH, HD>()))) void decode_kernel(DecodeArgs a) {
-  __shared__ int32_t s_ids[HALVES * kMaxWavesPerWG][kChunkTiles * tile_blocks<CACHE>()];
-  const int lane = threadIdx.x % kWave;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int W = blockDim.x / (HALVES * kWave);  // kv heads per workgroup
-  const int kvh = blockIdx.y * W + (HALVES == 1 ? wave : wave % W);  // the wave's (pair of) kv heads
-  const int kv0 = PAIR ? 2 * kvh : kvh;  // first kv head of the wave
-  const int half = HALVES == 1 ? 0 : wave / W;
-
-  const int64_t L0 = seq_len_of(a, lane);
-  const Plan plan = make_plan(a, lane, L0);
-  // One range per workgroup, or two: ranges 2x and 2x + 1 when paired, else x and x + grid.x
-  // (the second only when the batch needs more ranges than there are workgroups).
-  int64_t r = blockIdx.x;
-  if constexpr (HALVES == 2)
-    r = plan.paired ? 2 * (int64_t)blockIdx.x + half
-                    : (int64_t)blockIdx.x + half * (int64_t)gridDim.x;
-  // The range's cut-sequence descriptor for merge_by_range_kernel: "none" first, overwritten by
-  // the same lane below if the range starts a cut sequence.  Every range below max_ranges gets
-  // one per call, so the workspace needs no initialisation.  It holds only values the walk
-  // already has (the merge derives the last range from them), so the walk keeps no more of the
-  // plan live than before.
-  const bool cut_writer = a.cut_desc && kvh == 0 && lane == 0 && r < a.max_ranges;
-  if (cut_writer) {
-    a.ws_cut[4 * r] = -1;
-    a.ws_cut[4 * r + 2] = plan.U;
-    a.ws_cut[4 * r + 3] = pack_plan(plan);
-  }
-  if (r >= plan.P) return;
-  const int64_t u0 = range_start(plan, r);
-  const int64_t u1 = range_start(plan, r + 1);
-  const bool last_range = r == plan.P - 1;
-
-  int64_t cum = 0;  // units of the sequences before this 64-sequence chunk
-  int64_t L = L0;
-  for (int64_t base = 0; base < a.batch; base += kWave) {
-    if (base > 0) L = seq_len_of(a, base + lane);
-    const int64_t n = tiles_of(a, L);
-    const int64_t u = units_of(a, n);
-    const int64_t incl = units_scan(a, u, lane) + cum;
-    const int64_t excl = incl - u;
-    const int64_t chunk_end = readlane64(incl, kWave - 1);
-    if (chunk_end >= u0) {
-      // Empty sequences occupy no units: the range holding their position writes their zeros.
-      uint64_t zmask = __ballot(base + lane < a.batch && n == 0 && excl >= u0 &&
-                                (excl < u1 || (last_range && excl == plan.U)));
-      while (zmask) {
-        const int j = __builtin_ctzll(zmask);
-        zmask &= zmask - 1;
-        if constexpr (PAIR) {
-          write_zero_rows<QT, 64>(a, base + j, kv0, lane);
-          write_zero_rows<QT, 64>(a, base + j, kv0 + 1, lane);
-        } else {
-          write_zero_rows<QT, HD>(a, base + j, kvh, lane);
-        }
-      }
-      // Sequences whose tiles (units past the start cost) meet [u0, u1).
-      uint64_t mask = __ballot(n > 0 && incl > u0 && excl + a.seq_cost < u1);
-      while (mask) {
-        const int j = __builtin_ctzll(mask);
-        mask &= mask - 1;
-        const int64_t first = readlane64(excl, j) + a.seq_cost;  // unit of tile 0
-        const int64_t nb = readlane64(n, j);
-        const int64_t Lb = readlane64(L, j);
-        const int64_t ta = (u0 > first ? u0 : first) - first;
-        const int64_t te = (u1 < first + nb ? u1 : first + nb) - first;
-        if (ta >= te) continue;
-        const bool full = ta == 0 && te == nb;
-        if (cut_writer && ta == 0 && te < nb) {  // b starts here and runs past this range
-          a.ws_cut[4 * r] = base + j;
-          a.ws_cut[4 * r + 1] = first + nb - 1;
-        }
-        run_segment<CACHE, QT, NT, QQ, HD, DEPTH, false, PAIR>(a, s_ids[wave], base + j, Lb, kv0, ta,
-                                                               te, full, 2 * r + cut_slot(ta), lane);
-      }
-    }
-    if (chunk_end >= u1 && !last_range) break;
-    cum = chunk_end;
-  }
-}
-
-// Short sequences, one workgroup per (sequence b = blockIdx.x, kv head blockIdx.y): its
-// group_waves<HD>() waves take equal shares of the sequence's tiles, leave their softmax states in
-// LDS, and waves 0-3 merge them into the output rows.  No partial records and no merge kernel: a
-// call costs one launch and the dependent loads of one segment.  Eight waves (two per SIMD) up
-// to head_dim 128; four at 256, one per SIMD as its registers need, whose states then take
-// 64 KB of LDS (eight would need 128 KB and spill).
-// SPLIT (few long sequences): gridDim.z workgroups per (sequence, kv head), workgroup z taking
-// tiles [z n / Z, (z + 1) n / Z) of the sequence's n; each leaves one record per query head
-// (row (b Z + z) Hq + h, the layout of the range records) for merge_split_kernel, and an empty
-// sequence leaves none (that kernel writes its zero rows).
-template <int HD>
-constexpr int group_waves() {
-  return HD > 128 ? 4 : 8;
-}
-
-template <int CACHE, int QT, bool QQ, int HD, bool SPLIT>
-__global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves_per_eu(HD > 128 ? 1 : 2))) void group_kernel(DecodeArgs a) {
-  constexpr int NW = group_waves<HD>();
-  __shared__ int32_t s_ids[NW][kChunkTiles * tile_blocks<CACHE>()];
-  __shared__ float s_acc[NW][HD / 4 * kWave];
-  __shared__ float s_m[NW][16];
-  __shared__ float s_l[NW][16];
-  const int lane = threadIdx.x % kWave;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int li = lane & 15;
-  const int lg = lane >> 4;
-  const int G = a.group;
-  const int64_t b = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int64_t L = seq_len_of(a, b);
-  const int64_t n = tiles_of(a, L);
-  if (n == 0) {  // uniform over the workgroup: every wave leaves before the barrier
-    if (!SPLIT && wave == 0) write_zero_rows<QT, HD>(a, b, kvh, lane);
-    return;
-  }
-  // Loaded before the tile loop: after the barrier it would add a memory latency to every call.
-  const float vscale = (CACHE == kI8 && !SPLIT) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
-  int64_t t0 = 0, span = n;  // this workgroup's tiles of the sequence
-  if constexpr (SPLIT) {
-    t0 = (int64_t)blockIdx.z * n / gridDim.z;
-    span = ((int64_t)blockIdx.z + 1) * n / gridDim.z - t0;
-  }
-  const int64_t ta = t0 + wave * span / NW;
-  const int64_t tb = t0 + (wave + 1) * span / NW;
-  if (ta < tb) {
-    run_segment<CACHE, QT, false, QQ, HD, 2, true>(a, s_ids[wave], b, L, kvh, ta, tb, false, 0,
-                                                   lane, s_acc[wave], s_m[wave], s_l[wave]);
-  } else if (li < G) {  // no tiles for this wave: the neutral state
-#pragma unroll
-    for (int j = 0; j < HD / 4; ++j) s_acc[wave][j * kWave + lane] = 0.0f;
-    if (lg == 0) {
-      s_m[wave][li] = -INFINITY;
-      s_l[wave][li] = 0.0f;
-    }
-  }
-  __syncthreads();
-  // Online-softmax merge of the NW states (exp2 domain), as merge_kernel does for records.  The
-  // four row groups rr of the accumulator layout are independent, so waves 0..3 take one each
-  // (head_dim elements HD/4 lg + HD/16 rr + [0, HD/16) of lane (li, lg)): wave 0 merging all
-  // of them took 2.3 us of a 9.4 us call at B = 1 x 512 tokens.
-  if (wave >= 4 || li >= G) return;
-  const int rr = wave;
-  float M = -INFINITY, Ls = 0.0f;
-  float O[HD / 16];
-#pragma unroll
-  for (int dt = 0; dt < HD / 16; ++dt) O[dt] = 0.0f;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) {
-    const float m = s_m[w][li];
-    const float l = s_l[w][li];
-    float A[HD / 16];
-#pragma unroll
-    for (int dt = 0; dt < HD / 16; ++dt) A[dt] = s_acc[w][(rr * (HD / 16) + dt) * kWave + lane];
-    const float Mn = fmaxf(M, m);
-    if (Mn == -INFINITY) {  // nothing finite yet: add unscaled (a NaN still reaches the output)
-      Ls += l;
-#pragma unroll
-      for (int dt = 0; dt < HD / 16; ++dt) O[dt] += A[dt];
-    } else {
-      const float ca = exp2_fast(M - Mn);
-      const float cb = exp2_fast(m - Mn);
-      Ls = Ls * ca + l * cb;
-#pragma unroll
-      for (int dt = 0; dt < HD / 16; ++dt) O[dt] = O[dt] * ca + A[dt] * cb;
-      M = Mn;
-    }
-  }
-  if constexpr (SPLIT) {
-    const int64_t row = ((int64_t)b * gridDim.z + blockIdx.z) * a.num_q_heads + kvh * G + li;
-    store_n<kF32, HD / 16>(reinterpret_cast<char*>(a.ws_acc + row * HD) + (HD / 4 * lg + HD / 16 * rr) * 4, O);
-    if (rr == 0 && lg == 0) {
-      a.ws_m[row] = M;
-      a.ws_l[row] = Ls;
-    }
-    return;
-  }
-  const float inv = Ls > 0.0f ? vscale / Ls : 0.0f;
-  char* op = a.out + (b * a.o_sb + (int64_t)(kvh * G + li) * a.o_sh) * esize<QT>();
-  float o[HD / 16];
-#pragma unroll
-  for (int dt = 0; dt < HD / 16; ++dt) o[dt] = O[dt] * inv;
-  store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), o);
-}
-
-// Merge of the split per-sequence layout's records: a.split = Z <= 64 records per (sequence b =
-// blockIdx.x, query head h = blockIdx.y), one wave.  Every record load is issued at entry (in
-// chunks of 16 records, each chunk taken only when Z reaches it, the index clamped into [0, Z)):
-// lane z < Z reads record z's running max and sum and each lane HD / 64 accumulator elements of
-// every record, so the call waits for one memory latency.  The wave then reduces the maxima and
-// the weighted sums, and each lane combines its elements over the Z records.  A record without
-// a finite maximum is weighted 1 when no record has one, so a NaN still reaches the output, as
-// in merge_in.
-template <int CACHE, int QT, int HD>
-__global__ __launch_bounds__(64) void merge_split_kernel(DecodeArgs a) {
-  constexpr int D = HD / 64;  // accumulator elements per lane
-  constexpr int kChunk = 16, kChunks = 64 / kChunk;
-  const int lane = threadIdx.x;
-  const int64_t b = blockIdx.x;
-  const int h = blockIdx.y;
-  const int Z = a.split;
-  char* op = a.out + (b * a.o_sb + (int64_t)h * a.o_sh + D * lane) * esize<QT>();
-  float O[D];
-#pragma unroll
-  for (int j = 0; j < D; ++j) O[j] = 0.0f;
-  float inv = 0.0f;
-  if (seq_len_of(a, b) > 0) {  // uniform: an empty sequence left no records (zero rows)
-    const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[h / a.group], 1e-6f) : 1.0f;
-    const int64_t row0 = b * Z * a.num_q_heads + h;  // record z: row0 + z Hq
-    const int64_t stride = (int64_t)a.num_q_heads * HD;
-    const float* acc = a.ws_acc + row0 * HD + D * lane;
-    float A[kChunks][kChunk][D];
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
-      if (c * kChunk < Z) {
-#pragma unroll
-        for (int k = 0; k < kChunk; ++k) {
-          const int z = c * kChunk + k < Z ? c * kChunk + k : Z - 1;
-#pragma unroll
-          for (int j = 0; j < D; ++j) A[c][k][j] = acc[z * stride + j];
-        }
-      }
-    }
-    const int64_t rz = row0 + (int64_t)(lane < Z ? lane : 0) * a.num_q_heads;
-    float m = a.ws_m[rz];
-    float l = a.ws_l[rz];
-    if (lane >= Z) {
-      m = -INFINITY;
-      l = 0.0f;
-    }
-    float M = m;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-    const float w = lane < Z ? (M == -INFINITY ? 1.0f : exp2_fast(m - M)) : 0.0f;
-    float Lw = l * w;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) Lw += __shfl_xor(Lw, o);
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
-      if (c * kChunk < Z) {
-#pragma unroll
-        for (int k = 0; k < kChunk; ++k) {
-          const float wk = __shfl(w, c * kChunk + k);
-          if (c * kChunk + k < Z) {
-#pragma unroll
-            for (int j = 0; j < D; ++j) O[j] += wk * A[c][k][j];
-          }
-        }
-      }
-    }
-    inv = Lw > 0.0f ? vscale / Lw : 0.0f;
-  }
-#pragma unroll
-  for (int j = 0; j < D; ++j) {
-    const float v = O[j] * inv;
-    if constexpr (QT == kF32)
-      reinterpret_cast<float*>(op)[j] = v;
-    else if constexpr (QT == kF16)
-      reinterpret_cast<_Float16*>(op)[j] = (_Float16)v;
-    else
-      reinterpret_cast<__bf16*>(op)[j] = (__bf16)v;
-  }
-}
-
-// Stores 4 consecutive fp32 values as DT (aligned to 4 elements).
-template <int DT>
-__device__ __forceinline__ void store4(char* p, f32x4 x) {
-  if constexpr (DT == kF32) {
-    *reinterpret_cast<f32x4*>(p) = x;
-  } else if constexpr (DT == kF16) {
-    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-    f16x4 h = {(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
-    *reinterpret_cast<f16x4*>(p) = h;
-  } else {
-    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-    bf16x4 h = {(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]};
-    *reinterpret_cast<bf16x4*>(p) = h;
-  }
-}
-
-// Online-softmax merge of one more partial (m, l, acc) into a running (M, L, O).  A partial
-// without a finite maximum is added unscaled, so non-finite scores (a NaN query) still reach the
-// output as NaN, as they do in the reference.
-__device__ __forceinline__ void merge_in(float& M, float& L, f32x4& O, float m, float l, f32x4 acc) {
-  const float Mn = fmaxf(M, m);
-  if (Mn == -INFINITY) {
-    L += l;
-    O += acc;
-    return;
-  }
-  const float a = exp2_fast(M - Mn);
-  const float c = exp2_fast(m - Mn);
-  L = L * a + l * c;
-  O = O * a + acc * c;
-  M = Mn;
-}
-
-// Folds the partial records of query head h of a cut sequence b whose tiles lie in ranges
-// r0 .. r0 + nr - 1 (range r0's slot-1 record, the later ranges' slot-0 records) and stores its
-// output row; a workgroup of MW waves.  A wave's lanes are RS = 256 / HD range slots of HD / 4
-// columns: lane (slot rs, column c4) of wave w owns head_dim elements [4 c4, 4 c4 + 4) of ranges
-// RS w + rs, RS w + rs + RS MW, ... and folds them in with one online-softmax pass, FOLD ranges'
-// loads in flight at a time (FOLD RS MW ranges per round for the workgroup); the RS MW running
-// states per column are then merged through LDS.  About 1 + nr / (FOLD RS MW) dependent memory
-// latencies.  Sixteen waves do not help a long sequence (one 32k-token sequence cut 256 ways: 7.2
-// us with eight waves, 8.7 with 16: its workgroup streams nr x 512 bytes per query head on one
-// compute unit).
-template <int CACHE, int QT, int MW, int HD, int FOLD = 4>
-__device__ __forceinline__ void merge_records(const DecodeArgs& a, int64_t b, int h, int64_t r0,
-                                              int64_t nr) {
-  constexpr int C4 = HD / 4;      // float4 columns of a head
-  constexpr int RS = kWave / C4;  // range slots per wave
-  __shared__ float s_m[RS * MW][C4];
-  __shared__ float s_l[RS * MW][C4];
-  __shared__ f32x4 s_o[RS * MW][C4];
-  const int kvh = h / a.group;
-  // Loaded at entry: after the barrier below it would add a memory latency to every merge.
-  const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
-  const int lane = threadIdx.x % kWave;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int rs = lane / C4;  // range slot of this lane within the wave
-  const int c4 = lane % C4;  // head_dim elements [4 c4, 4 c4 + 4)
-  const int slot = RS * wave + rs;  // 0 .. RS MW - 1
-  auto row_of = [&](int64_t c) -> int64_t {  // partial row of range r0 + c, head h
-    return (2 * (r0 + c) + cut_slot(c)) * a.num_q_heads + h;  // tile 0 lies in range r0
-  };
-
-  constexpr int kStride = RS * MW;
-  float M = -INFINITY, L = 0.0f;
-  f32x4 O = (f32x4)(0.0f);
-  for (int64_t cb = slot; cb < nr; cb += FOLD * kStride) {
-    // All FOLD loads unconditionally (a slot past the last range reads the last range's record
-    // again and is then ignored): a branch around each load made the compiler wait for the
-    // previous ones before issuing the next, one memory latency per range instead of per round.
-    float m[FOLD], l[FOLD];
-    f32x4 v[FOLD];
-#pragma unroll
-    for (int u = 0; u < FOLD; ++u) {
-      const int64_t c = cb + u * kStride;
-      const int64_t row = row_of(c < nr ? c : nr - 1);
-      m[u] = a.ws_m[row];
-      l[u] = a.ws_l[row];
-      v[u] = *reinterpret_cast<const f32x4*>(a.ws_acc + row * HD + 4 * c4);
-    }
-#pragma unroll
-    for (int u = 0; u < FOLD; ++u) {
-      const bool in = cb + u * kStride < nr;
-      merge_in(M, L, O, in ? m[u] : -INFINITY, in ? l[u] : 0.0f, in ? v[u] : (f32x4)(0.0f));
-    }
-  }
-  s_m[slot][c4] = M;
-  s_l[slot][c4] = L;
-  s_o[slot][c4] = O;
-  __syncthreads();
-  if (threadIdx.x >= C4) return;
-  M = -INFINITY;
-  L = 0.0f;
-  O = (f32x4)(0.0f);
-#pragma unroll
-  for (int k = 0; k < kStride; ++k) merge_in(M, L, O, s_m[k][c4], s_l[k][c4], s_o[k][c4]);
-  const float inv = L > 0.0f ? vscale / L : 0.0f;
-  store4<QT>(a.out + (b * a.o_sb + (int64_t)h * a.o_sh + 4 * c4) * esize<QT>(), O * inv);
-}
-
-// The merge indexed by sequence: grid (batch, num_q_heads), MW waves per query head; workgroup
-// (b, h) finds b's ranges from the plan (every sequence's units before b, i.e. a scan of
-// seq_lens[0 .. b]) and merges them if b is cut.  The host picks MW from the average number of
-// ranges per sequence (one wave when a round covers them, up to eight for a few long sequences).
-// Each wave's scan reads and sums all of the batch's lengths, so the cost grows with the batch
-// (B x num_q_heads waves x B / 64 chunks): the host takes it for batches below half the range
-// count, where its grid is also the smaller one.
-constexpr int kMergeChunks = 8;  // 64-sequence chunks of seq_lens a merge wave requests at once
-
-template <int CACHE, int QT, int MW, int HD, int FOLD>
-__global__ __launch_bounds__(MW * 64) void merge_kernel(DecodeArgs a) {
-  const int64_t b = blockIdx.x;
-  const int h = blockIdx.y;
-  const int lane = threadIdx.x % kWave;
-
-  // The plan (units of the whole batch) and S, the units before sequence b.  Above 64 sequences
-  // the lengths of the first kMergeChunks x 64 are requested at once instead of one 64-sequence
-  // chunk after another (B = 256: merge 10.9 -> 9.6 us; B = 128: 6.5 -> 6.1 us).
-  const int64_t nch = (a.batch + kWave - 1) / kWave;
-  const int64_t cb = b / kWave;  // b's chunk
-  const int bl = (int)(b - cb * kWave);
-  int64_t U = 0, S = 0, n = 0;
-  if (nch == 1) {
-    const int64_t L0 = seq_len_of(a, lane);
-    const int64_t u = units_of(a, tiles_of(a, L0));
-    U = units_sum(a, u, lane);
-    S = units_sum(a, lane < bl ? u : 0, lane);
-    n = tiles_of(a, readlane64(L0, bl));
-  } else {
-    int64_t Lc[kMergeChunks];
-    seq_len_chunks(a, 0, lane, Lc);
-#pragma unroll
-    for (int c = 0; c < kMergeChunks; ++c) {
-      if (c >= nch) break;
-      const int64_t u = units_of(a, tiles_of(a, Lc[c]));
-      const int64_t chunk = units_sum(a, u, lane);
-      U += chunk;
-      if (c < cb) {
-        S += chunk;
-      } else if (c == cb) {
-        S += units_sum(a, lane < bl ? u : 0, lane);
-        n = tiles_of(a, readlane64(Lc[c], bl));
-      }
-    }
-    for (int64_t c = kMergeChunks; c < nch; ++c) {  // batches above kMergeChunks x 64 sequences
-      const int64_t u = units_of(a, tiles_of(a, seq_len_of(a, c * kWave + lane)));
-      const int64_t chunk = units_sum(a, u, lane);
-      U += chunk;
-      if (c < cb) {
-        S += chunk;
-      } else if (c == cb) {
-        S += units_sum(a, lane < bl ? u : 0, lane);
-        n = tiles_of(a, seq_len_of(a, b));
-      }
-    }
-  }
-  const Plan plan = plan_of_units(a, U);
-  if (n == 0) return;  // zeros written by decode_kernel
-  const int64_t first = S + a.seq_cost;  // unit of tile 0
-  const int64_t r0 = range_of(plan, first);
-  const int64_t r1 = range_of(plan, first + n - 1);
-  if (r0 == r1) return;  // finished inside one range by decode_kernel
-  merge_records<CACHE, QT, MW, HD, FOLD>(a, b, h, r0, r1 - r0 + 1);
-}
-
-// The merge indexed by range: grid (max_ranges, num_q_heads), one wave per query head; workgroup
-// (r0, h) merges the cut sequence that range r0 starts, named by the decode kernel's descriptor
-// with the unit of its last tile, whose range under the plan is its last range r1 (ranges that
-// start none return at once).  No scan of seq_lens: its
-// cost does not grow with the batch (B = 256 x U[1, 2048]: 9.6 -> 5.0 us; B = 128 x U[1, 4096]:
-// 6.2 -> 5.0 us), but every range costs a workgroup, which for batches below half the range
-// count is the larger grid (B = 64 at 256 ranges: 4.6 -> 6.1 us).
-template <int CACHE, int QT, int HD>
-__global__ __launch_bounds__(64) void merge_by_range_kernel(DecodeArgs a) {
-  const int64_t r0 = blockIdx.x;
-  const int64_t b = a.ws_cut[4 * r0];
-  const int64_t last = a.ws_cut[4 * r0 + 1];
-  const Plan plan = unpack_plan(a.ws_cut[4 * r0 + 2], a.ws_cut[4 * r0 + 3]);
-  // b < 0: range r0 starts no cut sequence.  The other bounds hold for every descriptor the
-  // decode kernel writes (a MERGE call that does not follow MAIN on the same workspace reads
-  // whatever is there; they keep it inside the buffers).  One test of all of them (no
-  // short-circuit) has the kernel arguments read with the descriptor, not one dependent load
-  // after another.
-  const int64_t max_ranges = a.max_ranges;
-  if ((b < 0) | (b >= a.batch) | (plan.U <= 0) | (plan.P <= 0) | (plan.P > max_ranges) |
-      (last < 0) | (last >= plan.U) | ((int)blockIdx.y >= a.num_q_heads))
-    return;
-  const int64_t r1 = range_of(plan, last);
-  if (r1 <= r0 || r1 >= max_ranges) return;
-  merge_records<CACHE, QT, 1, HD>(a, b, (int)blockIdx.y, r0, r1 - r0 + 1);
-}
-
-}  // namespace int8kv
+#include "paged_decode_kernels.h"
 
 using namespace int8kv;
+
 
 namespace {
 
@@ -1592,14 +104,6 @@ constexpr int64_t kNonTemporalMinBytes = 128LL << 20;
 // MI355X; with equal halves the second then runs alone for the last quarter of the call.
 // 160 (62.5 %) measured best between cfg3 (~152) and B=32 x 8320 (~168): -2 us at both.
 constexpr int32_t kFirstShare = 160;
-
-// kv heads per workgroup (one wave each per range it owns): the largest of 4, 3, 2, 1 dividing
-// num_kv_heads.
-int waves_per_wg(int32_t num_kv_heads) {
-  for (int w = kMaxWavesPerWG; w > 1; --w)
-    if (num_kv_heads % w == 0) return w;
-  return 1;
-}
 
 // Compute units of the current device, queried on every call (no state is kept between calls;
 // the runtime answers from its cached device properties).  256 on MI355X.
@@ -1752,141 +256,6 @@ bool shape_ok(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32
          block_size_ok(block_size);
 }
 
-template <int CACHE, int QT, bool NT, bool QQ, int HD, bool PAIR = false>
-void launch_main(const DecodeArgs& a, dim3 grid, int W, hipStream_t s) {
-  if constexpr (CACHE == kI8 && HD <= 128) {  // HD 256: one range per workgroup, two tiles
-    if (a.halves == 2) {
-      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 2, HD, 2, PAIR>), grid, dim3(2 * W * kWave), 0,
-                         s, a);
-      return;
-    }
-    // Four tiles in flight leave no registers for an fp32 query's lo operands: two for those.
-    if (a.depth == 4 && QT != kF32) {
-      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 4, PAIR>), grid, dim3(W * kWave), 0, s,
-                         a);
-      return;
-    }
-  }
-  hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 2, PAIR>), grid, dim3(W * kWave), 0, s, a);
-}
-
-// The range decode kernel for one call: kv-head pairs at head_dim 64 run the HD = 128 kernel
-// with PAIR (see DecodeArgs::kv_pair).
-template <int CACHE, int QT, int HD, bool PAIR>
-void launch_ranges(const DecodeArgs& a, dim3 grid, int W, bool nt, hipStream_t s) {
-  constexpr int KH = PAIR ? 128 : HD;
-  // INT8 caches: non-temporal loads for large pools, int8 scores for a quantised query.
-  if constexpr (CACHE == kI8) {
-    if (nt && a.quantize_q)
-      launch_main<CACHE, QT, true, true, KH, PAIR>(a, grid, W, s);
-    else if (nt)
-      launch_main<CACHE, QT, true, false, KH, PAIR>(a, grid, W, s);
-    else if (a.quantize_q)
-      launch_main<CACHE, QT, false, true, KH, PAIR>(a, grid, W, s);
-    else
-      launch_main<CACHE, QT, false, false, KH, PAIR>(a, grid, W, s);
-  } else {
-    launch_main<CACHE, QT, false, false, KH, PAIR>(a, grid, W, s);
-  }
-}
-
-template <int CACHE, int QT, int HD>
-int launch(const DecodeArgs& a, uint32_t flags, bool nt, hipStream_t s) {
-  const int32_t hv = a.kv_pair ? a.num_kv_heads / 2 : a.num_kv_heads;  // kv heads (pairs) per range
-  const int W = waves_per_wg(a.group_mode ? a.num_kv_heads : hv);
-  if (a.group_mode) {  // one kernel, plus merge_split_kernel when split
-    if (flags & INT8KV_DECODE_MAIN) {
-      dim3 grid((unsigned)a.batch, (unsigned)a.num_kv_heads, (unsigned)(a.split > 0 ? a.split : 1));
-      const dim3 block(group_waves<HD>() * kWave);
-      if (a.split > 0) {
-        if (a.quantize_q)
-          hipLaunchKernelGGL((group_kernel<CACHE, QT, true, HD, true>), grid, block, 0, s, a);
-        else
-          hipLaunchKernelGGL((group_kernel<CACHE, QT, false, HD, true>), grid, block, 0, s, a);
-      } else {
-        if (a.quantize_q)
-          hipLaunchKernelGGL((group_kernel<CACHE, QT, true, HD, false>), grid, block, 0, s, a);
-        else
-          hipLaunchKernelGGL((group_kernel<CACHE, QT, false, HD, false>), grid, block, 0, s, a);
-      }
-      hipError_t e = hipGetLastError();
-      if (e != hipSuccess) return (int)e;
-    }
-    if (a.split > 0 && (flags & INT8KV_DECODE_MERGE)) {
-      dim3 grid((unsigned)a.batch, (unsigned)a.num_q_heads);
-      hipLaunchKernelGGL((merge_split_kernel<CACHE, QT, HD>), grid, dim3(kWave), 0, s, a);
-      hipError_t e = hipGetLastError();
-      if (e != hipSuccess) return (int)e;
-    }
-    return INT8KV_OK;
-  }
-  if (flags & INT8KV_DECODE_MAIN) {
-    dim3 grid((unsigned)((a.max_ranges + a.halves - 1) / a.halves), (unsigned)(hv / W));
-    if constexpr (HD == 64) {
-      if (a.kv_pair)
-        launch_ranges<CACHE, QT, HD, true>(a, grid, W, nt, s);
-      else
-        launch_ranges<CACHE, QT, HD, false>(a, grid, W, nt, s);
-    } else {
-      launch_ranges<CACHE, QT, HD, false>(a, grid, W, nt, s);
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return (int)e;
-  }
-  if (flags & INT8KV_DECODE_MERGE) {
-    if (a.cut_desc) {  // the smaller grid, and no scan of seq_lens
-      dim3 grid((unsigned)a.max_ranges, (unsigned)a.num_q_heads);
-      hipLaunchKernelGGL((merge_by_range_kernel<CACHE, QT, HD>), grid, dim3(kWave), 0, s, a);
-    } else {
-      dim3 grid((unsigned)a.batch, (unsigned)a.num_q_heads);
-      // Ranges per sequence on average; one round of a wave takes 2 x FOLD of them (at head_dim
-      // 128).  More waves and eight records per round only for long cut sequences (MI355X, op =
-      // decode + merge): one 32k-token sequence cut 256 ways 21.3 -> 18.4 us with 8 waves x 8,
-      // B = 1 x 4096 (67 ranges) 12.1 -> 11.6 us and B = 2 x 16384 (128 ranges each) 18.4 ->
-      // 17.4 us with 4 x 8, while at 32-36 ranges per sequence (B = 8 x 4096, 1 x 2048,
-      // 4 x 2048) eight per round costs 0.2-0.3 us and eight waves 1 us.
-      // The estimate is bounded by the longest sequence the table allows: a range holds at least
-      // min_tiles units, so no sequence spans more than units_max / min_tiles + 1 ranges.
-      const int64_t units_max =
-          (((int64_t)a.width << a.block_shift) + a.tile_tokens - 1) / a.tile_tokens + a.seq_cost;
-      const int64_t span_max = (units_max + a.min_tiles - 1) / a.min_tiles + 1;
-      int64_t per_seq = ((int64_t)a.max_ranges + a.batch - 1) / a.batch;
-      if (per_seq > span_max) per_seq = span_max;
-      if (per_seq <= 8)
-        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 1, HD, 4>), grid, dim3(kWave), 0, s, a);
-      else if (per_seq <= 16)
-        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 2, HD, 4>), grid, dim3(2 * kWave), 0, s, a);
-      else if (per_seq <= 48)
-        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 4, HD, 4>), grid, dim3(4 * kWave), 0, s, a);
-      else if (per_seq <= 128)
-        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 4, HD, 8>), grid, dim3(4 * kWave), 0, s, a);
-      else
-        hipLaunchKernelGGL((merge_kernel<CACHE, QT, 8, HD, 8>), grid, dim3(8 * kWave), 0, s, a);
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return (int)e;
-  }
-  return INT8KV_OK;
-}
-
-template <int CACHE>
-int launch_q(const DecodeArgs& a, int query_dtype, uint32_t flags, bool nt, hipStream_t s) {
-  switch (query_dtype) {
-    case INT8KV_F32:
-      return a.head_dim == 64    ? launch<CACHE, kF32, 64>(a, flags, nt, s)
-             : a.head_dim == 128 ? launch<CACHE, kF32, 128>(a, flags, nt, s)
-                                 : launch<CACHE, kF32, 256>(a, flags, nt, s);
-    case INT8KV_F16:
-      return a.head_dim == 64    ? launch<CACHE, kF16, 64>(a, flags, nt, s)
-             : a.head_dim == 128 ? launch<CACHE, kF16, 128>(a, flags, nt, s)
-                                 : launch<CACHE, kF16, 256>(a, flags, nt, s);
-    default:
-      return a.head_dim == 64    ? launch<CACHE, kBF16, 64>(a, flags, nt, s)
-             : a.head_dim == 128 ? launch<CACHE, kBF16, 128>(a, flags, nt, s)
-                                 : launch<CACHE, kBF16, 256>(a, flags, nt, s);
-  }
-}
-
 }  // namespace
 
 extern "C" int32_t int8kv_decode_auto_ranges(int32_t num_kv_heads) {
@@ -1945,6 +314,151 @@ int current_scratch(void** addr) {
   return INT8KV_OK;
 }
 
+// Merge kernel of the range layout's merge indexed by sequence: waves per workgroup and records
+// per lane slot and round, from an estimate of the ranges per sequence (ranges / batch, bounded
+// by the longest sequence the table allows: a range holds at least min_tiles units, so no
+// sequence spans more than units_max / min_tiles + 1 ranges).  One round of a wave takes
+// 2 x FOLD ranges (at head_dim 128).  More waves and eight records per round only for long cut
+// sequences (MI355X, op = decode + merge): one 32k-token sequence cut 256 ways 21.3 -> 18.4 us
+// with 8 waves x 8, B = 1 x 4096 (67 ranges) 12.1 -> 11.6 us and B = 2 x 16384 (128 ranges each)
+// 18.4 -> 17.4 us with 4 x 8, while at 32-36 ranges per sequence (B = 8 x 4096, 1 x 2048,
+// 4 x 2048) eight per round costs 0.2-0.3 us and eight waves 1 us.
+void merge_shape(int64_t batch, int64_t table_width, int32_t block_size, int32_t tile_tokens,
+                 int32_t seq_cost, int32_t min_tiles, int32_t num_ranges, int32_t* waves,
+                 int32_t* fold) {
+  const int64_t units_max =
+      ((int64_t)table_width * block_size + tile_tokens - 1) / tile_tokens + seq_cost;
+  const int64_t span_max = (units_max + min_tiles - 1) / min_tiles + 1;
+  int64_t per_seq = ((int64_t)num_ranges + batch - 1) / batch;
+  if (per_seq > span_max) per_seq = span_max;
+  *fold = per_seq <= 48 ? 4 : 8;
+  *waves = per_seq <= 8 ? 1 : per_seq <= 16 ? 2 : per_seq <= 128 ? 4 : 8;
+}
+
+// The host's whole decision for one call (argument checks on sizes and dtypes included; no
+// pointer is looked at).  cus: compute units of the device the call runs on.  scratch_cap: the
+// no-allocation entry point's workspace limit (0 = none); an automatic range count is lowered
+// to fit it.
+int plan_call(int query_dtype, int cache_dtype, int64_t batch, int32_t num_q_heads,
+              int32_t num_kv_heads, int32_t head_dim, int64_t num_blocks, int32_t block_size,
+              int64_t table_width, int64_t key_head_stride, int64_t value_head_stride,
+              int32_t num_ranges, int32_t min_tiles, uint32_t flags, int64_t cus,
+              size_t scratch_cap, HostPlan* hp) {
+  if (query_dtype != INT8KV_F32 && query_dtype != INT8KV_F16 && query_dtype != INT8KV_BF16)
+    return INT8KV_E_DTYPE;
+  if (cache_dtype != INT8KV_I8 && cache_dtype != INT8KV_BF16 && cache_dtype != INT8KV_F16)
+    return INT8KV_E_DTYPE;
+  if (batch < 0 || !shape_ok(num_q_heads, num_kv_heads, head_dim, block_size) ||
+      num_blocks <= 0 || table_width <= 0 || table_width > 0x7fffffffLL || num_ranges < 0 ||
+      num_ranges > kMaxRangesLimit || min_tiles < 0 || batch > 0x7fffffffLL ||
+      num_kv_heads > 65535 || cus <= 0)
+    return INT8KV_E_SHAPE;
+  const bool i8 = cache_dtype == INT8KV_I8;
+  const int64_t ce = i8 ? 1 : 2;
+  const bool automatic = num_ranges == 0 && min_tiles == 0;
+  const bool auto_ranges_req = num_ranges == 0;
+  const bool kv_pair_ok = kv_pair_shape(num_q_heads, num_kv_heads, head_dim) &&
+                          key_head_stride == head_dim && value_head_stride == head_dim;
+  const int32_t wave_heads = kv_pair_ok ? num_kv_heads / 2 : num_kv_heads;  // per range
+  if (num_ranges == 0) num_ranges = auto_ranges(wave_heads, cus);
+  if (scratch_cap > 0 && auto_ranges_req) {
+    // The partials of the automatic count may exceed the fixed scratch array (large GQA groups
+    // or head_dim 256): take the most ranges it holds instead.
+    const size_t fit = scratch_cap / workspace_bytes(num_q_heads, 1, head_dim);
+    if (fit < 1) return INT8KV_E_SCRATCH;
+    if ((size_t)num_ranges > fit) num_ranges = (int32_t)fit;
+  }
+  if (min_tiles == 0) min_tiles = auto_min_tiles(batch, table_width, block_size, num_ranges);
+  HostPlan p{};
+  p.cus = cus;
+  p.num_ranges = num_ranges;
+  p.min_tiles = min_tiles;
+  p.need = workspace_bytes(num_q_heads, num_ranges, head_dim);
+  if (scratch_cap > 0 && p.need > scratch_cap) return INT8KV_E_SCRATCH;
+  // (An empty batch launches nothing; the rules below divide by it.)
+  p.group_mode = (flags & INT8KV_DECODE_PER_SEQUENCE) != 0 ||
+                 (automatic && batch > 0 &&
+                  use_per_sequence(i8, head_dim, batch, num_kv_heads, table_width, block_size,
+                                   cus));
+  p.split = 0;
+  if (batch > 0 && ((flags & INT8KV_DECODE_SPLIT_SEQUENCES) != 0 ||
+                    (automatic && !p.group_mode &&
+                     use_split(head_dim, batch, num_kv_heads, table_width, block_size, cus)))) {
+    p.group_mode = true;
+    // A caller's range count fixes the split count (num_ranges / batch workgroups per sequence
+    // and kv head, e.g. the reference's num_splits); the automatic one fills the chip.
+    p.split = auto_ranges_req
+                  ? split_count(batch, num_kv_heads, num_ranges, cus)
+                  : (int32_t)std::min<int64_t>(64, num_ranges / batch);
+    if (p.split < 2) p.split = 0;
+  }
+  p.kv_pair = kv_pair_ok && !p.group_mode;
+  const int32_t tile_tokens = kRows * (i8 ? tile_blocks<kI8>() : tile_blocks<kBF16>());
+  p.seq_cost = kSeqStartCost;
+  {
+    // Paired layout (two ranges per workgroup, the first one longer) for INT8 calls whose
+    // range count reaches a pair per CU (two waves per SIMD: only an explicit num_ranges does)
+    // and that can fill it: P >= pair_min needs at least pair_min * min_tiles units, bounded
+    // here by batch x (longest possible sequence).  16-bit caches (1 % slower paired) keep one
+    // range per workgroup.
+    const int64_t wgs_y = wave_heads / waves_per_wg(wave_heads);  // workgroups per range
+    const int64_t pair_min = (2LL * cus + wgs_y - 1) / wgs_y;
+    const double units_max =
+        (double)batch * (std::ceil((double)table_width * block_size / tile_tokens) + p.seq_cost);
+    const bool paired = i8 && head_dim <= 128 && num_ranges >= pair_min &&
+                        units_max >= (double)pair_min * min_tiles &&
+                        units_max >= (double)pair_min * kPairMinUnits;
+    p.halves = paired ? 2 : 1;
+    p.pair_min = paired ? (int32_t)pair_min : 0x7fffffff;
+    // One wave per SIMD at most (every range's waves resident at once) and long ranges: INT8
+    // waves keep four tiles in flight instead of two, the bytes in flight of two waves.
+    p.depth = i8 && !paired && head_dim <= 128 && (int64_t)num_ranges * wave_heads <= 4LL * cus &&
+                      units_max >= (double)kDeepMinUnits * num_ranges
+                  ? 4
+                  : 2;
+  }
+  // The layout above was chosen with the base charge; the plan itself charges what a sequence
+  // start costs at the chosen depth (kSeqStartCost*).  decode_kernel and merge_kernel read the
+  // same value, so their range bounds agree.
+  if (i8) p.seq_cost = p.depth == 4 ? kSeqStartCostI8Deep : kSeqStartCostI8;
+  // Four tiles in flight leave no registers for an fp32 query's lo operands: two for those.
+  p.launch_depth = p.group_mode ? 2 : (p.depth == 4 && query_dtype != INT8KV_F32 ? 4 : 2);
+  // Units of one sequence are at most ceil(table_width x block_size / 32) + seq_cost (lengths are
+  // clamped to the table); 64 of them fit the 32-bit wave scans unless one sequence could hold
+  // more than 2^25 tiles.
+  p.scan32 = (double)kWave * (std::ceil((double)table_width * block_size / tile_tokens) +
+                              p.seq_cost) < 2147483647.0;
+  // The merge indexed by range (from descriptors the decode kernel then writes) for batches of
+  // at least half the range count, where its grid is the smaller one; below that, the merge
+  // indexed by sequence, and no descriptors.
+  p.cut_desc = 2 * batch >= (int64_t)num_ranges;
+  if (p.group_mode) {
+    p.merge = p.split > 0 ? kMergeSplit : kMergeNone;
+    p.merge_waves = p.split > 0 ? 1 : 0;
+    p.merge_fold = 0;
+  } else if (p.cut_desc) {
+    p.merge = kMergeByRange;
+    p.merge_waves = 1;
+    p.merge_fold = 0;
+  } else {
+    p.merge = kMergeBySequence;
+    merge_shape(batch > 0 ? batch : 1, table_width, block_size, tile_tokens, p.seq_cost,
+                min_tiles, num_ranges, &p.merge_waves, &p.merge_fold);
+  }
+  // Non-temporal K/V loads when the call may stream more than kNonTemporalMinBytes: the most it
+  // can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).  Only
+  // INT8 caches use the hint (stream_load); their lanes read K in 32-byte runs at every head_dim
+  // (k_run).  With one 64-byte run per lane at head_dim 256 the hint had made those calls 13-15 %
+  // slower; with two 32-byte runs it makes them 10 % faster (Gemma-2-9B shape, B = 64 x
+  // U[1, 16384]: 347 -> 313 us, 6.44 TB/s).  The per-sequence kernels read without it.
+  const int64_t touch_blocks = batch * table_width < num_blocks ? batch * table_width : num_blocks;
+  p.nt = i8 && !p.group_mode &&
+         (double)touch_blocks * block_size * num_kv_heads * head_dim * ce * 2 >
+             (double)kNonTemporalMinBytes;
+  *hp = p;
+  return INT8KV_OK;
+}
+
 // Shared body of int8kv_paged_decode and int8kv_paged_decode_noalloc.  from_scratch: take the
 // current device's scratch array as the workspace (after every argument check, so a rejected
 // call touches no device).
@@ -1961,17 +475,17 @@ int decode_entry(
   if (!query_strides || !key_cache_strides || !value_cache_strides || !table_strides ||
       !out_strides)
     return INT8KV_E_NULL;
-  if (query_dtype != INT8KV_F32 && query_dtype != INT8KV_F16 && query_dtype != INT8KV_BF16)
-    return INT8KV_E_DTYPE;
-  if (cache_dtype != INT8KV_I8 && cache_dtype != INT8KV_BF16 && cache_dtype != INT8KV_F16)
-    return INT8KV_E_DTYPE;
   if (table_dtype != INT8KV_I32 && table_dtype != INT8KV_I64) return INT8KV_E_DTYPE;
   if (seq_lens_dtype != INT8KV_I32 && seq_lens_dtype != INT8KV_I64) return INT8KV_E_DTYPE;
-  if (batch < 0 || !shape_ok(num_q_heads, num_kv_heads, head_dim, block_size) ||
-      num_blocks <= 0 || table_width <= 0 || table_width > 0x7fffffffLL || num_ranges < 0 ||
-      num_ranges > kMaxRangesLimit || min_tiles < 0 || batch > 0x7fffffffLL ||
-      num_kv_heads > 65535)
-    return INT8KV_E_SHAPE;
+  HostPlan hp;
+  {
+    // Sizes and dtypes first (the plan checks them); the CU count only once they pass.
+    const int st = plan_call(query_dtype, cache_dtype, batch, num_q_heads, num_kv_heads, head_dim,
+                             num_blocks, block_size, table_width, key_cache_strides[2],
+                             value_cache_strides[2], num_ranges, min_tiles, flags, 256,
+                             from_scratch ? kScratchBytes : 0, &hp);
+    if (st != INT8KV_OK) return st;
+  }
   if (batch == 0) return INT8KV_OK;
   if (!query || !key_cache || !value_cache || !block_tables || !seq_lens || !out)
     return INT8KV_E_NULL;
@@ -1990,22 +504,19 @@ int decode_entry(
         !aligned16(value_cache, value_cache_strides[i] * ce))
       return INT8KV_E_STRIDE;
   }
-
-  const bool automatic = num_ranges == 0 && min_tiles == 0;
-  const int64_t cus = cu_count();
-  const bool kv_pair_ok = kv_pair_shape(num_q_heads, num_kv_heads, head_dim) &&
-                          key_cache_strides[2] == head_dim && value_cache_strides[2] == head_dim;
-  const int32_t wave_heads = kv_pair_ok ? num_kv_heads / 2 : num_kv_heads;  // per range
-  if (num_ranges == 0) num_ranges = auto_ranges(wave_heads, cus);
-  if (min_tiles == 0) min_tiles = auto_min_tiles(batch, table_width, block_size, num_ranges);
-  const size_t need = workspace_bytes(num_q_heads, num_ranges, head_dim);
+  {
+    const int st = plan_call(query_dtype, cache_dtype, batch, num_q_heads, num_kv_heads, head_dim,
+                             num_blocks, block_size, table_width, key_cache_strides[2],
+                             value_cache_strides[2], num_ranges, min_tiles, flags, cu_count(),
+                             from_scratch ? kScratchBytes : 0, &hp);
+    if (st != INT8KV_OK) return st;
+  }
   if (from_scratch) {
-    if (need > kScratchBytes) return INT8KV_E_SCRATCH;
     const int st = current_scratch(&workspace);
     if (st != INT8KV_OK) return st;
     workspace_bytes_given = kScratchBytes;
   }
-  if (workspace == nullptr || workspace_bytes_given < need || ((uintptr_t)workspace % 16) != 0)
+  if (workspace == nullptr || workspace_bytes_given < hp.need || ((uintptr_t)workspace % 16) != 0)
     return INT8KV_E_WORKSPACE;
 
   DecodeArgs a;
@@ -2029,7 +540,7 @@ int decode_entry(
   a.out = static_cast<char*>(out);
   a.o_sb = out_strides[0];
   a.o_sh = out_strides[1];
-  const int64_t recs = (int64_t)num_ranges * 2 * num_q_heads;
+  const int64_t recs = (int64_t)hp.num_ranges * 2 * num_q_heads;
   float* ws = static_cast<float*>(workspace);
   a.ws_acc = ws;
   a.ws_m = ws + recs * head_dim;
@@ -2042,86 +553,74 @@ int decode_entry(
   a.num_q_heads = num_q_heads;
   a.group = num_q_heads / num_kv_heads;
   a.width = (int32_t)table_width;
-  a.max_ranges = num_ranges;
-  a.min_tiles = min_tiles;
-  a.seq_cost = kSeqStartCost;
+  a.max_ranges = hp.num_ranges;
+  a.min_tiles = hp.min_tiles;
+  a.seq_cost = hp.seq_cost;
   a.quantize_q = (flags & INT8KV_DECODE_QUANTIZE_Q) != 0;
-  a.group_mode = (flags & INT8KV_DECODE_PER_SEQUENCE) != 0 ||
-                 (automatic &&
-                  use_per_sequence(cache_dtype == INT8KV_I8, head_dim, batch, num_kv_heads,
-                                   table_width, block_size, cus));
-  a.split = 0;
-  if ((flags & INT8KV_DECODE_SPLIT_SEQUENCES) != 0 ||
-      (automatic && !a.group_mode &&
-       use_split(head_dim, batch, num_kv_heads, table_width, block_size, cus))) {
-    a.group_mode = true;
-    a.split = split_count(batch, num_kv_heads, num_ranges, cus);
-  }
-  a.kv_pair = kv_pair_ok && !a.group_mode;
+  a.group_mode = hp.group_mode;
+  a.split = hp.split;
+  a.kv_pair = hp.kv_pair;
   a.block_shift = __builtin_ctz((unsigned)block_size);
   a.tile_tokens = kRows * (cache_dtype == INT8KV_I8 ? tile_blocks<kI8>() : tile_blocks<kBF16>());
   a.bt_is64 = table_dtype == INT8KV_I64;
   a.sl_is64 = seq_lens_dtype == INT8KV_I64;
   a.sm_scale_log2e = sm_scale * kLog2e;
   a.first_share = kFirstShare;
-  {
-    // Paired layout (two ranges per workgroup, the first one longer) for INT8 calls whose
-    // range count reaches a pair per CU (two waves per SIMD: only an explicit num_ranges does)
-    // and that can fill it: P >= pair_min needs at least pair_min * min_tiles units, bounded
-    // here by batch x (longest possible sequence).  16-bit caches (1 % slower paired) keep one
-    // range per workgroup.
-    const int64_t wgs_y = wave_heads / waves_per_wg(wave_heads);  // workgroups per range
-    const int64_t pair_min = (2LL * cus + wgs_y - 1) / wgs_y;
-    const double units_max =
-        (double)batch * (std::ceil((double)table_width * block_size / a.tile_tokens) + a.seq_cost);
-    const bool paired = cache_dtype == INT8KV_I8 && head_dim <= 128 && num_ranges >= pair_min &&
-                        units_max >= (double)pair_min * min_tiles &&
-                        units_max >= (double)pair_min * kPairMinUnits;
-    a.halves = paired ? 2 : 1;
-    a.pair_min = paired ? (int32_t)pair_min : 0x7fffffff;
-    // One wave per SIMD at most (every range's waves resident at once) and long ranges: INT8
-    // waves keep four tiles in flight instead of two, the bytes in flight of two waves.
-    a.depth = cache_dtype == INT8KV_I8 && !paired && head_dim <= 128 &&
-                      (int64_t)num_ranges * wave_heads <= 4LL * cus &&
-                      units_max >= (double)kDeepMinUnits * num_ranges
-                  ? 4
-                  : 2;
-  }
-  // The layout above was chosen with the base charge; the plan itself charges what a sequence
-  // start costs at the chosen depth (kSeqStartCost*).  decode_kernel and merge_kernel read the
-  // same value, so their range bounds agree.
-  if (cache_dtype == INT8KV_I8) a.seq_cost = a.depth == 4 ? kSeqStartCostI8Deep : kSeqStartCostI8;
-  // Units of one sequence are at most ceil(table_width x block_size / 32) + seq_cost (lengths are
-  // clamped to the table); 64 of them fit the 32-bit wave scans unless one sequence could hold
-  // more than 2^25 tiles.
-  a.scan32 = (double)kWave * (std::ceil((double)table_width * block_size / a.tile_tokens) +
-                              a.seq_cost) < 2147483647.0;
-  // The merge indexed by range (from descriptors the decode kernel then writes) for batches of
-  // at least half the range count, where its grid is the smaller one; below that, the merge
-  // indexed by sequence, and no descriptors.
-  a.cut_desc = 2 * batch >= (int64_t)a.max_ranges;
-
-  // Non-temporal K/V loads when the call may stream more than kNonTemporalMinBytes: the most it
-  // can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).  Only
-  // INT8 caches use the hint (stream_load); their lanes read K in 32-byte runs at every head_dim
-  // (k_run).  With one 64-byte run per lane at head_dim 256 the hint had made those calls 13-15 %
-  // slower; with two 32-byte runs it makes them 10 % faster (Gemma-2-9B shape, B = 64 x
-  // U[1, 16384]: 347 -> 313 us, 6.44 TB/s).
-  const int64_t touch_blocks = batch * table_width < num_blocks ? batch * table_width : num_blocks;
-  const bool nt = (double)touch_blocks * block_size * num_kv_heads * head_dim * ce * 2 >
-                  (double)kNonTemporalMinBytes;
+  a.halves = hp.halves;
+  a.pair_min = hp.pair_min;
+  a.depth = hp.depth;
+  a.scan32 = hp.scan32;
+  a.cut_desc = hp.merge == kMergeByRange;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (cache_dtype) {
     case INT8KV_I8:
-      return launch_q<kI8>(a, query_dtype, flags, nt, s);
+      return launch_cache_int8(a, hp, query_dtype, flags, s);
     case INT8KV_BF16:
-      return launch_q<kBF16>(a, query_dtype, flags, nt, s);
+      return launch_cache_bf16(a, hp, query_dtype, flags, s);
     default:
-      return launch_q<kF16>(a, query_dtype, flags, nt, s);
+      return launch_cache_fp16(a, hp, query_dtype, flags, s);
   }
 }
 
 }  // namespace
+
+extern "C" int int8kv_decode_plan(int query_dtype, int cache_dtype, int64_t batch,
+                                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  int64_t num_blocks, int32_t block_size, int64_t table_width,
+                                  int64_t key_head_stride, int64_t value_head_stride,
+                                  int32_t num_ranges, int32_t min_tiles, uint32_t flags,
+                                  int32_t compute_units, int32_t no_alloc,
+                                  int8kv_decode_plan_t* plan) {
+  if (plan == nullptr) return INT8KV_E_NULL;
+  if (compute_units < 0) return INT8KV_E_SHAPE;
+  const int64_t cus = compute_units > 0 ? compute_units : cu_count();
+  HostPlan hp;
+  const int st = plan_call(query_dtype, cache_dtype, batch, num_q_heads, num_kv_heads, head_dim,
+                           num_blocks, block_size, table_width, key_head_stride,
+                           value_head_stride, num_ranges, min_tiles, flags, cus,
+                           no_alloc ? kScratchBytes : 0, &hp);
+  if (st != INT8KV_OK) return st;
+  int8kv_decode_plan_t p{};
+  p.layout = !hp.group_mode ? INT8KV_LAYOUT_RANGES
+             : hp.split > 0 ? INT8KV_LAYOUT_SPLIT
+                            : INT8KV_LAYOUT_PER_SEQUENCE;
+  p.kernels = batch == 0 ? 0 : (hp.merge == kMergeNone ? 1 : 2);
+  p.num_ranges = hp.num_ranges;
+  p.min_tiles = hp.min_tiles;
+  p.seq_cost = hp.seq_cost;
+  p.ranges_per_workgroup = hp.group_mode ? 0 : hp.halves;
+  p.depth = hp.launch_depth;
+  p.kv_pair = hp.kv_pair ? 1 : 0;
+  p.split = hp.split;
+  p.non_temporal = hp.nt ? 1 : 0;
+  p.merge = hp.merge;
+  p.merge_waves = hp.merge_waves;
+  p.merge_fold = hp.merge_fold;
+  p.compute_units = (int32_t)cus;
+  p.workspace_bytes = hp.need;
+  *plan = p;
+  return INT8KV_OK;
+}
 
 extern "C" int int8kv_paged_decode(
     const void* query, int query_dtype, int64_t batch, int32_t num_q_heads, int32_t head_dim,

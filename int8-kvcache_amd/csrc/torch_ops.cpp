@@ -98,13 +98,18 @@ hipStream_t current_stream(const at::Tensor& t) {
 }
 
 constexpr int64_t kMaxRanges = 1 << 20;
+constexpr int64_t kMaxSplits = 64;  // workgroups per (sequence, kv head) the split merge combines
 
-// num_splits splits per sequence = num_splits * batch equal ranges of the token stream; none = 0
-// (the library's automatic choice).
-int32_t ranges_for(int64_t batch, const c10::optional<int64_t>& num_splits) {
-  if (!num_splits.has_value()) return 0;
-  int64_t r = *num_splits * std::max<int64_t>(1, batch);
-  return (int32_t)std::max<int64_t>(1, std::min<int64_t>(kMaxRanges, r));
+// The reference's num_splits (src/triton_ops/int8_paged_attention.py:590-604) as the library's
+// (num_ranges, flags): none = automatic; 1 = a single pass (one workgroup per sequence and kv
+// head, INT8KV_DECODE_PER_SEQUENCE); S >= 2 = S workgroups per sequence and kv head over equal
+// shares of its tiles (INT8KV_DECODE_SPLIT_SEQUENCES with num_ranges = S x batch), at most 64.
+std::pair<int32_t, uint32_t> split_request(int64_t batch, const c10::optional<int64_t>& num_splits) {
+  if (!num_splits.has_value()) return {0, 0u};
+  if (*num_splits <= 1) return {0, INT8KV_DECODE_PER_SEQUENCE};
+  const int64_t s = std::min<int64_t>(*num_splits, kMaxSplits);
+  const int64_t r = std::min<int64_t>(kMaxRanges, s * std::max<int64_t>(1, batch));
+  return {(int32_t)r, INT8KV_DECODE_SPLIT_SEQUENCES};
 }
 
 // Workspace of an eager call, kept per (device, stream) for the calling host thread: a call's
@@ -177,6 +182,7 @@ at::Tensor int8_paged_attention(const at::Tensor& query, const at::Tensor& key_c
   const int64_t B = query.size(0), Hq = query.size(1), D = query.size(2);
   const int64_t Hkv = key_cache.size(2);
   require(value_cache.sizes() == key_cache.sizes());
+  require(Hkv > 0, "key_cache has no kv heads");
   require(key_cache.size(3) == D && Hq % Hkv == 0);
   require(block_tables.size(0) == B && seq_lens.numel() == B);
   require(k_scale.dim() == 1 && v_scale.dim() == 1);
@@ -189,9 +195,11 @@ at::Tensor int8_paged_attention(const at::Tensor& query, const at::Tensor& key_c
     throw ValueFailure("Unknown impl='" + impl + "'; expected 'auto', 'v3' or 'v4'");
   if (impl == "v3" && !num_splits.has_value()) num_splits = 1;
   at::Tensor out = at::empty({B, Hq, D}, query.options());
-  const int64_t flags = INT8KV_DECODE_ALL | (quantize_q ? INT8KV_DECODE_QUANTIZE_Q : 0);
+  const auto split = split_request(B, num_splits);
+  const int64_t flags =
+      INT8KV_DECODE_ALL | split.second | (quantize_q ? INT8KV_DECODE_QUANTIZE_Q : 0);
   return decode_into(query, key_cache, value_cache, block_tables, seq_lens, fp32_vector(k_scale),
-                     fp32_vector(v_scale), out, ranges_for(B, num_splits), flags, c10::nullopt, 0);
+                     fp32_vector(v_scale), out, split.first, flags, c10::nullopt, 0);
 }
 
 // src/triton_ops/bf16_paged_attention.py:118-165.
@@ -206,15 +214,17 @@ at::Tensor bf16_paged_attention(const at::Tensor& query, const at::Tensor& key_c
   require(is_index(block_tables.scalar_type()) && is_index(seq_lens.scalar_type()));
   const int64_t B = query.size(0), Hq = query.size(1), D = query.size(2);
   require(value_cache.sizes() == key_cache.sizes());
+  require(key_cache.size(2) > 0, "key_cache has no kv heads");
   require(key_cache.size(3) == D && Hq % key_cache.size(2) == 0);
   require(block_tables.size(0) == B && seq_lens.numel() == B);
   require(key_cache.stride(-1) == 1 && value_cache.stride(-1) == 1);
   require(query.is_cuda(), "bf16_paged_attention needs GPU tensors");
   require_same_device({&key_cache, &value_cache, &block_tables, &seq_lens}, query);
   at::Tensor out = at::empty({B, Hq, D}, query.options());
+  const auto split = split_request(B, num_splits);
   return decode_into(query, key_cache, value_cache, block_tables, seq_lens, c10::nullopt,
-                     c10::nullopt, out, ranges_for(B, num_splits), INT8KV_DECODE_ALL, c10::nullopt,
-                     0);
+                     c10::nullopt, out, split.first, INT8KV_DECODE_ALL | split.second,
+                     c10::nullopt, 0);
 }
 
 // src/triton_ops/int8_cache_write.py:85-149 (validation :100-115).
@@ -261,8 +271,14 @@ at::Tensor paged_decode(const at::Tensor& query, const at::Tensor& key_cache,
                         const at::Tensor& seq_lens, const c10::optional<at::Tensor>& k_scale,
                         const c10::optional<at::Tensor>& v_scale, at::Tensor out, int64_t num_ranges,
                         int64_t flags, const c10::optional<at::Tensor>& workspace, int64_t min_tiles) {
-  require(query.dim() == 3 && key_cache.dim() == 4 && out.sizes() == query.sizes());
+  require(query.dim() == 3 && key_cache.dim() == 4 && value_cache.dim() == 4 &&
+          out.sizes() == query.sizes());
+  require(block_tables.dim() == 2 && seq_lens.dim() == 1);
+  require(value_cache.sizes() == key_cache.sizes());
   require(query.is_cuda(), "paged_decode needs GPU tensors");
+  require_same_device({&key_cache, &value_cache, &block_tables, &seq_lens, &out}, query);
+  if (k_scale.has_value()) require(k_scale->device() == query.device() && k_scale->dim() == 1);
+  if (v_scale.has_value()) require(v_scale->device() == query.device() && v_scale->dim() == 1);
   return decode_into(query, key_cache, value_cache, block_tables, seq_lens, k_scale, v_scale, out,
                      num_ranges, flags, workspace, min_tiles);
 }

@@ -19,7 +19,10 @@ CSRC_DIR = PKG_DIR.parent / "csrc"
 INCLUDE_DIR = PKG_DIR.parent.parent / "include"
 LIB_PATH = PKG_DIR / "libint8kv.so"
 
-SOURCES = ["cache_write.hip", "paged_decode.hip", "decode_loop_ops.hip"]
+# The paged decode's kernels compile per cache type in parallel (paged_decode_<type>.hip, from
+# paged_decode_kernels.h); paged_decode.hip is its host side.
+SOURCES = ["cache_write.hip", "paged_decode.hip", "paged_decode_int8.hip", "paged_decode_bf16.hip",
+           "paged_decode_fp16.hip", "decode_loop_ops.hip"]
 # The torch extension over the C ABI (host code only; torch headers, linked to libint8kv.so).
 EXT_SOURCE = "torch_ops.cpp"
 EXT_NAME = "_int8kv_torch"
@@ -79,25 +82,45 @@ def _torch_ext_flags():
     return cflags, lflags
 
 
-def build_library(verbose: bool = False, torch_ext: bool = True) -> Path:
-    """Compiles every HIP source into LIB_PATH and the torch extension into EXT_PATH (always
-    rebuilds): one compiler process per source, in parallel, then the links."""
+OBJ_CACHE = PKG_DIR.parent / "build"  # objects kept by incremental builds (git-ignored)
+
+
+def build_library(verbose: bool = False, torch_ext: bool = True, incremental: bool = False) -> Path:
+    """Compiles every HIP source into LIB_PATH and the torch extension into EXT_PATH: one
+    compiler process per source, in parallel, then the links.  By default everything is rebuilt
+    in a temporary directory; ``incremental`` keeps the objects in OBJ_CACHE and recompiles only
+    the sources older than their object or than any header they may include (a developer's
+    edit-build loop)."""
     from concurrent.futures import ThreadPoolExecutor
 
     hipcc = hipcc_path()
-    obj_dir = Path(tempfile.mkdtemp(prefix="int8kv_build_"))
+    if incremental:
+        OBJ_CACHE.mkdir(parents=True, exist_ok=True)
+        obj_dir = OBJ_CACHE
+    else:
+        obj_dir = Path(tempfile.mkdtemp(prefix="int8kv_build_"))
+    headers = [*CSRC_DIR.glob("*.h"), *INCLUDE_DIR.glob("*.h")]
+    newest_header = max((h.stat().st_mtime for h in headers), default=0.0)
+
+    def stale(src: Path, obj: Path) -> bool:
+        if not incremental or not obj.exists():
+            return True
+        return obj.stat().st_mtime < max(src.stat().st_mtime, newest_header)
+
     try:
         compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
         objs = [obj_dir / (Path(s).stem + ".o") for s in SOURCES]
         cmds = [[hipcc, *compile_flags, f"-I{INCLUDE_DIR}", "-c", str(CSRC_DIR / s), "-o", str(o)]
-                for s, o in zip(SOURCES, objs)]
+                for s, o in zip(SOURCES, objs) if stale(CSRC_DIR / s, o)]
         ext_obj = obj_dir / "torch_ops.o"
         if torch_ext:
             cflags, lflags = _torch_ext_flags()
-            cmds.append(["g++", *cflags, "-c", str(CSRC_DIR / EXT_SOURCE), "-o", str(ext_obj)])
-        with ThreadPoolExecutor(max_workers=len(cmds)) as pool:
-            for fut in [pool.submit(_run, c, verbose) for c in cmds]:
-                fut.result()
+            if stale(CSRC_DIR / EXT_SOURCE, ext_obj):
+                cmds.append(["g++", *cflags, "-c", str(CSRC_DIR / EXT_SOURCE), "-o", str(ext_obj)])
+        if cmds:
+            with ThreadPoolExecutor(max_workers=len(cmds)) as pool:
+                for fut in [pool.submit(_run, c, verbose) for c in cmds]:
+                    fut.result()
         tmp = LIB_PATH.with_suffix(".so.tmp")
         _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)],
              verbose)
@@ -107,9 +130,10 @@ def build_library(verbose: bool = False, torch_ext: bool = True) -> Path:
             _run(["g++", "-shared", str(ext_obj), *lflags, "-o", str(tmp)], verbose)
             os.replace(tmp, EXT_PATH)
     finally:
-        shutil.rmtree(obj_dir, ignore_errors=True)
+        if not incremental:
+            shutil.rmtree(obj_dir, ignore_errors=True)
     return LIB_PATH
 
 
 if __name__ == "__main__":
-    print(build_library(verbose="-v" in sys.argv))
+    print(build_library(verbose="-v" in sys.argv, incremental="--incremental" in sys.argv))

@@ -58,15 +58,24 @@ def _cached_workspace(dev, stream: int, need: int) -> torch.Tensor:
     return ws
 
 
-def ranges_for(batch: int, num_splits) -> int:
-    """Range count for a forced split count (0 = let the library choose).
+MAX_SPLITS = 64  # workgroups per (sequence, kv head) the split layout's merge combines
 
-    The kernel cuts the batch's token stream into equal ranges; ``num_splits`` splits per
-    sequence correspond to ``num_splits * batch`` ranges (exactly so for equal lengths).
-    """
+
+def split_request(batch: int, num_splits) -> tuple[int, int]:
+    """(num_ranges, flags) of int8kv_paged_decode for the reference's ``num_splits``
+    (src/triton_ops/int8_paged_attention.py:590-604: grid (B, Hkv, S), split s over logical
+    blocks [s n / S, (s + 1) n / S)): None = the library's automatic choice; 1 = a single pass,
+    one workgroup per (sequence, kv head) with no partials and no merge
+    (INT8KV_DECODE_PER_SEQUENCE); S >= 2 = S workgroups per (sequence, kv head) over equal
+    shares of its tiles, combined by the merge kernel (INT8KV_DECODE_SPLIT_SEQUENCES with
+    num_ranges = S x batch; at most 64 splits)."""
     if num_splits is None:
-        return 0
-    return max(1, min(MAX_RANGES, int(num_splits) * max(1, int(batch))))
+        return 0, 0
+    s = int(num_splits)
+    if s <= 1:
+        return 0, _lib.DECODE_PER_SEQUENCE
+    s = min(s, MAX_SPLITS)
+    return min(MAX_RANGES, s * max(1, int(batch))), _lib.DECODE_SPLIT_SEQUENCES
 
 
 def debug_check_slots(slot_mapping, num_blocks: int, block_size: int) -> None:

@@ -29,6 +29,26 @@ DECODE_MAIN, DECODE_MERGE, DECODE_ALL, DECODE_QUANTIZE_Q = 1, 2, 3, 4
 DECODE_PER_SEQUENCE = 8
 DECODE_SPLIT_SEQUENCES = 16
 
+# int8kv_decode_plan_t.layout / .merge
+LAYOUT_RANGES, LAYOUT_PER_SEQUENCE, LAYOUT_SPLIT = 0, 1, 2
+LAYOUT_NAMES = {LAYOUT_RANGES: "ranges", LAYOUT_PER_SEQUENCE: "per_sequence", LAYOUT_SPLIT: "split"}
+MERGE_NAMES = {0: "none", 1: "by_sequence", 2: "by_range", 3: "split"}
+
+
+class DecodePlan(ctypes.Structure):
+    """int8kv_decode_plan_t (include/int8kv.h)."""
+
+    _fields_ = [(name, ctypes.c_int32) for name in (
+        "layout", "kernels", "num_ranges", "min_tiles", "seq_cost", "ranges_per_workgroup", "depth",
+        "kv_pair", "split", "non_temporal", "merge", "merge_waves", "merge_fold", "compute_units")
+    ] + [("workspace_bytes", ctypes.c_uint64)]
+
+    def as_dict(self) -> dict:
+        d = {name: getattr(self, name) for name, _ in self._fields_}
+        d["layout"] = LAYOUT_NAMES[self.layout]
+        d["merge"] = MERGE_NAMES[self.merge]
+        return d
+
 ERRORS = {
     -1: "INT8KV_E_NULL (a required pointer is NULL)",
     -2: "INT8KV_E_DTYPE (unsupported element type)",
@@ -72,6 +92,11 @@ def load() -> ctypes.CDLL:
     lib.int8kv_decode_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
     lib.int8kv_decode_auto_ranges.restype = i32
     lib.int8kv_decode_auto_ranges.argtypes = [i32]
+    lib.int8kv_decode_plan.restype = ctypes.c_int
+    lib.int8kv_decode_plan.argtypes = [
+        ctypes.c_int, ctypes.c_int, i64, i32, i32, i32, i64, i32, i64, i64, i64, i32, i32, u32, i32,
+        i32, ctypes.POINTER(DecodePlan),
+    ]
     lib.int8kv_paged_decode.restype = ctypes.c_int
     lib.int8kv_paged_decode.argtypes = [
         _vp, ctypes.c_int, i64, i32, i32, _c_i64p, _vp, _vp, ctypes.c_int, i64, i32, i32,
@@ -101,6 +126,29 @@ def load() -> ctypes.CDLL:
     lib.int8kv_version.argtypes = []
     _lib = lib
     return lib
+
+
+def decode_plan(query_dtype, cache_dtype, batch: int, num_q_heads: int, num_kv_heads: int,
+                head_dim: int, num_blocks: int, block_size: int, table_width: int,
+                key_head_stride: int | None = None, value_head_stride: int | None = None,
+                num_ranges: int = 0, min_tiles: int = 0, flags: int = DECODE_ALL,
+                compute_units: int = 0, no_alloc: bool = False) -> dict:
+    """What int8kv_paged_decode (or, with ``no_alloc``, int8kv_paged_decode_noalloc) does for
+    these sizes: layout, range count, tiles in flight, merge kernel... (int8kv_decode_plan).
+    Dtypes are torch dtypes or dtype codes; the head strides default to head_dim (contiguous
+    caches); ``compute_units`` 0 means the current device.  Pure host computation: no kernel is
+    launched and no device memory is read."""
+    lib = load()
+    qd = DTYPE_CODE.get(query_dtype, query_dtype)
+    cd = DTYPE_CODE.get(cache_dtype, cache_dtype)
+    ks = head_dim if key_head_stride is None else key_head_stride
+    vs = head_dim if value_head_stride is None else value_head_stride
+    plan = DecodePlan()
+    st = lib.int8kv_decode_plan(qd, cd, batch, num_q_heads, num_kv_heads, head_dim, num_blocks,
+                                block_size, table_width, ks, vs, num_ranges, min_tiles, flags,
+                                compute_units, int(bool(no_alloc)), ctypes.byref(plan))
+    check(st, "int8kv_decode_plan")
+    return plan.as_dict()
 
 
 _STRIDE_ARRAYS: dict = {}

@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _decode, _ext
+from . import _decode, _ext, _lib
 
 
 def bf16_paged_attention(
@@ -21,7 +21,10 @@ def bf16_paged_attention(
     *,
     num_splits: int | None = None,
 ) -> torch.Tensor:
-    """Paged decode on a 16-bit KV cache [num_blocks, BS, Hkv, D] (bf16 or fp16)."""
+    """Paged decode on a 16-bit KV cache [num_blocks, BS, Hkv, D] (bf16 or fp16).
+
+    ``num_splits`` (not in the reference's signature; keyword only) has int8_paged_attention's
+    meaning: None automatic, 1 a single pass, S >= 2 S splits per sequence."""
     ext = _ext.module()
     if ext is not None and not _decode.DEBUG_CHECKS:
         return ext.bf16_paged_attention(query, key_cache, value_cache, block_tables, seq_lens,
@@ -45,8 +48,9 @@ def bf16_paged_attention(
             and seq_lens.device == dev), "all tensors must be on one device (the GPU)"
     if _decode.DEBUG_CHECKS:
         _decode.debug_check(block_tables, seq_lens, num_blocks, block_size, False)
-    ranges = _decode.ranges_for(B, num_splits)
+    ranges, split_flags = _decode.split_request(B, num_splits)
     output = torch.empty((B, Hq, D), device=query.device, dtype=query.dtype)
     return _decode.paged_decode(
-        query, key_cache, value_cache, block_tables, seq_lens, None, None, output, ranges
+        query, key_cache, value_cache, block_tables, seq_lens, None, None, output, ranges,
+        _lib.DECODE_ALL | split_flags,
     )

@@ -10,12 +10,15 @@ libint8kv.so.  Differences that a caller can observe:
 * Work split: the kernel cuts the batch's token stream (all sequences' 32-token tiles in batch
   order) into equal ranges, one workgroup each, so ragged batches are balanced; sequences cut
   by a range bound are combined by a merge pass.
-* ``impl``: "v4" and "auto" run the group-shared kernel with the automatic range count; "v3"
-  (one pass per query head and sequence in the reference, :393-504) runs the same kernel with
-  one range per sequence on average.  Any other value raises ValueError, as in the reference
-  (:767-768).
-* ``num_splits``: an integer S asks for S splits per sequence, i.e. S * B ranges (the reference
-  splits the logical blocks of the longest sequence into S ranges, :156-162).
+* ``impl``: "v4" and "auto" run the group-shared kernels with the automatic layout; "v3" (one
+  pass per query head and sequence in the reference, :393-504) runs a single pass: one
+  workgroup per (sequence, kv head), whose waves share the sequence's tiles and combine their
+  softmax states on chip (no partials, no merge kernel).  Any other value raises ValueError, as
+  in the reference (:767-768).
+* ``num_splits``: 1 is that single pass; S >= 2 runs S workgroups per (sequence, kv head), each
+  over an equal share of the sequence's tiles, whose partials the merge kernel combines (the
+  reference's grid (B, Hkv, S), :590-604; it splits the table's logical blocks, :156-162, this
+  build the sequence's own tiles).  At most 64 splits are used.
 * ``quantize_q=True`` quantises each (sequence, query head) row of q to int8 first, as the
   reference does (:137-146, :798-802): q_scale = max(absmax / 127, 1e-6),
   q8 = clamp(round_half_away_from_zero(q / q_scale), -127, 127), scores scaled by q_scale.
@@ -81,9 +84,9 @@ def int8_paged_attention(
         v_scale = v_scale.to(torch.float32).contiguous()
     if impl == "v3" and num_splits is None:
         num_splits = 1
-    ranges = _decode.ranges_for(B, num_splits)
+    ranges, split_flags = _decode.split_request(B, num_splits)
     output = torch.empty((B, Hq, D), device=dev, dtype=query.dtype)
-    flags = _lib.DECODE_ALL | (_lib.DECODE_QUANTIZE_Q if quantize_q else 0)
+    flags = _lib.DECODE_ALL | split_flags | (_lib.DECODE_QUANTIZE_Q if quantize_q else 0)
     return _decode.paged_decode(
         query, key_cache, value_cache, block_tables, seq_lens, k_scale, v_scale, output, ranges,
         flags,

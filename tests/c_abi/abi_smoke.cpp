@@ -167,6 +167,12 @@ int main() {
                                      t_st, dlens, INT8KV_I32, dks, dvs, sm, dout2, q_st, 0, 0,
                                      INT8KV_DECODE_ALL, stream));
   HIP_OK(hipStreamSynchronize(stream));
+  int8kv_decode_plan_t plan;
+  LIB_OK(int8kv_decode_plan(INT8KV_BF16, INT8KV_I8, B, kHq, kHkv, kD, NB, kBS, width, kD, kD, 0, 0,
+                            INT8KV_DECODE_ALL, 0, 0, &plan));
+  std::printf("automatic plan: layout %d, %d kernel(s), %d ranges, workspace %llu bytes\n",
+              plan.layout, plan.kernels, plan.num_ranges,
+              (unsigned long long)plan.workspace_bytes);
 
   std::vector<int8_t> kc(cache_bytes), vc(cache_bytes);
   std::vector<uint16_t> out(q.size()), out2(q.size()), out3(q.size());

@@ -90,3 +90,22 @@ def bf16_caches(c: DecodeCase, dtype=torch.bfloat16):
 def to_dev(c: DecodeCase, dev):
     return (c.query.to(dev), torch.from_numpy(c.kc).to(dev), torch.from_numpy(c.vc).to(dev),
             c.block_tables.to(dev), c.seq_lens.to(dev), c.k_scale.to(dev), c.v_scale.to(dev))
+
+
+def ranges_call(case_or_tensors, dev, splits=None, quantize_q=False, out=None, min_tiles=0):
+    """INT8 decode through the library's range layout with ``splits`` x batch explicit ranges
+    (None: the automatic range count with ``min_tiles``, 2 if 0): int8kv_paged_decode called
+    directly, so tests can pin the range layout and its range count (the drop-in operator's
+    num_splits selects the per-sequence and split layouts).  ``case_or_tensors``: a DecodeCase
+    or the tuple of to_dev."""
+    from int8kv import _decode, _lib
+
+    t = to_dev(case_or_tensors, dev) if isinstance(case_or_tensors, DecodeCase) else case_or_tensors
+    q, kc, vc, bt, sl, ks, vs = t
+    ranges = 0 if splits is None else max(1, int(splits) * q.shape[0])
+    res = torch.empty_like(q) if out is None else out
+    flags = _lib.DECODE_ALL | (_lib.DECODE_QUANTIZE_Q if quantize_q else 0)
+    _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, res, ranges, flags, None,
+                         (min_tiles or 2) if splits is None else 0)
+    torch.cuda.synchronize()
+    return res

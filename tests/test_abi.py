@@ -37,6 +37,7 @@ def test_header_declares_expected_entry_points():
         "int8kv_argmax_rows",
         "int8kv_cache_write",
         "int8kv_decode_auto_ranges",
+        "int8kv_decode_plan",
         "int8kv_decode_workspace_bytes",
         "int8kv_dynamic_cache_write",
         "int8kv_paged_decode",

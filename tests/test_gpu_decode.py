@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import int8kv
-from cases import bf16_caches, decode_case, oracle_int8, to_dev
+from cases import bf16_caches, decode_case, oracle_int8, ranges_call, to_dev
 from conftest import MAX_ABS, MIN_COS, metrics
 from oracle import int8kv_oracle as O
 
@@ -80,6 +80,8 @@ def test_tile_block_chunk_boundaries(cuda, lens):
     ref = oracle_int8(c)
     for chunk in (None, 1, 3, 7):
         _check(_int8(c, cuda, num_splits=chunk), ref, f"{lens} splits={chunk}")
+    for splits in (1, 3, 7):
+        _check(ranges_call(c, cuda, splits), ref, f"{lens} {splits} ranges per sequence")
 
 
 def test_one_token_sequences_return_v0(cuda):
@@ -297,15 +299,13 @@ def test_large_pool_streaming_path(cuda):
     btw = torch.zeros(bt.shape[0], width, dtype=bt.dtype, device=cuda)
     btw[:, : bt.shape[1]] = bt
     _check(int8kv.int8_paged_attention(q, kb, vb, btw, sl, ks, vs), oracle_int8(c), "large pool")
-    small = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs, num_splits=1)
-    big = int8kv.int8_paged_attention(q, kb, vb, btw, sl, ks, vs, num_splits=1)
-    torch.cuda.synchronize()
+    small = ranges_call((q, kc, vc, bt, sl, ks, vs), cuda, 1)
+    big = ranges_call((q, kb, vb, btw, sl, ks, vs), cuda, 1)
     _check(big, oracle_int8(c), "large pool, one range per sequence")
     assert torch.equal(small, big)
     # the int8-score kernel (quantize_q) on the streaming path as well
-    small_q = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs, quantize_q=True, num_splits=1)
-    big_q = int8kv.int8_paged_attention(q, kb, vb, btw, sl, ks, vs, quantize_q=True, num_splits=1)
-    torch.cuda.synchronize()
+    small_q = ranges_call((q, kc, vc, bt, sl, ks, vs), cuda, 1, quantize_q=True)
+    big_q = ranges_call((q, kb, vb, btw, sl, ks, vs), cuda, 1, quantize_q=True)
     ref_q = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
                                   c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
                                   quantize_q=True)
@@ -322,6 +322,8 @@ def test_block_sizes(cuda, block_size):
     ref = oracle_int8(c)
     for splits in (None, 1, 3, 7):
         _check(_int8(c, cuda, num_splits=splits), ref, f"int8 bs={block_size} splits={splits}")
+    for splits in (1, 3, 7):
+        _check(ranges_call(c, cuda, splits), ref, f"int8 bs={block_size} {splits} ranges per seq")
     ref_q = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
                                   c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
                                   quantize_q=True)
@@ -351,6 +353,10 @@ def test_block_size_relabelling_is_bit_exact(cuda):
         b = int8kv.int8_paged_attention(q, kc16, vc16, bt16, sl, ks, vs, num_splits=splits)
         torch.cuda.synchronize()
         assert torch.equal(a, b), f"int8 splits={splits}"
+        if splits is not None:
+            a = ranges_call((q, kc, vc, bt, sl, ks, vs), cuda, splits)
+            b = ranges_call((q, kc16, vc16, bt16, sl, ks, vs), cuda, splits)
+            assert torch.equal(a, b), f"int8 {splits} ranges per sequence"
     k32, v32 = (x.to(cuda) for x in bf16_caches(c))
     a = int8kv.bf16_paged_attention(q, k32, v32, bt, sl)
     b = int8kv.bf16_paged_attention(q, k32.view(2 * nb, 16, 4, 128), v32.view(2 * nb, 16, 4, 128),
@@ -406,8 +412,9 @@ def test_paired_ranges_regime(cuda, hq, hkv, lens):
     c = decode_case(lens, seed=hkv + len(lens), hq=hq, hkv=hkv)
     ref = oracle_int8(c)
     splits = _pair_splits(hkv, len(lens))
-    _check(_int8(c, cuda, num_splits=splits), ref, f"paired hq={hq} hkv={hkv}")
+    _check(ranges_call(c, cuda, splits), ref, f"paired hq={hq} hkv={hkv}")
     _check(_int8(c, cuda), ref, f"automatic hq={hq} hkv={hkv}")
+    _check(ranges_call(c, cuda, 1), ref, f"one range per sequence hq={hq} hkv={hkv}")
     _check(_int8(c, cuda, num_splits=1), ref, f"single pass hq={hq} hkv={hkv}")
 
 
@@ -421,15 +428,20 @@ def test_four_tiles_in_flight(cuda, splits):
     lens = [4097, 8229, 65, 97, 33, 1, 16384 + 95, 640]
     c = decode_case(lens, seed=40 + (splits or 0), extra_blocks=5)
     ref = oracle_int8(c)
-    _check(_int8(c, cuda, num_splits=splits), ref, f"splits={splits}")
+
+    def call(**kw):
+        return _int8(c, cuda, **kw) if splits is None else ranges_call(c, cuda, splits, **kw)
+
+    _check(call(), ref, f"splits={splits}")
     ref_q = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
                                   c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
                                   quantize_q=True)
-    _check(_int8(c, cuda, num_splits=splits, quantize_q=True), ref_q, f"splits={splits} qq")
+    _check(call(quantize_q=True), ref_q, f"splits={splits} qq")
 
 
-@pytest.mark.parametrize("splits", [None, 1, 3])
-def test_batches_beyond_one_wave_of_sequences(cuda, splits):
+@pytest.mark.parametrize("how,splits", [("op", None), ("op", 1), ("op", 3), ("ranges", 1),
+                                        ("ranges", 3)])
+def test_batches_beyond_one_wave_of_sequences(cuda, how, splits):
     """B = 200 (four 64-sequence chunks in the kernels' batch walk) with ragged lengths, some
     empty sequences spread over the chunks, int64 lengths and tables."""
     g = torch.Generator().manual_seed(77)
@@ -439,14 +451,17 @@ def test_batches_beyond_one_wave_of_sequences(cuda, splits):
     for b in (0, 63, 64, 130, 199):
         sl[b] = 0
     q, kc, vc, bt, _, ks, vs = to_dev(c, cuda)
-    out = int8kv.int8_paged_attention(q, kc, vc, bt.to(torch.int64), sl.to(cuda), ks, vs,
-                                      num_splits=splits)
-    torch.cuda.synchronize()
+    if how == "op":
+        out = int8kv.int8_paged_attention(q, kc, vc, bt.to(torch.int64), sl.to(cuda), ks, vs,
+                                          num_splits=splits)
+        torch.cuda.synchronize()
+    else:
+        out = ranges_call((q, kc, vc, bt.to(torch.int64), sl.to(cuda), ks, vs), cuda, splits)
     ref = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
                                 sl.numpy(), c.k_scale.numpy(), c.v_scale.numpy())
     for b in (0, 63, 64, 130, 199):
         assert (out[b] == 0).all(), b
-    _check(out, ref, f"B=200 splits={splits}")
+    _check(out, ref, f"B=200 {how} splits={splits}")
 
 
 @pytest.mark.parametrize("splits", [None, 3])
@@ -462,8 +477,8 @@ def test_batches_beyond_eight_chunks(cuda, splits):
     for b in (5, 300, 520, 599):
         sl[b] = 0
     q, kc, vc, bt, _, ks, vs = to_dev(c, cuda)
-    out = int8kv.int8_paged_attention(q, kc, vc, bt, sl.to(cuda), ks, vs, num_splits=splits)
-    torch.cuda.synchronize()
+    # 3 ranges per sequence: the merge indexed by sequence (2 B < ranges)
+    out = ranges_call((q, kc, vc, bt, sl.to(cuda), ks, vs), cuda, splits)
     ref = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
                                 sl.numpy(), c.k_scale.numpy(), c.v_scale.numpy())
     for b in (5, 300, 520, 599):
@@ -484,8 +499,7 @@ def test_wide_tables_take_the_64bit_unit_scan(cuda, splits):
     sl = c.seq_lens.clone()
     sl[10] = sl[65] = 0
     q, kc, vc, bt, _, ks, vs = to_dev(c, cuda)
-    out = int8kv.int8_paged_attention(q, kc, vc, bt, sl.to(cuda), ks, vs, num_splits=splits)
-    torch.cuda.synchronize()
+    out = ranges_call((q, kc, vc, bt, sl.to(cuda), ks, vs), cuda, splits)
     ref = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
                                 sl.numpy(), c.k_scale.numpy(), c.v_scale.numpy())
     assert (out[10] == 0).all() and (out[65] == 0).all()
@@ -504,6 +518,8 @@ def test_head_dim_64(cuda, hq, hkv):
     ref = oracle_int8(c)
     for splits in (None, 1, 3):
         _check(_int8(c, cuda, num_splits=splits), ref, f"d64 {hq}/{hkv} splits={splits}")
+    for splits in (1, 3):
+        _check(ranges_call(c, cuda, splits), ref, f"d64 {hq}/{hkv} {splits} ranges per seq")
     ref_q = O.paged_attention_ref(c.query.float().numpy(), c.kc, c.vc, c.block_tables.numpy(),
                                   c.seq_lens.numpy(), c.k_scale.numpy(), c.v_scale.numpy(),
                                   quantize_q=True)
@@ -529,8 +545,9 @@ def test_head_dim_64_paired_regime(cuda):
     for lens in ([8192] * 16, [8192] * 15 + [77]):
         c = decode_case(lens, seed=64 + len(lens), hq=32, hkv=8, head_dim=64, extra_blocks=3)
         ref = oracle_int8(c)
-        _check(_int8(c, cuda, num_splits=_pair_splits(8, len(lens))), ref, f"d64 large {lens[-1]}")
+        _check(ranges_call(c, cuda, _pair_splits(8, len(lens))), ref, f"d64 large {lens[-1]}")
         _check(_int8(c, cuda), ref, f"d64 automatic {lens[-1]}")
+        _check(ranges_call(c, cuda, 1), ref, f"d64 one range per sequence {lens[-1]}")
         _check(_int8(c, cuda, num_splits=1), ref, f"d64 single pass {lens[-1]}")
 
 
@@ -680,14 +697,39 @@ AUTO_LAYOUT_POINTS = [
 ]
 
 
+def _forced_like(plan, q, kc, vc, bt, sl, ks, vs):
+    """The call forced into the layout a plan names (flags, or the plan's explicit range count
+    and minimum range for the range layout), which runs the same kernels as the automatic call
+    the plan describes."""
+    from int8kv import _decode, _lib
+
+    out = torch.empty_like(q)
+    if plan["layout"] == "per_sequence":
+        args = (0, _lib.DECODE_ALL | _lib.DECODE_PER_SEQUENCE, None, 0)
+    elif plan["layout"] == "split":
+        args = (0, _lib.DECODE_ALL | _lib.DECODE_SPLIT_SEQUENCES, None, 0)
+    else:
+        args = (plan["num_ranges"], _lib.DECODE_ALL, None, plan["min_tiles"])
+    _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, out, *args)
+    torch.cuda.synchronize()
+    return out
+
+
+def _plan_of(q, kc, bt, cus=0):
+    from int8kv import _lib
+
+    return _lib.decode_plan(q.dtype, kc.dtype, q.shape[0], q.shape[1], kc.shape[2], q.shape[2],
+                            kc.shape[0], kc.shape[1], bt.shape[1], kc.stride(2), kc.stride(2),
+                            compute_units=cus)
+
+
 @pytest.mark.parametrize("d,hq,hkv,cache,batch,width,per_seq", AUTO_LAYOUT_POINTS)
 def test_automatic_layout_choice(cuda, d, hq, hkv, cache, batch, width, per_seq):
-    """The automatic call (num_ranges = 0, min_tiles = 0) takes the per-sequence layout exactly
-    where the rule says: its output is then bit-identical to the forced per-sequence layout's
-    (and differs from it otherwise, the range layout summing in another order); both match the
-    oracle.  Ragged lengths up to the table width, one empty sequence."""
-    if torch.cuda.get_device_properties(cuda).multi_processor_count != 256:
-        pytest.skip("the thresholds are stated for 256 compute units")
+    """The automatic call (num_ranges = 0, min_tiles = 0) runs the layout int8kv_decode_plan
+    reports for this device: its output is bit-identical to the call forced into that layout,
+    and both match the oracle.  At 256 compute units the plan is the rule's choice on each side
+    of its thresholds (the CPU tests check the rule itself, for other CU counts too).  Ragged
+    lengths up to the table width, one empty sequence."""
     g = torch.Generator().manual_seed(batch * width + d)
     lens = torch.randint(1, width * 16 + 1, (batch,), generator=g).tolist()
     lens[0] = width * 16
@@ -707,11 +749,13 @@ def test_automatic_layout_choice(cuda, d, hq, hkv, cache, batch, width, per_seq)
                                     v16.float().numpy(), c.block_tables.numpy(), c.seq_lens.numpy())
         kc, vc, ks, vs = k16.to(cuda), v16.to(cuda), None, None
         auto = int8kv.bf16_paged_attention(q, kc, vc, bt, sl)
-    forced = _group(q, kc, vc, bt, sl, ks, vs)
+    plan = _plan_of(q, kc, bt)
+    assert (_plan_of(q, kc, bt, 256)["layout"] == "per_sequence") == per_seq
+    forced = _forced_like(plan, q, kc, vc, bt, sl, ks, vs)
     torch.cuda.synchronize()
-    _check(auto, ref, f"automatic {cache} d={d} B={batch} width={width}")
-    _check(forced, ref, f"per-sequence {cache} d={d} B={batch} width={width}")
-    assert torch.equal(auto, forced) == per_seq
+    _check(auto, ref, f"automatic {cache} d={d} B={batch} width={width} ({plan['layout']})")
+    _check(forced, ref, f"forced {plan['layout']} {cache} d={d} B={batch} width={width}")
+    assert torch.equal(auto, forced)
 
 
 @pytest.mark.parametrize("hq,hkv,d", [(28, 4, 128), (32, 8, 64), (16, 8, 256), (8, 1, 128)])
@@ -765,13 +809,9 @@ AUTO_SPLIT_POINTS = [
 
 @pytest.mark.parametrize("d,hq,hkv,batch,width,split", AUTO_SPLIT_POINTS)
 def test_automatic_split_choice(cuda, d, hq, hkv, batch, width, split):
-    """The automatic call takes the split per-sequence layout exactly where the rule says: its
-    output is then bit-identical to the forced INT8KV_DECODE_SPLIT_SEQUENCES call's (and differs
-    otherwise); both match the oracle."""
-    from int8kv import _decode, _lib
-
-    if torch.cuda.get_device_properties(cuda).multi_processor_count != 256:
-        pytest.skip("the thresholds are stated for 256 compute units")
+    """The automatic call runs the layout the plan reports for this device (bit-identical to the
+    call forced into it, both against the oracle); at 256 compute units that is the split layout
+    exactly where the rule says."""
     g = torch.Generator().manual_seed(batch * width + d + 1)
     lens = torch.randint(1, width * 16 + 1, (batch,), generator=g).tolist()
     lens[0] = width * 16
@@ -780,11 +820,10 @@ def test_automatic_split_choice(cuda, d, hq, hkv, batch, width, split):
     q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
     q = q.float()  # fp32 outputs: a bf16 rounding could hide a different summation order
     auto = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs)
-    forced = torch.empty_like(q)
-    _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, forced, 0,
-                         _lib.DECODE_ALL | _lib.DECODE_SPLIT_SEQUENCES)
-    torch.cuda.synchronize()
+    plan = _plan_of(q, kc, bt)
+    assert (_plan_of(q, kc, bt, 256)["layout"] == "split") == split
+    forced = _forced_like(plan, q, kc, vc, bt, sl, ks, vs)
     ref = oracle_int8(c)
-    _check(auto, ref, f"automatic d={d} B={batch} width={width}")
-    _check(forced, ref, f"split d={d} B={batch} width={width}")
-    assert torch.equal(auto, forced) == split
+    _check(auto, ref, f"automatic d={d} B={batch} width={width} ({plan['layout']})")
+    _check(forced, ref, f"forced {plan['layout']} d={d} B={batch} width={width}")
+    assert torch.equal(auto, forced)

@@ -18,7 +18,7 @@ import pytest
 import torch
 
 import int8kv
-from cases import bf16_caches, decode_case, oracle_int8, to_dev
+from cases import bf16_caches, decode_case, oracle_int8, ranges_call, to_dev
 from conftest import MAX_ABS, MIN_COS, metrics
 from oracle import int8kv_oracle as O
 
@@ -88,6 +88,9 @@ def test_merge_by_range_and_large_batch(cuda):
     q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
     ref = oracle_int8(c)
     for splits in (1, 2, 3):
+        out = ranges_call((q, kc, vc, bt, sl, ks, vs), cuda, splits)
+        assert (out[50] == 0).all()
+        _check(out, ref, f"B=96 {splits} ranges per sequence")
         out = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs, num_splits=splits)
         torch.cuda.synchronize()
         assert (out[50] == 0).all()

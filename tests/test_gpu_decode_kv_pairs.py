@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import int8kv
-from cases import bf16_caches, decode_case, oracle_int8, to_dev
+from cases import bf16_caches, decode_case, oracle_int8, ranges_call, to_dev
 from conftest import MAX_ABS, MIN_COS, metrics
 from oracle import int8kv_oracle as O
 
@@ -42,6 +42,10 @@ def test_int8_pairs_and_fallbacks(cuda, hq, hkv):
         torch.cuda.synchronize()
         assert (out[0] == 0).all()
         _check(out, ref, f"int8 {hq}/{hkv} splits={splits}")
+    for splits in (1, 2, 5):  # the range layout, where the kv heads go in pairs
+        out = ranges_call((q, kc, vc, bt, sl, ks, vs), cuda, splits)
+        assert (out[0] == 0).all()
+        _check(out, ref, f"int8 {hq}/{hkv} {splits} ranges per sequence")
     for qdt in (torch.float16, torch.float32):
         out = int8kv.int8_paged_attention(q.to(qdt), kc, vc, bt, sl, ks, vs)
         torch.cuda.synchronize()

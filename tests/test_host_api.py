@@ -94,13 +94,18 @@ def test_dequantize_debug_helper():
     assert out.tolist() == [[[[0.5, -1.0], [6.0, 8.0]]]]
 
 
-def test_ranges_for_forced_splits():
-    assert _decode.ranges_for(64, None) == 0
-    assert _decode.ranges_for(64, 1) == 64
-    assert _decode.ranges_for(3, 4) == 12
-    assert _decode.ranges_for(0, 4) == 4
-    assert _decode.ranges_for(5, 0) == 1
-    assert _decode.ranges_for(1 << 20, 8) == 1 << 20
+def test_split_request_maps_num_splits():
+    """num_splits of the reference (None automatic, 1 a single pass, S splits per sequence) as
+    the library's (num_ranges, flags)."""
+    from int8kv import _lib
+
+    assert _decode.split_request(64, None) == (0, 0)
+    assert _decode.split_request(64, 1) == (0, _lib.DECODE_PER_SEQUENCE)
+    assert _decode.split_request(64, 0) == (0, _lib.DECODE_PER_SEQUENCE)
+    assert _decode.split_request(3, 4) == (12, _lib.DECODE_SPLIT_SEQUENCES)
+    assert _decode.split_request(0, 4) == (4, _lib.DECODE_SPLIT_SEQUENCES)
+    assert _decode.split_request(5, 100) == (5 * 64, _lib.DECODE_SPLIT_SEQUENCES)  # at most 64
+    assert _decode.split_request(1 << 20, 8) == (1 << 20, _lib.DECODE_SPLIT_SEQUENCES)
 
 
 def test_synthetic_generators():

@@ -118,6 +118,28 @@ def test_head_dim_64_and_split_layouts(cuda):
         assert err <= MAX_ABS and cos >= MIN_COS, (what, err, cos)
 
 
+def test_large_group_fits_the_scratch_with_fewer_ranges(cuda):
+    """A GQA group whose automatic range count's partials exceed the 16 MiB array (32 query
+    heads per 2 kv heads at head_dim 128: 512 ranges would need 17.1 MB) runs with the most
+    ranges the array holds (int8kv_decode_plan reports the count) instead of being refused: the
+    same bits as the workspace entry point at that range count, within the oracle bar."""
+    g = torch.Generator().manual_seed(41)
+    lens = torch.randint(1, 3000, (64,), generator=g).tolist()
+    c = decode_case(lens, seed=41, hq=32, hkv=2, extra_blocks=3)
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    args = (q.dtype, kc.dtype, 64, 32, 2, 128, kc.shape[0], 16, bt.shape[1])
+    small = _lib.decode_plan(*args, no_alloc=True)
+    full = _lib.decode_plan(*args)
+    assert small["layout"] == full["layout"] == "ranges"
+    assert small["num_ranges"] < full["num_ranges"] and small["workspace_bytes"] <= 16 << 20
+    got = _noalloc(q, kc, vc, bt, sl, ks, vs, torch.full_like(q, float("nan")))
+    want = _with_workspace(q, kc, vc, bt, sl, ks, vs, small["num_ranges"])
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    err, cos, _ = metrics(got.float().cpu().numpy(), oracle_int8(c))
+    assert err <= MAX_ABS and cos >= MIN_COS, (err, cos)
+
+
 def test_oversized_request_is_refused(cuda):
     c = decode_case([64], seed=34)
     q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
