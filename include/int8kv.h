@@ -124,13 +124,16 @@ int int8kv_dynamic_cache_write(const void* key, const void* value, int src_dtype
  * (4 x compute units / num_kv_heads: 256 for 4 kv heads on MI355X).
  * At head_dim 64 with an even num_kv_heads and at most 8 query heads per kv head, the decode
  * takes kv heads in pairs (one wave per pair) and its automatic count is that of
- * num_kv_heads / 2 (int8kv_decode_workspace_bytes(..., 0) accounts for it).
+ * num_kv_heads / 2; with more than 16 query heads per kv head each kv head takes
+ * ceil(group / 16) waves (column tiles of 16 query heads) and the count is that of
+ * num_kv_heads x ceil(group / 16).  int8kv_decode_workspace_bytes(..., 0) accounts for both.
  */
 int32_t int8kv_decode_auto_ranges(int32_t num_kv_heads);
 
 /*
  * Bytes of device workspace int8kv_paged_decode needs (the split partials: one running max,
- * one running sum and one head_dim accumulator per range, slot and query head, and per range a
+ * one running sum and one accumulator of head_dim rounded up to 64, 128 or 256 elements per
+ * range, slot and query head, and per range a
  * 32-byte descriptor of the cut sequence it starts); independent of the batch, the context
  * lengths and the block-table width.  num_ranges is the value that will
  * be passed to int8kv_paged_decode (0 = automatic, for the current device).  Returns 0 for
@@ -221,9 +224,11 @@ int int8kv_decode_plan(int query_dtype, int cache_dtype, int64_t batch, int32_t 
  *                 one sequence into more than 128 ranges; decided from batch, table width and
  *                 block size only).
  *                 With num_ranges = 0 and min_tiles = 0, short calls take the per-sequence layout
- *                 below instead (decided from head_dim, batch, num_kv_heads, table width and
- *                 block size only, with tokens = table width x block size and W = batch x
- *                 num_kv_heads workgroups; head_dim 128, INT8 cache: W <= CUs, and tokens <= 768,
+ *                 below instead (decided from head_dim, batch, num_kv_heads, group, table width
+ *                 and block size only, with tokens = table width x block size and W = batch x
+ *                 num_kv_heads x ceil(group / 16) workgroups; "head_dim" in these rules is
+ *                 head_dim rounded up to 64, 128 or 256; head_dim 128, INT8 cache: W <= CUs,
+ *                 and tokens <= 768,
  *                 or tokens <= 2048 with W >= (tiles per wave - 3) x CUs / 8, at most CUs / 2,
  *                 except with W <= CUs / 8, 3 or more tiles per wave and W x tiles >= CUs (then
  *                 the split layout below);
@@ -256,9 +261,13 @@ int int8kv_decode_plan(int query_dtype, int cache_dtype, int64_t batch, int32_t 
  *                 and each wave then holds at most 4 tiles of 32 tokens (2 at head_dim 64) of
  *                 the longest possible sequence (table width x block size).
  *
- * Supported sizes: head_dim 64, 128 or 256, block_size
- * a power of two in [16, 65536] (16 and 32 are vLLM's usual values), group = num_q_heads /
- * num_kv_heads in [1, 16].  Other sizes return INT8KV_E_SHAPE.
+ * Supported sizes: head_dim a multiple of 16 in [16, 256] (64, 128 and 256 run their own
+ * kernels; the others run the next of them with the elements past head_dim neither loaded into
+ * an output nor stored: 80, 96 and 112 on the 128-wide kernels, for example), block_size a
+ * power of two in [16, 65536] (16 and 32 are vLLM's usual values), any integer group =
+ * num_q_heads / num_kv_heads with num_kv_heads x ceil(group / 16) <= 65535 (a kv head's query
+ * heads are taken 16 at a time, one wave or workgroup per 16: multi-query attention with 64
+ * query heads runs 4 waves per kv head).  Other sizes return INT8KV_E_SHAPE.
  */
 int int8kv_paged_decode(const void* query, int query_dtype, int64_t batch, int32_t num_q_heads,
                         int32_t head_dim, const int64_t query_strides[3], const void* key_cache,

@@ -249,11 +249,24 @@ bool block_size_ok(int32_t block_size) {
   return block_size >= kRows && block_size <= kMaxBlock && (block_size & (block_size - 1)) == 0;
 }
 
+// head_dim: a multiple of 16 from 16 to 256 (the kernels run at 64, 128 or 256, padded_head_dim;
+// 16-byte K pieces and V columns of whole 16-element groups stay inside the cache row).  Any GQA
+// group: above 16 query heads per kv head the grid takes ceil(group / 16) column tiles of 16 per
+// kv head (col_tiles), up to 65535 grid heads.
 bool shape_ok(int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size) {
-  return num_kv_heads > 0 && num_q_heads > 0 && num_q_heads % num_kv_heads == 0 &&
-         num_q_heads / num_kv_heads <= kMaxGroup &&
-         (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
-         block_size_ok(block_size);
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads != 0) return false;
+  const int64_t tiles = (num_q_heads / num_kv_heads + kMaxGroup - 1) / kMaxGroup;
+  return (int64_t)num_kv_heads * tiles <= 65535 && head_dim >= 16 && head_dim <= 256 &&
+         head_dim % 16 == 0 && block_size_ok(block_size);
+}
+
+// MFMA column tiles of 16 query heads per kv head, and the grid's heads (kv heads x tiles).
+int32_t col_tiles(int32_t num_q_heads, int32_t num_kv_heads) {
+  return (num_q_heads / num_kv_heads + kMaxGroup - 1) / kMaxGroup;
+}
+
+int32_t grid_heads(int32_t num_q_heads, int32_t num_kv_heads) {
+  return num_kv_heads * col_tiles(num_q_heads, num_kv_heads);
 }
 
 }  // namespace
@@ -270,10 +283,11 @@ extern "C" size_t int8kv_decode_workspace_bytes(int32_t num_q_heads, int32_t num
       num_ranges > kMaxRangesLimit)
     return 0;
   if (num_ranges == 0)
-    num_ranges = auto_ranges(
-        kv_pair_shape(num_q_heads, num_kv_heads, head_dim) ? num_kv_heads / 2 : num_kv_heads,
-        cu_count());
-  return workspace_bytes(num_q_heads, num_ranges, head_dim);
+    num_ranges = auto_ranges(kv_pair_shape(num_q_heads, num_kv_heads, head_dim)
+                                 ? num_kv_heads / 2
+                                 : grid_heads(num_q_heads, num_kv_heads),
+                             cu_count());
+  return workspace_bytes(num_q_heads, num_ranges, padded_head_dim(head_dim));
 }
 
 // ------------------------------------------------------------------ no-allocation scratch
@@ -350,45 +364,54 @@ int plan_call(int query_dtype, int cache_dtype, int64_t batch, int32_t num_q_hea
     return INT8KV_E_DTYPE;
   if (batch < 0 || !shape_ok(num_q_heads, num_kv_heads, head_dim, block_size) ||
       num_blocks <= 0 || table_width <= 0 || table_width > 0x7fffffffLL || num_ranges < 0 ||
-      num_ranges > kMaxRangesLimit || min_tiles < 0 || batch > 0x7fffffffLL ||
-      num_kv_heads > 65535 || cus <= 0)
+      num_ranges > kMaxRangesLimit || min_tiles < 0 || batch > 0x7fffffffLL || cus <= 0)
     return INT8KV_E_SHAPE;
   const bool i8 = cache_dtype == INT8KV_I8;
   const int64_t ce = i8 ? 1 : 2;
   const bool automatic = num_ranges == 0 && min_tiles == 0;
   const bool auto_ranges_req = num_ranges == 0;
+  // The kernels run at hd (head_dim padded to 64, 128 or 256) over the grid heads hv (kv heads,
+  // times the column tiles of groups above 16 query heads).  Every layout rule below is stated
+  // for the kernels' shape; the padded instances keep one range per workgroup with two tiles in
+  // flight.
+  const int32_t hd = padded_head_dim(head_dim);
+  const bool pad = hd != head_dim;
+  const int32_t hv = grid_heads(num_q_heads, num_kv_heads);
   const bool kv_pair_ok = kv_pair_shape(num_q_heads, num_kv_heads, head_dim) &&
                           key_head_stride == head_dim && value_head_stride == head_dim;
-  const int32_t wave_heads = kv_pair_ok ? num_kv_heads / 2 : num_kv_heads;  // per range
+  const int32_t wave_heads = kv_pair_ok ? num_kv_heads / 2 : hv;  // per range
   if (num_ranges == 0) num_ranges = auto_ranges(wave_heads, cus);
   if (scratch_cap > 0 && auto_ranges_req) {
     // The partials of the automatic count may exceed the fixed scratch array (large GQA groups
     // or head_dim 256): take the most ranges it holds instead.
-    const size_t fit = scratch_cap / workspace_bytes(num_q_heads, 1, head_dim);
+    const size_t fit = scratch_cap / workspace_bytes(num_q_heads, 1, hd);
     if (fit < 1) return INT8KV_E_SCRATCH;
     if ((size_t)num_ranges > fit) num_ranges = (int32_t)fit;
   }
   if (min_tiles == 0) min_tiles = auto_min_tiles(batch, table_width, block_size, num_ranges);
   HostPlan p{};
   p.cus = cus;
+  p.hd = hd;
+  p.pad = pad;
+  p.grid_heads = hv;
+  p.col_tiles = col_tiles(num_q_heads, num_kv_heads);
   p.num_ranges = num_ranges;
   p.min_tiles = min_tiles;
-  p.need = workspace_bytes(num_q_heads, num_ranges, head_dim);
+  p.need = workspace_bytes(num_q_heads, num_ranges, hd);
   if (scratch_cap > 0 && p.need > scratch_cap) return INT8KV_E_SCRATCH;
   // (An empty batch launches nothing; the rules below divide by it.)
   p.group_mode = (flags & INT8KV_DECODE_PER_SEQUENCE) != 0 ||
                  (automatic && batch > 0 &&
-                  use_per_sequence(i8, head_dim, batch, num_kv_heads, table_width, block_size,
-                                   cus));
+                  use_per_sequence(i8, hd, batch, hv, table_width, block_size, cus));
   p.split = 0;
   if (batch > 0 && ((flags & INT8KV_DECODE_SPLIT_SEQUENCES) != 0 ||
                     (automatic && !p.group_mode &&
-                     use_split(head_dim, batch, num_kv_heads, table_width, block_size, cus)))) {
+                     use_split(hd, batch, hv, table_width, block_size, cus)))) {
     p.group_mode = true;
     // A caller's range count fixes the split count (num_ranges / batch workgroups per sequence
     // and kv head, e.g. the reference's num_splits); the automatic one fills the chip.
     p.split = auto_ranges_req
-                  ? split_count(batch, num_kv_heads, num_ranges, cus)
+                  ? split_count(batch, hv, num_ranges, cus)
                   : (int32_t)std::min<int64_t>(64, num_ranges / batch);
     if (p.split < 2) p.split = 0;
   }
@@ -405,14 +428,15 @@ int plan_call(int query_dtype, int cache_dtype, int64_t batch, int32_t num_q_hea
     const int64_t pair_min = (2LL * cus + wgs_y - 1) / wgs_y;
     const double units_max =
         (double)batch * (std::ceil((double)table_width * block_size / tile_tokens) + p.seq_cost);
-    const bool paired = i8 && head_dim <= 128 && num_ranges >= pair_min &&
+    const bool paired = i8 && hd <= 128 && !pad && num_ranges >= pair_min &&
                         units_max >= (double)pair_min * min_tiles &&
                         units_max >= (double)pair_min * kPairMinUnits;
     p.halves = paired ? 2 : 1;
     p.pair_min = paired ? (int32_t)pair_min : 0x7fffffff;
     // One wave per SIMD at most (every range's waves resident at once) and long ranges: INT8
     // waves keep four tiles in flight instead of two, the bytes in flight of two waves.
-    p.depth = i8 && !paired && head_dim <= 128 && (int64_t)num_ranges * wave_heads <= 4LL * cus &&
+    p.depth = i8 && !paired && hd <= 128 && !pad &&
+                      (int64_t)num_ranges * wave_heads <= 4LL * cus &&
                       units_max >= (double)kDeepMinUnits * num_ranges
                   ? 4
                   : 2;
@@ -543,15 +567,16 @@ int decode_entry(
   const int64_t recs = (int64_t)hp.num_ranges * 2 * num_q_heads;
   float* ws = static_cast<float*>(workspace);
   a.ws_acc = ws;
-  a.ws_m = ws + recs * head_dim;
-  a.ws_l = ws + recs * (head_dim + 1);
-  a.ws_cut = reinterpret_cast<int64_t*>(ws + recs * (head_dim + 2));
+  a.ws_m = ws + recs * hp.hd;
+  a.ws_l = ws + recs * (hp.hd + 1);
+  a.ws_cut = reinterpret_cast<int64_t*>(ws + recs * (hp.hd + 2));
   a.head_dim = head_dim;
   a.num_blocks = num_blocks;
   a.batch = batch;
-  a.num_kv_heads = num_kv_heads;
+  a.num_kv_heads = hp.grid_heads;
   a.num_q_heads = num_q_heads;
   a.group = num_q_heads / num_kv_heads;
+  a.col_tiles = hp.col_tiles;
   a.width = (int32_t)table_width;
   a.max_ranges = hp.num_ranges;
   a.min_tiles = hp.min_tiles;
@@ -574,11 +599,14 @@ int decode_entry(
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (cache_dtype) {
     case INT8KV_I8:
-      return launch_cache_int8(a, hp, query_dtype, flags, s);
+      return hp.pad ? launch_cache_int8_pad(a, hp, query_dtype, flags, s)
+                    : launch_cache_int8(a, hp, query_dtype, flags, s);
     case INT8KV_BF16:
-      return launch_cache_bf16(a, hp, query_dtype, flags, s);
+      return hp.pad ? launch_cache_bf16_pad(a, hp, query_dtype, flags, s)
+                    : launch_cache_bf16(a, hp, query_dtype, flags, s);
     default:
-      return launch_cache_fp16(a, hp, query_dtype, flags, s);
+      return hp.pad ? launch_cache_fp16_pad(a, hp, query_dtype, flags, s)
+                    : launch_cache_fp16(a, hp, query_dtype, flags, s);
   }
 }
 

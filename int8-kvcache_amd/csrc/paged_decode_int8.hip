@@ -1,5 +1,5 @@
-// The paged decode kernels for one cache type (int8), instantiated here so that the three
-// cache types compile in parallel (see paged_decode_kernels.h).
+// The paged decode kernels for one cache type (int8), instantiated here so that the cache types
+// compile in parallel (see paged_decode_kernels.h).
 
 #include "paged_decode_kernels.h"
 
@@ -7,7 +7,7 @@ namespace int8kv {
 
 int launch_cache_int8(const DecodeArgs& a, const HostPlan& hp, int query_dtype, uint32_t flags,
                       hipStream_t s) {
-  return launch_q<kI8>(a, hp, query_dtype, flags, s);
+  return launch_q<kI8, false>(a, hp, query_dtype, flags, s);
 }
 
 }  // namespace int8kv

@@ -51,9 +51,10 @@ struct DecodeArgs {
                        // paired packed), from which the merge finds the sequence's last range
   int64_t num_blocks;
   int64_t batch;
-  int32_t num_kv_heads;
+  int32_t num_kv_heads;  // heads of the grid: kv heads x col_tiles (see head_map)
   int32_t num_q_heads;
-  int32_t group;
+  int32_t group;        // query heads per kv head
+  int32_t col_tiles;    // MFMA column tiles of 16 query heads per kv head: ceil(group / 16)
   int32_t width;       // block-table width in blocks
   int32_t max_ranges;  // P upper bound (= grid.x of decode_kernel)
   int32_t min_tiles;   // P <= ceil(U / min_tiles)
@@ -69,13 +70,31 @@ struct DecodeArgs {
   int32_t halves;       // ranges per workgroup (1, or 2 with the paired layout)
   int32_t depth;        // tiles of K/V loads in flight per wave (2, or 4: INT8, one range per WG)
   int32_t group_mode;   // one workgroup per (sequence, kv head), states merged in LDS
-  int32_t head_dim;     // 64, 128 or 256
+  int32_t head_dim;     // the cache's head_dim: a multiple of 16, at most the kernels' HD
   int32_t scan32;       // a 64-sequence chunk's units fit 32 bits (see units_scan)
   int32_t cut_desc;     // write ws_cut (merge_by_range_kernel follows)
   int32_t kv_pair;      // head_dim 64: each wave takes kv heads 2k and 2k + 1 as one 128-wide head
   int32_t split;        // per-sequence layout over `split` workgroups per (sequence, kv head), whose
                         // records merge_split_kernel combines (0: one workgroup, no records)
 };
+
+// A grid head (a wave's or workgroup's "kv head") is one column tile of up to 16 query heads of
+// one kv head: grid head vh is kv head vh / col_tiles and its query heads q0 .. q0 + g - 1,
+// q0 = kv head x group + 16 (vh % col_tiles).  With at most 16 query heads per kv head (every
+// shape but the largest multi-query ones) it is the kv head itself.
+struct HeadMap {
+  int kv;  // kv head (cache head, its scales)
+  int q0;  // first query head
+  int g;   // query heads in this tile (the MFMA columns used)
+};
+
+__device__ __forceinline__ HeadMap head_map(const DecodeArgs& a, int vh) {
+  if (a.col_tiles == 1) return {vh, vh * a.group, a.group};
+  const int kv = vh / a.col_tiles;
+  const int t = vh - kv * a.col_tiles;
+  const int rest = a.group - 16 * t;
+  return {kv, kv * a.group + 16 * t, rest < 16 ? rest : 16};
+}
 
 // ------------------------------------------------------------------------ wave utilities
 __device__ __forceinline__ int64_t wave_sum(int64_t x) {
@@ -412,7 +431,10 @@ __device__ __forceinline__ constexpr int k_run(int run, int lg) {
   return HD > 128 ? run * (HD / 2) + lg * (HD / 8) : lg * (HD / 4);
 }
 
-template <int CACHE, int NB, bool NT, int HD>
+// PAD (head_dim D < HD): a lane's 16-byte pieces at or past element D read the row's first piece
+// instead, which keeps every access inside the row; their products meet query elements that are
+// zero, and the V columns at or past D feed output columns that are never stored.
+template <int CACHE, int NB, bool NT, int HD, bool PAD = false>
 __device__ __forceinline__ void issue_k(KTile<CACHE, NB, HD>& r, const char* kb,
                                         const TileRows<NB>& ph, const DecodeArgs& a, int li,
                                         int lg) {
@@ -424,22 +446,32 @@ __device__ __forceinline__ void issue_k(KTile<CACHE, NB, HD>& r, const char* kb,
     const char* row = kb + ph.id[s] * a.kc_sb + (ph.row[s] + li) * a.kc_ss;
 #pragma unroll
     for (int run = 0; run < kRuns; ++run) {
-      const u32x4* k4 = reinterpret_cast<const u32x4*>(row + k_run<HD>(run, lg) * E);
+      if constexpr (PAD) {
 #pragma unroll
-      for (int i = 0; i < PR; ++i) r.k[s][run * PR + i] = stream_load<CACHE, NT>(&k4[i]);
+        for (int i = 0; i < PR; ++i) {
+          const int e = k_run<HD>(run, lg) + i * (16 / E);
+          r.k[s][run * PR + i] = stream_load<CACHE, NT>(
+              reinterpret_cast<const u32x4*>(row + (e < a.head_dim ? e * E : 0)));
+        }
+      } else {
+        const u32x4* k4 = reinterpret_cast<const u32x4*>(row + k_run<HD>(run, lg) * E);
+#pragma unroll
+        for (int i = 0; i < PR; ++i) r.k[s][run * PR + i] = stream_load<CACHE, NT>(&k4[i]);
+      }
     }
   }
 }
 
-template <int CACHE, int NB, bool NT, int HD>
+template <int CACHE, int NB, bool NT, int HD, bool PAD = false>
 __device__ __forceinline__ void issue_v(VTile<CACHE, NB, HD>& r, const char* vb,
                                         const TileRows<NB>& ph, const DecodeArgs& a, int li,
                                         int lg) {
   constexpr int E = esize<CACHE>();
   constexpr int DW = v_dwords<CACHE, HD>();
+  const int vcol = PAD && HD / 16 * li >= a.head_dim ? 0 : li * (HD / 16 * E);
 #pragma unroll
   for (int s = 0; s < NB; ++s) {
-    const char* vp = vb + ph.id[s] * a.vc_sb + (ph.row[s] + 4 * lg) * a.vc_ss + li * (HD / 16 * E);
+    const char* vp = vb + ph.id[s] * a.vc_sb + (ph.row[s] + 4 * lg) * a.vc_ss + vcol;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const char* rp = vp + rr * a.vc_ss;
@@ -635,13 +667,15 @@ struct QueryRaw<kF32, HD> {
 //   head kvh G + li; its 64 elements go to the lanes of its own kv head's half (lg / 2 = 0 for
 //   li < G, 1 above) and the other half's lanes hold zeros, so each column's scores use only its
 //   own kv head's K elements.
-template <int QT, int HD, bool PAIR = false>
-__device__ __forceinline__ void issue_query(const DecodeArgs& a, int64_t b, int kvh, int li,
-                                            int lg, QueryRaw<QT, HD>& raw) {
+//   hm: the grid head's query heads (head_map).  PAD: elements at or past head_dim are zero.
+template <int QT, int HD, bool PAIR = false, bool PAD = false>
+__device__ __forceinline__ void issue_query(const DecodeArgs& a, int64_t b, const HeadMap& hm,
+                                            int li, int lg, QueryRaw<QT, HD>& raw) {
   constexpr int QE = esize<QT>();
   typedef typename std::remove_reference<decltype(raw.w[0])>::type Vec;
   constexpr int N = sizeof(raw.w) / sizeof(raw.w[0]);
   constexpr int kRuns = HD > 128 ? 2 : 1;
+  const int kvh = hm.kv;
   if constexpr (PAIR) {
     static_assert(HD == 128, "pairs of 64-wide kv heads");
     if (li < 2 * a.group && (lg >> 1) == (li >= a.group ? 1 : 0)) {
@@ -659,13 +693,31 @@ __device__ __forceinline__ void issue_query(const DecodeArgs& a, int64_t b, int 
   // from a row pointer plus k_run's offset instead, hipcc's allocation of the depth-2 INT8
   // kernel put a wait for the older loads before each V load of the tile loop (137 instead of
   // 100 s_waitcnt), which cost 0.3-0.45 us per call at B = 1 x 32768 and B = 8 x 4096.
-  if (kRuns == 1 && li < a.group) {
+  if constexpr (PAD) {
+    constexpr int VE = sizeof(Vec) / QE;  // elements per vector
+    if (li < hm.g) {
+      const char* qrow = a.q + ((int64_t)b * a.q_sb + (int64_t)(hm.q0 + li) * a.q_sh) * QE;
+#pragma unroll
+      for (int run = 0; run < kRuns; ++run)
+#pragma unroll
+        for (int i = 0; i < N / kRuns; ++i) {
+          const int e = k_run<HD>(run, lg) + i * VE;
+          raw.w[run * (N / kRuns) + i] =
+              e < a.head_dim ? *reinterpret_cast<const Vec*>(qrow + e * QE) : (Vec)(0);
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) raw.w[i] = (Vec)(0);
+    }
+    return;
+  }
+  if (kRuns == 1 && li < hm.g) {
     const Vec* qp = reinterpret_cast<const Vec*>(
-        a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh + HD / 4 * lg) * QE);
+        a.q + ((int64_t)b * a.q_sb + (int64_t)(hm.q0 + li) * a.q_sh + HD / 4 * lg) * QE);
 #pragma unroll
     for (int i = 0; i < N; ++i) raw.w[i] = qp[i];
-  } else if (li < a.group) {
-    const char* qrow = a.q + ((int64_t)b * a.q_sb + (int64_t)(kvh * a.group + li) * a.q_sh) * QE;
+  } else if (li < hm.g) {
+    const char* qrow = a.q + ((int64_t)b * a.q_sb + (int64_t)(hm.q0 + li) * a.q_sh) * QE;
 #pragma unroll
     for (int run = 0; run < kRuns; ++run) {
       const Vec* qp = reinterpret_cast<const Vec*>(qrow + k_run<HD>(run, lg) * QE);
@@ -799,19 +851,24 @@ __device__ __forceinline__ void stage_block_ids(const DecodeArgs& a, int32_t* id
   }
 }
 
-// Output rows of an empty sequence: zeros for the kv head's query heads (one wave).
-template <int QT, int HD>
-__device__ __forceinline__ void write_zero_rows(const DecodeArgs& a, int64_t b, int kvh, int lane) {
+// Output rows of an empty sequence: zeros for the grid head's query heads (one wave).  PAD: only
+// the columns below head_dim.  (The mask is compiled in only where it is needed: in the
+// depth-2 INT8 range kernels this runtime test alone made hipcc place a wait before each V load
+// of the tile loop, 139 s_waitcnt instead of 100.)
+template <int QT, int HD, bool PAD = false>
+__device__ __forceinline__ void write_zero_rows(const DecodeArgs& a, int64_t b, const HeadMap& hm,
+                                                int lane) {
   const int li = lane & 15;
   const int lg = lane >> 4;
-  if (li >= a.group) return;
-  char* op = a.out + (b * a.o_sb + (int64_t)(kvh * a.group + li) * a.o_sh) * esize<QT>();
+  if (li >= hm.g) return;
+  char* op = a.out + (b * a.o_sb + (int64_t)(hm.q0 + li) * a.o_sh) * esize<QT>();
   float z[HD / 16];
 #pragma unroll
   for (int i = 0; i < HD / 16; ++i) z[i] = 0.0f;
 #pragma unroll
   for (int rr = 0; rr < 4; ++rr)
-    store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), z);
+    if (!PAD || HD / 4 * lg + HD / 16 * rr < a.head_dim)
+      store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), z);
 }
 
 // Processes tiles [ta, tb) of sequence b (length L) for kv head kvh with one wave, then writes
@@ -819,17 +876,21 @@ __device__ __forceinline__ void write_zero_rows(const DecodeArgs& a, int64_t b, 
 // DEPTH: tiles of K/V loads kept in flight (register buffers).  GROUP: leave the state
 // (running max, sum, accumulators) in this wave's LDS slot (g_acc [HD/4][64], g_m, g_l [16])
 // for the workgroup to merge, instead of an output row or a partial record.
+// vh: the grid head (head_map); with PAIR the first kv head of the pair.  PAD: head_dim below HD
+// (issue_k); the output columns at or past head_dim are not stored.
 template <int CACHE, int QT, bool NT, bool QQ, int HD, int DEPTH, bool GROUP = false,
-          bool PAIR = false>
+          bool PAIR = false, bool PAD = false>
 __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, int64_t b,
-                                            int64_t L, int kvh, int64_t ta, int64_t tb,
+                                            int64_t L, int vh, int64_t ta, int64_t tb,
                                             bool full, int64_t rec, int lane,
                                             float* g_acc = nullptr, float* g_m = nullptr,
                                             float* g_l = nullptr) {
   typedef typename MfmaOp<CACHE>::T OpT;
   const int li = lane & 15;
   const int lg = lane >> 4;
-  const int G = a.group;
+  const HeadMap hm = head_map(a, vh);
+  const int kvh = hm.kv;
+  const int G = hm.g;
 
   f32x4 acc[HD / 16];
 #pragma unroll
@@ -877,8 +938,8 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       blocks_of(c0 + d < c1 ? c0 + d : c1 - 1, ph[d]);
-      issue_k<CACHE, NB, NT, HD>(kt[d], kb, ph[d], a, li, lg);
-      issue_v<CACHE, NB, NT, HD>(vt[d], vb, ph[d], a, li, lg);
+      issue_k<CACHE, NB, NT, HD, PAD>(kt[d], kb, ph[d], a, li, lg);
+      issue_v<CACHE, NB, NT, HD, PAD>(vt[d], vb, ph[d], a, li, lg);
     }
   };
 
@@ -893,7 +954,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   float s_scale;
   {
     QueryRaw<QT, HD> qraw;
-    issue_query<QT, HD, PAIR>(a, b, kvh, li, lg, qraw);
+    issue_query<QT, HD, PAIR, PAD>(a, b, hm, li, lg, qraw);
     chunk_prologue();
     s_scale = finish_query<CACHE, QT, QQ, HD, PAIR, GROUP>(a, qraw, kvh, qop, qlo, q8op);
   }
@@ -910,11 +971,11 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
                                            acc, m_run, l_part, valid, lg, s_scale, pop);
     if (refill) {
       blocks_of(t + d + DEPTH, ph[d]);
-      issue_k<CACHE, NB, NT, HD>(kt[d], kb, ph[d], a, li, lg);
+      issue_k<CACHE, NB, NT, HD, PAD>(kt[d], kb, ph[d], a, li, lg);
     }
     __builtin_amdgcn_sched_barrier(0);
     tile_pv<CACHE, NB, HD>(vt[d], pop, acc, valid, lg);
-    if (refill) issue_v<CACHE, NB, NT, HD>(vt[d], vb, ph[d], a, li, lg);
+    if (refill) issue_v<CACHE, NB, NT, HD, PAD>(vt[d], vb, ph[d], a, li, lg);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -1000,7 +1061,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     }
     return;
   }
-  const int h = kvh * G + li;
+  const int h = hm.q0 + li;
   if (full) {
     const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
     const float inv = l_part > 0.0f ? vscale / l_part : 0.0f;
@@ -1010,7 +1071,8 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
       float o[HD / 16];
 #pragma unroll
       for (int dt = 0; dt < HD / 16; ++dt) o[dt] = acc[dt][rr] * inv;
-      store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), o);
+      if (!PAD || HD / 4 * lg + HD / 16 * rr < a.head_dim)
+        store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), o);
     }
   } else {
     const int64_t row = rec * a.num_q_heads + h;
@@ -1042,7 +1104,8 @@ constexpr int decode_waves_per_eu() {
   return (DEPTH > 2 || CACHE != kI8 || HD > 128) ? 1 : 2;
 }
 
-template <int CACHE, int QT, bool NT, bool QQ, int HALVES, int HD, int DEPTH, bool PAIR = false>
+template <int CACHE, int QT, bool NT, bool QQ, int HALVES, int HD, int DEPTH, bool PAIR = false,
+          bool PAD = false>
 __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(decode_waves_per_eu<CACHE, DEPTH, HD>()))) void decode_kernel(DecodeArgs a) {
   __shared__ int32_t s_ids[HALVES * kMaxWavesPerWG][kChunkTiles * tile_blocks<CACHE>()];
   const int lane = threadIdx.x % kWave;
@@ -1093,10 +1156,10 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(de
         const int j = __builtin_ctzll(zmask);
         zmask &= zmask - 1;
         if constexpr (PAIR) {
-          write_zero_rows<QT, 64>(a, base + j, kv0, lane);
-          write_zero_rows<QT, 64>(a, base + j, kv0 + 1, lane);
+          write_zero_rows<QT, 64>(a, base + j, head_map(a, kv0), lane);
+          write_zero_rows<QT, 64>(a, base + j, head_map(a, kv0 + 1), lane);
         } else {
-          write_zero_rows<QT, HD>(a, base + j, kvh, lane);
+          write_zero_rows<QT, HD, PAD>(a, base + j, head_map(a, kvh), lane);
         }
       }
       // Sequences whose tiles (units past the start cost) meet [u0, u1).
@@ -1115,8 +1178,8 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(de
           a.ws_cut[4 * r] = base + j;
           a.ws_cut[4 * r + 1] = first + nb - 1;
         }
-        run_segment<CACHE, QT, NT, QQ, HD, DEPTH, false, PAIR>(a, s_ids[wave], base + j, Lb, kv0, ta,
-                                                               te, full, 2 * r + cut_slot(ta), lane);
+        run_segment<CACHE, QT, NT, QQ, HD, DEPTH, false, PAIR, PAD>(
+            a, s_ids[wave], base + j, Lb, kv0, ta, te, full, 2 * r + cut_slot(ta), lane);
       }
     }
     if (chunk_end >= u1 && !last_range) break;
@@ -1139,7 +1202,7 @@ constexpr int group_waves() {
   return HD > 128 ? 4 : 8;
 }
 
-template <int CACHE, int QT, bool QQ, int HD, bool SPLIT>
+template <int CACHE, int QT, bool QQ, int HD, bool SPLIT, bool PAD = false>
 __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves_per_eu(HD > 128 ? 1 : 2))) void group_kernel(DecodeArgs a) {
   constexpr int NW = group_waves<HD>();
   __shared__ int32_t s_ids[NW][kChunkTiles * tile_blocks<CACHE>()];
@@ -1150,17 +1213,18 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int li = lane & 15;
   const int lg = lane >> 4;
-  const int G = a.group;
   const int64_t b = blockIdx.x;
-  const int kvh = blockIdx.y;
+  const int vh = blockIdx.y;  // grid head (head_map)
+  const HeadMap hm = head_map(a, vh);
+  const int G = hm.g;
   const int64_t L = seq_len_of(a, b);
   const int64_t n = tiles_of(a, L);
   if (n == 0) {  // uniform over the workgroup: every wave leaves before the barrier
-    if (!SPLIT && wave == 0) write_zero_rows<QT, HD>(a, b, kvh, lane);
+    if (!SPLIT && wave == 0) write_zero_rows<QT, HD, PAD>(a, b, hm, lane);
     return;
   }
   // Loaded before the tile loop: after the barrier it would add a memory latency to every call.
-  const float vscale = (CACHE == kI8 && !SPLIT) ? fmaxf(a.v_scale[kvh], 1e-6f) : 1.0f;
+  const float vscale = (CACHE == kI8 && !SPLIT) ? fmaxf(a.v_scale[hm.kv], 1e-6f) : 1.0f;
   int64_t t0 = 0, span = n;  // this workgroup's tiles of the sequence
   if constexpr (SPLIT) {
     t0 = (int64_t)blockIdx.z * n / gridDim.z;
@@ -1169,8 +1233,8 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
   const int64_t ta = t0 + wave * span / NW;
   const int64_t tb = t0 + (wave + 1) * span / NW;
   if (ta < tb) {
-    run_segment<CACHE, QT, false, QQ, HD, 2, true>(a, s_ids[wave], b, L, kvh, ta, tb, false, 0,
-                                                   lane, s_acc[wave], s_m[wave], s_l[wave]);
+    run_segment<CACHE, QT, false, QQ, HD, 2, true, false, PAD>(
+        a, s_ids[wave], b, L, vh, ta, tb, false, 0, lane, s_acc[wave], s_m[wave], s_l[wave]);
   } else if (li < G) {  // no tiles for this wave: the neutral state
 #pragma unroll
     for (int j = 0; j < HD / 4; ++j) s_acc[wave][j * kWave + lane] = 0.0f;
@@ -1212,7 +1276,7 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
     }
   }
   if constexpr (SPLIT) {
-    const int64_t row = ((int64_t)b * gridDim.z + blockIdx.z) * a.num_q_heads + kvh * G + li;
+    const int64_t row = ((int64_t)b * gridDim.z + blockIdx.z) * a.num_q_heads + hm.q0 + li;
     store_n<kF32, HD / 16>(reinterpret_cast<char*>(a.ws_acc + row * HD) + (HD / 4 * lg + HD / 16 * rr) * 4, O);
     if (rr == 0 && lg == 0) {
       a.ws_m[row] = M;
@@ -1221,11 +1285,12 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
     return;
   }
   const float inv = Ls > 0.0f ? vscale / Ls : 0.0f;
-  char* op = a.out + (b * a.o_sb + (int64_t)(kvh * G + li) * a.o_sh) * esize<QT>();
+  char* op = a.out + (b * a.o_sb + (int64_t)(hm.q0 + li) * a.o_sh) * esize<QT>();
   float o[HD / 16];
 #pragma unroll
   for (int dt = 0; dt < HD / 16; ++dt) o[dt] = O[dt] * inv;
-  store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), o);
+  if (!PAD || HD / 4 * lg + HD / 16 * rr < a.head_dim)
+    store_n<QT, HD / 16>(op + (HD / 4 * lg + HD / 16 * rr) * esize<QT>(), o);
 }
 
 // Merge of the split per-sequence layout's records: a.split = Z <= 64 records per (sequence b =
@@ -1295,6 +1360,7 @@ __global__ __launch_bounds__(64) void merge_split_kernel(DecodeArgs a) {
     }
     inv = Lw > 0.0f ? vscale / Lw : 0.0f;
   }
+  if (D * lane >= a.head_dim) return;  // (head_dim below HD: the padded columns)
 #pragma unroll
   for (int j = 0; j < D; ++j) {
     const float v = O[j] * inv;
@@ -1404,7 +1470,8 @@ __device__ __forceinline__ void merge_records(const DecodeArgs& a, int64_t b, in
 #pragma unroll
   for (int k = 0; k < kStride; ++k) merge_in(M, L, O, s_m[k][c4], s_l[k][c4], s_o[k][c4]);
   const float inv = L > 0.0f ? vscale / L : 0.0f;
-  store4<QT>(a.out + (b * a.o_sb + (int64_t)h * a.o_sh + 4 * c4) * esize<QT>(), O * inv);
+  if (4 * c4 < a.head_dim)  // (head_dim below HD: the padded columns)
+    store4<QT>(a.out + (b * a.o_sb + (int64_t)h * a.o_sh + 4 * c4) * esize<QT>(), O * inv);
 }
 
 // The merge indexed by sequence: grid (batch, num_q_heads), MW waves per query head; workgroup
@@ -1509,41 +1576,47 @@ inline int waves_per_wg(int32_t num_kv_heads) {
   return 1;
 }
 
-template <int CACHE, int QT, bool NT, bool QQ, int HD, bool PAIR = false>
+template <int CACHE, int QT, bool NT, bool QQ, int HD, bool PAIR = false, bool PAD = false>
 inline void launch_main(const DecodeArgs& a, dim3 grid, int W, hipStream_t s) {
-  if constexpr (CACHE == kI8 && HD <= 128) {  // HD 256: one range per workgroup, two tiles
-    if (a.halves == 2) {
-      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 2, HD, 2, PAIR>), grid, dim3(2 * W * kWave), 0,
-                         s, a);
-      return;
+  if constexpr (PAD) {  // head_dim below HD: one range per workgroup, two tiles (the plan's)
+    hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 2, false, true>), grid,
+                       dim3(W * kWave), 0, s, a);
+  } else {
+    if constexpr (CACHE == kI8 && HD <= 128) {  // HD 256: one range per workgroup, two tiles
+      if (a.halves == 2) {
+        hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 2, HD, 2, PAIR>), grid,
+                           dim3(2 * W * kWave), 0, s, a);
+        return;
+      }
+      // Four tiles in flight leave no registers for an fp32 query's lo operands: two for those.
+      if (a.depth == 4 && QT != kF32) {
+        hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 4, PAIR>), grid,
+                           dim3(W * kWave), 0, s, a);
+        return;
+      }
     }
-    // Four tiles in flight leave no registers for an fp32 query's lo operands: two for those.
-    if (a.depth == 4 && QT != kF32) {
-      hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 4, PAIR>), grid, dim3(W * kWave), 0, s,
-                         a);
-      return;
-    }
+    hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 2, PAIR>), grid, dim3(W * kWave),
+                       0, s, a);
   }
-  hipLaunchKernelGGL((decode_kernel<CACHE, QT, NT, QQ, 1, HD, 2, PAIR>), grid, dim3(W * kWave), 0, s, a);
 }
 
 // The range decode kernel for one call: kv-head pairs at head_dim 64 run the HD = 128 kernel
 // with PAIR (see DecodeArgs::kv_pair).
-template <int CACHE, int QT, int HD, bool PAIR>
+template <int CACHE, int QT, int HD, bool PAIR, bool PAD>
 void launch_ranges(const DecodeArgs& a, dim3 grid, int W, bool nt, hipStream_t s) {
   constexpr int KH = PAIR ? 128 : HD;
   // INT8 caches: non-temporal loads for large pools, int8 scores for a quantised query.
   if constexpr (CACHE == kI8) {
     if (nt && a.quantize_q)
-      launch_main<CACHE, QT, true, true, KH, PAIR>(a, grid, W, s);
+      launch_main<CACHE, QT, true, true, KH, PAIR, PAD>(a, grid, W, s);
     else if (nt)
-      launch_main<CACHE, QT, true, false, KH, PAIR>(a, grid, W, s);
+      launch_main<CACHE, QT, true, false, KH, PAIR, PAD>(a, grid, W, s);
     else if (a.quantize_q)
-      launch_main<CACHE, QT, false, true, KH, PAIR>(a, grid, W, s);
+      launch_main<CACHE, QT, false, true, KH, PAIR, PAD>(a, grid, W, s);
     else
-      launch_main<CACHE, QT, false, false, KH, PAIR>(a, grid, W, s);
+      launch_main<CACHE, QT, false, false, KH, PAIR, PAD>(a, grid, W, s);
   } else {
-    launch_main<CACHE, QT, false, false, KH, PAIR>(a, grid, W, s);
+    launch_main<CACHE, QT, false, false, KH, PAIR, PAD>(a, grid, W, s);
   }
 }
 
@@ -1570,11 +1643,17 @@ struct HostPlan {
   int32_t merge_waves;  // waves per merge workgroup
   int32_t merge_fold;   // merge by sequence: records per lane slot and round
   int32_t launch_depth; // tiles in flight of the kernel instance that runs
+  int32_t hd;           // the kernels' head_dim (padded_head_dim)
+  bool pad;             // the cache's head_dim is below hd
+  int32_t grid_heads;   // kv heads x col_tiles
+  int32_t col_tiles;    // MFMA column tiles of 16 query heads per kv head
   int64_t cus;
   size_t need;          // workspace bytes
 };
 
-template <int CACHE, int QT, int HD>
+// PAD: head_dim below HD (the kernels' padded instances; the plan keeps them to one range per
+// workgroup with two tiles in flight and no kv-head pairs).
+template <int CACHE, int QT, int HD, bool PAD>
 int launch(const DecodeArgs& a, const HostPlan& hp, uint32_t flags, hipStream_t s) {
   const bool nt = hp.nt;
   const int32_t hv = a.kv_pair ? a.num_kv_heads / 2 : a.num_kv_heads;  // kv heads (pairs) per range
@@ -1585,14 +1664,15 @@ int launch(const DecodeArgs& a, const HostPlan& hp, uint32_t flags, hipStream_t 
       const dim3 block(group_waves<HD>() * kWave);
       if (a.split > 0) {
         if (a.quantize_q)
-          hipLaunchKernelGGL((group_kernel<CACHE, QT, true, HD, true>), grid, block, 0, s, a);
+          hipLaunchKernelGGL((group_kernel<CACHE, QT, true, HD, true, PAD>), grid, block, 0, s, a);
         else
-          hipLaunchKernelGGL((group_kernel<CACHE, QT, false, HD, true>), grid, block, 0, s, a);
+          hipLaunchKernelGGL((group_kernel<CACHE, QT, false, HD, true, PAD>), grid, block, 0, s, a);
       } else {
         if (a.quantize_q)
-          hipLaunchKernelGGL((group_kernel<CACHE, QT, true, HD, false>), grid, block, 0, s, a);
+          hipLaunchKernelGGL((group_kernel<CACHE, QT, true, HD, false, PAD>), grid, block, 0, s, a);
         else
-          hipLaunchKernelGGL((group_kernel<CACHE, QT, false, HD, false>), grid, block, 0, s, a);
+          hipLaunchKernelGGL((group_kernel<CACHE, QT, false, HD, false, PAD>), grid, block, 0, s,
+                             a);
       }
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return (int)e;
@@ -1607,13 +1687,13 @@ int launch(const DecodeArgs& a, const HostPlan& hp, uint32_t flags, hipStream_t 
   }
   if (flags & INT8KV_DECODE_MAIN) {
     dim3 grid((unsigned)((a.max_ranges + a.halves - 1) / a.halves), (unsigned)(hv / W));
-    if constexpr (HD == 64) {
+    if constexpr (HD == 64 && !PAD) {
       if (a.kv_pair)
-        launch_ranges<CACHE, QT, HD, true>(a, grid, W, nt, s);
+        launch_ranges<CACHE, QT, HD, true, false>(a, grid, W, nt, s);
       else
-        launch_ranges<CACHE, QT, HD, false>(a, grid, W, nt, s);
+        launch_ranges<CACHE, QT, HD, false, false>(a, grid, W, nt, s);
     } else {
-      launch_ranges<CACHE, QT, HD, false>(a, grid, W, nt, s);
+      launch_ranges<CACHE, QT, HD, false, PAD>(a, grid, W, nt, s);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
@@ -1648,33 +1728,46 @@ int launch(const DecodeArgs& a, const HostPlan& hp, uint32_t flags, hipStream_t 
   return INT8KV_OK;
 }
 
-template <int CACHE>
+// The kernels' head_dim (HD) for a cache head_dim: the power of two 64, 128 or 256 at or above
+// it; below it the padded instances run (elements at or past head_dim are never loaded into
+// products that reach an output, nor stored).
+inline int padded_head_dim(int head_dim) { return head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256; }
+
+template <int CACHE, bool PAD>
 int launch_q(const DecodeArgs& a, const HostPlan& hp, int query_dtype, uint32_t flags,
              hipStream_t s) {
+  const int hd = padded_head_dim(a.head_dim);
   switch (query_dtype) {
     case INT8KV_F32:
-      return a.head_dim == 64    ? launch<CACHE, kF32, 64>(a, hp, flags, s)
-             : a.head_dim == 128 ? launch<CACHE, kF32, 128>(a, hp, flags, s)
-                                 : launch<CACHE, kF32, 256>(a, hp, flags, s);
+      return hd == 64    ? launch<CACHE, kF32, 64, PAD>(a, hp, flags, s)
+             : hd == 128 ? launch<CACHE, kF32, 128, PAD>(a, hp, flags, s)
+                         : launch<CACHE, kF32, 256, PAD>(a, hp, flags, s);
     case INT8KV_F16:
-      return a.head_dim == 64    ? launch<CACHE, kF16, 64>(a, hp, flags, s)
-             : a.head_dim == 128 ? launch<CACHE, kF16, 128>(a, hp, flags, s)
-                                 : launch<CACHE, kF16, 256>(a, hp, flags, s);
+      return hd == 64    ? launch<CACHE, kF16, 64, PAD>(a, hp, flags, s)
+             : hd == 128 ? launch<CACHE, kF16, 128, PAD>(a, hp, flags, s)
+                         : launch<CACHE, kF16, 256, PAD>(a, hp, flags, s);
     default:
-      return a.head_dim == 64    ? launch<CACHE, kBF16, 64>(a, hp, flags, s)
-             : a.head_dim == 128 ? launch<CACHE, kBF16, 128>(a, hp, flags, s)
-                                 : launch<CACHE, kBF16, 256>(a, hp, flags, s);
+      return hd == 64    ? launch<CACHE, kBF16, 64, PAD>(a, hp, flags, s)
+             : hd == 128 ? launch<CACHE, kBF16, 128, PAD>(a, hp, flags, s)
+                         : launch<CACHE, kBF16, 256, PAD>(a, hp, flags, s);
   }
 }
 
 
-// One cache type's launcher (defined in paged_decode_<type>.hip).
+// One cache type's launcher (defined in paged_decode_<type>.hip), and the one for head_dims
+// below the kernels' HD (paged_decode_<type>_pad.hip).
 int launch_cache_int8(const DecodeArgs& a, const HostPlan& hp, int query_dtype, uint32_t flags,
                       hipStream_t s);
 int launch_cache_bf16(const DecodeArgs& a, const HostPlan& hp, int query_dtype, uint32_t flags,
                       hipStream_t s);
 int launch_cache_fp16(const DecodeArgs& a, const HostPlan& hp, int query_dtype, uint32_t flags,
                       hipStream_t s);
+int launch_cache_int8_pad(const DecodeArgs& a, const HostPlan& hp, int query_dtype,
+                          uint32_t flags, hipStream_t s);
+int launch_cache_bf16_pad(const DecodeArgs& a, const HostPlan& hp, int query_dtype,
+                          uint32_t flags, hipStream_t s);
+int launch_cache_fp16_pad(const DecodeArgs& a, const HostPlan& hp, int query_dtype,
+                          uint32_t flags, hipStream_t s);
 
 }  // namespace int8kv
 

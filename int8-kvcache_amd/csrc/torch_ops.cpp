@@ -168,6 +168,13 @@ void require_same_device(std::initializer_list<const at::Tensor*> ts, const at::
     require(t->device() == first.device(), "all tensors must be on one device (the GPU)");
 }
 
+// head_dims the decode kernels run (the reference pads any head_dim to a power of two under a
+// mask, src/triton_ops/int8_paged_attention.py:556-558,588-589; other sizes fail here, before
+// the C ABI, with the reference's AssertionError).
+bool head_dim_ok(int64_t d) { return d >= 16 && d <= 256 && d % 16 == 0; }
+const char* const kHeadDimText =
+    "head_dim must be a multiple of 16 from 16 to 256 (this build's decode kernels)";
+
 // src/triton_ops/int8_paged_attention.py:683-769 (validation :698-719, impl :767-768).
 at::Tensor int8_paged_attention(const at::Tensor& query, const at::Tensor& key_cache,
                                 const at::Tensor& value_cache, const at::Tensor& block_tables,
@@ -184,6 +191,7 @@ at::Tensor int8_paged_attention(const at::Tensor& query, const at::Tensor& key_c
   require(value_cache.sizes() == key_cache.sizes());
   require(Hkv > 0, "key_cache has no kv heads");
   require(key_cache.size(3) == D && Hq % Hkv == 0);
+  require(head_dim_ok(D), kHeadDimText);
   require(block_tables.size(0) == B && seq_lens.numel() == B);
   require(k_scale.dim() == 1 && v_scale.dim() == 1);
   require(k_scale.numel() == Hkv && v_scale.numel() == Hkv);
@@ -216,6 +224,7 @@ at::Tensor bf16_paged_attention(const at::Tensor& query, const at::Tensor& key_c
   require(value_cache.sizes() == key_cache.sizes());
   require(key_cache.size(2) > 0, "key_cache has no kv heads");
   require(key_cache.size(3) == D && Hq % key_cache.size(2) == 0);
+  require(head_dim_ok(D), kHeadDimText);
   require(block_tables.size(0) == B && seq_lens.numel() == B);
   require(key_cache.stride(-1) == 1 && value_cache.stride(-1) == 1);
   require(query.is_cuda(), "bf16_paged_attention needs GPU tensors");

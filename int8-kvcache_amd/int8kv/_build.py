@@ -19,10 +19,12 @@ CSRC_DIR = PKG_DIR.parent / "csrc"
 INCLUDE_DIR = PKG_DIR.parent.parent / "include"
 LIB_PATH = PKG_DIR / "libint8kv.so"
 
-# The paged decode's kernels compile per cache type in parallel (paged_decode_<type>.hip, from
+# The paged decode's kernels compile per cache type in parallel (paged_decode_<type>.hip and, for
+# head_dims below the kernels' 64 / 128 / 256, paged_decode_<type>_pad.hip, from
 # paged_decode_kernels.h); paged_decode.hip is its host side.
 SOURCES = ["cache_write.hip", "paged_decode.hip", "paged_decode_int8.hip", "paged_decode_bf16.hip",
-           "paged_decode_fp16.hip", "decode_loop_ops.hip"]
+           "paged_decode_fp16.hip", "paged_decode_int8_pad.hip", "paged_decode_bf16_pad.hip",
+           "paged_decode_fp16_pad.hip", "decode_loop_ops.hip"]
 # The torch extension over the C ABI (host code only; torch headers, linked to libint8kv.so).
 EXT_SOURCE = "torch_ops.cpp"
 EXT_NAME = "_int8kv_torch"

@@ -12,6 +12,14 @@ from . import _ext, _lib
 
 QUERY_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
+# head_dims the decode kernels run: multiples of 16 up to 256 (the reference pads any head_dim to a
+# power of two under a mask, src/triton_ops/int8_paged_attention.py:556-558,588-589).
+HEAD_DIM_TEXT = "head_dim must be a multiple of 16 from 16 to 256 (this build's decode kernels)"
+
+
+def head_dim_ok(d: int) -> bool:
+    return 16 <= d <= 256 and d % 16 == 0
+
 # When set, the op also runs the reference's host-synchronising input checks
 # (src/triton_ops/int8_paged_attention.py:720-723) and checks block ids; off by default because
 # each check is a device-to-host copy.

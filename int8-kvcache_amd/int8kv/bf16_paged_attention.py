@@ -40,6 +40,7 @@ def bf16_paged_attention(
     num_blocks, block_size, Hkv, cache_D = key_cache.shape
     assert value_cache.shape == key_cache.shape
     assert cache_D == D and Hq % Hkv == 0
+    assert _decode.head_dim_ok(D), _decode.HEAD_DIM_TEXT
     assert block_tables.shape[0] == B and seq_lens.numel() == B
     assert key_cache.stride(-1) == 1 and value_cache.stride(-1) == 1
     dev = query.device

@@ -4,8 +4,10 @@ The reference's callers import the operators from ``src.triton_ops.*``
 (vllm_int8/vllm_shadow_cache_patch.py:5, vllm_int8/vllm_int8_cache_ops.py:281,
 vllm_int8/vllm_int8_attention_patch.py:8-10, vllm_int8/vllm_int8_attention_backend.py:10-12).
 ``install_reference_aliases()`` registers this package's modules under those names in
-``sys.modules`` so those imports bind to the HIP operators without editing the callers.  Only the
-operator modules are aliased; the reference's pure-torch checking helpers are not provided.
+``sys.modules`` so those imports bind to the HIP operators without editing the callers.  The
+aliased operator modules also export the reference's two pure-torch checkers under their names
+(``torch_int8_kv_cache_write_reference`` and ``torch_int8_paged_attention_reference``, from
+``int8kv.torch_reference``), for callers' own tests; no operator calls them.
 """
 
 from __future__ import annotations

@@ -64,6 +64,7 @@ def int8_paged_attention(
     num_blocks, block_size, Hkv, cache_D = key_cache.shape
     assert value_cache.shape == key_cache.shape
     assert cache_D == D and Hq % Hkv == 0
+    assert _decode.head_dim_ok(D), _decode.HEAD_DIM_TEXT
     assert block_tables.shape[0] == B and seq_lens.numel() == B
     assert k_scale.ndim == 1 and v_scale.ndim == 1
     assert k_scale.numel() == Hkv and v_scale.numel() == Hkv

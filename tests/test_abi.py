@@ -64,8 +64,11 @@ def test_workspace_bytes(lib):
     assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 512) == 512 * per_range(28, 128)
     assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 1) == per_range(28, 128)
     assert per_range(28, 128) % 16 == 0 and per_range(7, 64) % 16 == 0
+    # head_dims below 64, 128 or 256 keep records of that width
+    for d, hd in ((16, 64), (32, 64), (96, 128), (80, 128), (192, 256)):
+        assert lib.int8kv_decode_workspace_bytes(28, 4, d, 16, 9) == 9 * per_range(28, hd)
     # unsupported sizes -> 0
-    for d in (32, 96, 192, 512):  # head_dim: 64, 128 or 256
+    for d in (0, 8, 24, 72, 272, 512):  # head_dim: a multiple of 16 in [16, 256]
         assert lib.int8kv_decode_workspace_bytes(28, 4, d, 16, 0) == 0
     assert lib.int8kv_decode_workspace_bytes(16, 8, 256, 16, 5) == 5 * per_range(16, 256)
     assert lib.int8kv_decode_workspace_bytes(28, 4, 64, 16, 3) == 3 * per_range(28, 64)
@@ -73,7 +76,10 @@ def test_workspace_bytes(lib):
         assert lib.int8kv_decode_workspace_bytes(28, 4, 128, bs, 0) == 0
     for bs in (16, 32, 64, 1 << 16):  # the partials do not depend on the block size
         assert lib.int8kv_decode_workspace_bytes(28, 4, 128, bs, 7) == 7 * per_range(28, 128)
-    assert lib.int8kv_decode_workspace_bytes(34, 2, 128, 16, 0) == 0  # group 17
+    assert lib.int8kv_decode_workspace_bytes(30, 4, 128, 16, 0) == 0  # not a whole group
+    # group 17: two column tiles per kv head, the automatic count of 4 grid heads
+    assert lib.int8kv_decode_workspace_bytes(34, 2, 128, 16, 0) == \
+        lib.int8kv_decode_auto_ranges(4) * per_range(34, 128)
     assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, -1) == 0
     assert lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, (1 << 20) + 1) == 0
     # automatic: a few workgroups per compute unit (no GPU here: the library assumes 256 CUs)
@@ -102,7 +108,8 @@ def test_decode_rejects_bad_arguments_without_launching(lib):
     assert _decode_call(lib, query_dtype=3) == -2
     assert _decode_call(lib, cache_dtype=4) == -2
     assert _decode_call(lib, table_dtype=2) == -2
-    assert _decode_call(lib, head_dim=96) == -3
+    assert _decode_call(lib, head_dim=72) == -3
+    assert _decode_call(lib, head_dim=272) == -3
     assert _decode_call(lib, block_size=8) == -3
     assert _decode_call(lib, block_size=48) == -3
     assert _decode_call(lib, num_q_heads=30) == -3
@@ -142,7 +149,7 @@ def test_noalloc_decode_rejects_without_touching_the_device(lib):
     too_many = limit // per_range + 1
     assert call(ranges=too_many) == -6
     assert call(ranges=too_many, num_q_heads=56) == -6
-    assert call(query_dtype=3) == -2 and call(head_dim=96) == -3 and call(query=None) == -1
+    assert call(query_dtype=3) == -2 and call(head_dim=72) == -3 and call(query=None) == -1
     assert call(query=24) == -4
     assert call(batch=0) == 0
 

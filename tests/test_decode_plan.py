@@ -283,13 +283,58 @@ def test_noalloc_lowers_the_automatic_range_count():
     assert plan(batch=64, width=2048, ranges=too_many)["num_ranges"] == too_many
 
 
+# ------------------------------------------------------------------ widened shapes
+def _per_range(hq, d):
+    return 2 * hq * (d + 2) * 4 + 32
+
+
+@pytest.mark.parametrize("d, hd", [(16, 64), (48, 64), (80, 128), (96, 128), (112, 128),
+                                   (160, 256), (192, 256), (240, 256)])
+def test_padded_head_dims(d, hd):
+    """A head_dim below 64, 128 or 256 runs the next of those kernels: its records are that wide,
+    the layout rules are those of the padded width, and the range layout keeps one range per
+    workgroup with two tiles in flight (no pairs, no four-deep pipeline, no kv-head pairs)."""
+    for kw in (dict(batch=64, width=2048), dict(batch=64, width=2048, ranges=512),
+               dict(batch=64, width=252)):
+        p = plan(d=d, **kw)
+        ref = plan(d=hd, head_stride=hd + 16, **kw)  # (no kv-head pairs at 64)
+        assert p["layout"] == ref["layout"] == "ranges"
+        assert p["num_ranges"] == ref["num_ranges"]
+        assert p["workspace_bytes"] == p["num_ranges"] * _per_range(28, hd)
+        assert (p["ranges_per_workgroup"], p["depth"], p["kv_pair"]) == (1, 2, 0)
+    for kw in (dict(batch=4, width=32), dict(batch=1, width=2048), dict(batch=64, width=16)):
+        assert layout(d=d, **kw) == layout(d=hd, **kw)
+    assert plan(d=d, hq=32, hkv=8, batch=64, width=2048)["kv_pair"] == 0
+
+
+def test_groups_above_16_take_column_tiles():
+    """More than 16 query heads per kv head: ceil(group / 16) waves per kv head, so the range
+    count, the per-sequence and split rules and the workspace are those of kv heads x tiles."""
+    for hq, hkv, tiles in ((34, 2, 2), (64, 1, 4), (71, 1, 5), (48, 2, 3), (128, 8, 1 * 8)):
+        t = -(-(hq // hkv) // 16)
+        grid = hkv * t
+        for kw in (dict(batch=64, width=2048), dict(batch=2, width=32), dict(batch=1, width=4096)):
+            p = plan(hq=hq, hkv=hkv, **kw)
+            # the kv-head count with the same grid heads and group <= 16 takes the same layout
+            ref = plan(hq=grid, hkv=grid, **kw)
+            assert p["layout"] == ref["layout"], (hq, hkv, kw)
+            assert p["num_ranges"] == ref["num_ranges"]
+            assert p["workspace_bytes"] == p["num_ranges"] * _per_range(hq, 128)
+    # MQA with 64 query heads: 4 grid heads, the automatic count of 4 kv heads
+    assert plan(hq=64, hkv=1, batch=64, width=2048)["num_ranges"] == \
+        plan(hq=28, hkv=4, batch=64, width=2048)["num_ranges"]
+
+
 def test_plan_rejects_what_the_decode_rejects():
-    with pytest.raises(_lib.Int8KVError, match="E_SHAPE"):
-        plan(d=96)
+    for d in (8, 72, 100, 272, 512):  # head_dim: a multiple of 16 in [16, 256]
+        with pytest.raises(_lib.Int8KVError, match="E_SHAPE"):
+            plan(d=d)
     with pytest.raises(_lib.Int8KVError, match="E_SHAPE"):
         plan(bs=8)
     with pytest.raises(_lib.Int8KVError, match="E_SHAPE"):
-        plan(hq=34, hkv=2)  # group 17
+        plan(hq=30, hkv=4)  # not a whole group
+    with pytest.raises(_lib.Int8KVError, match="E_SHAPE"):
+        plan(hq=65535 * 17, hkv=65535)  # 131070 grid heads
     with pytest.raises(_lib.Int8KVError, match="E_SHAPE"):
         plan(cus=-1)
     with pytest.raises(_lib.Int8KVError, match="E_DTYPE"):

@@ -552,13 +552,30 @@ def test_head_dim_64_paired_regime(cuda):
 
 
 def test_unsupported_head_dims_raise(cuda):
+    """head_dims the kernels do not run (not a multiple of 16, or above 256) fail before the C ABI
+    with an AssertionError naming the supported set, on both operators and both host paths; the
+    C ABI itself returns INT8KV_E_SHAPE."""
+    from int8kv import _decode, _ext
+
     c = decode_case([40], seed=3)
     q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
-    for d in (32, 96, 192, 512):  # 64, 128 and 256 are supported
+    for d in (8, 72, 200, 272, 512):
         kx = torch.zeros(kc.shape[0], 16, 4, d, dtype=torch.int8, device=cuda)
         qx = torch.zeros(q.shape[0], q.shape[1], d, dtype=q.dtype, device=cuda)
+        for debug in (False, True):  # the extension, then the ctypes path
+            old = _decode.DEBUG_CHECKS
+            _decode.DEBUG_CHECKS = debug
+            try:
+                with pytest.raises(AssertionError, match="multiple of 16"):
+                    int8kv.int8_paged_attention(qx, kx, kx.clone(), bt, sl, ks, vs)
+                with pytest.raises(AssertionError, match="multiple of 16"):
+                    int8kv.bf16_paged_attention(qx, kx.bfloat16(), kx.bfloat16(), bt, sl)
+            finally:
+                _decode.DEBUG_CHECKS = old
+        out = torch.empty_like(qx)
         with pytest.raises(RuntimeError, match="E_SHAPE"):
-            int8kv.int8_paged_attention(qx, kx, kx.clone(), bt, sl, ks, vs)
+            _decode.paged_decode(qx, kx, kx.clone(), bt, sl, ks, vs, out)
+    assert _ext.module() is not None
 
 
 def _group(q, kc, vc, bt, sl, ks, vs, extra_flags=0):

@@ -5,7 +5,7 @@ same plan, partials in the library's fixed scratch array instead).  Two calls in
 same GPU, the second with a smaller input, both bit-identical to the workspace entry point and
 within the oracle bar; then the INT8 x BF16-cache and forced-range variants, the merge indexed by
 range, head_dim 256, head_dim 64 (kv-head pairs, per-sequence layout) and the split
-per-sequence layout.
+per-sequence layout, a padded head_dim and a group above 16.
 """
 
 from __future__ import annotations
@@ -138,6 +138,24 @@ def test_large_group_fits_the_scratch_with_fewer_ranges(cuda):
     assert torch.equal(got, want)
     err, cos, _ = metrics(got.float().cpu().numpy(), oracle_int8(c))
     assert err <= MAX_ABS and cos >= MIN_COS, (err, cos)
+
+
+def test_padded_head_dim_and_groups_above_16(cuda):
+    """A head_dim of 80 (records of the 128-wide kernels in the scratch array), then a smaller
+    call with 71 query heads on one kv head (five column tiles of the same kv head)."""
+    for lens, seed, hq, hkv, d, what in (
+            ([5000, 1, 3000, 0, 4100, 77, 900, 2600], 42, 16, 2, 80, "head_dim 80, group 8"),
+            ([700, 3, 1500], 43, 71, 1, 64, "71 query heads, one kv head")):
+        print(f"noalloc: {what}", flush=True)
+        case = decode_case(lens, seed=seed, hq=hq, hkv=hkv, head_dim=d, extra_blocks=3)
+        q, kc, vc, bt, sl, ks, vs = to_dev(case, cuda)
+        for ranges in (0, 2 * len(lens)):
+            want = _with_workspace(q, kc, vc, bt, sl, ks, vs, ranges)
+            got = _noalloc(q, kc, vc, bt, sl, ks, vs, torch.full_like(q, float("nan")), ranges)
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), f"{what}, ranges={ranges}"
+        err, cos, _ = metrics(got.float().cpu().numpy(), oracle_int8(case))
+        assert err <= MAX_ABS and cos >= MIN_COS, (what, err, cos)
 
 
 def test_oversized_request_is_refused(cuda):
