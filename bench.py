@@ -718,6 +718,88 @@ def cold_legs(dev, out_path: str | None) -> dict:
     return res
 
 
+def ceiling_legs(dev, out_path: str | None) -> dict:
+    """Read ceilings of the INT8 decode's K/V stream on this GPU (include/int8kv_probe.h), next to
+    the decode itself, all on one 1 GiB shuffled pool (65,536 INT8 blocks of 16 tokens x 4 kv
+    heads x 128 for K and as many for V, 256 ranges x 128 tiles): a plain streaming read of the
+    pool (ordinary and non-temporal loads), the decode's own per-lane K/V loads without its
+    arithmetic (ordinary and non-temporal), and the INT8 decode kernel over the same blocks
+    (64 sequences of 16,384 tokens, its automatic plan: the range layout, non-temporal loads).
+    Event-timed back-to-back launches; TB/s of the pool's bytes (the decode: its algorithmic
+    bytes)."""
+    import torch
+
+    import int8kv
+    from int8kv import _decode, _lib, roofline
+
+    lib = _lib.load()
+    R, T = 256, 128                      # ranges, tiles per range
+    NB = R * T * 2                       # 16-token blocks
+    pool = torch.empty(2, NB, 16, 4, 128, dtype=torch.int8, device=dev)
+    g = torch.Generator(device=dev).manual_seed(5)
+    pool.view(-1).copy_(torch.randint(-127, 128, (pool.numel(),), generator=g, device=dev,
+                                      dtype=torch.int8))
+    kc, vc = pool[0], pool[1]
+    perm = torch.randperm(NB, generator=torch.Generator().manual_seed(6)).to(torch.int32)
+    ids = perm.to(dev)
+    nbytes = pool.numel()
+    stream = _lib.stream_handle(dev)
+    sink = torch.empty(1 << 20, dtype=torch.int32, device=dev)
+    res = {"pool_bytes": nbytes, "ranges": R, "tiles_per_range": T}
+
+    def probe_stream(nt):
+        def fn():
+            _lib.check(lib.int8kv_probe_stream_read(pool.data_ptr(), nbytes, nt, sink.data_ptr(),
+                                                    256 * 8 * 256, stream), "probe_stream_read")
+        return fn
+
+    def probe_decode(nt):
+        def fn():
+            _lib.check(lib.int8kv_probe_decode_loads(kc.data_ptr(), vc.data_ptr(), NB, 4,
+                                                     ids.data_ptr(), ids.numel(), R, T, nt,
+                                                     sink.data_ptr(), sink.numel(), stream),
+                       "probe_decode_loads")
+        return fn
+
+    for name, fn in (("stream_read", probe_stream(0)), ("stream_read_nt", probe_stream(1)),
+                     ("decode_loads", probe_decode(0)), ("decode_loads_nt", probe_decode(1))):
+        settle(fn, batch=5, min_ms=30.0)
+        ms = time_events(fn, 20, 5)
+        res[name + "_us"] = round(ms * 1e3, 2)
+        res[name + "_TBps"] = round(nbytes / ms / 1e9, 3)
+        log(f"ceiling: {name}: {ms * 1e3:.2f} us, {nbytes / ms / 1e9:.3f} TB/s")
+    # The decode over the same blocks: 64 sequences of 16,384 tokens, sequence b owning blocks
+    # perm[1024 b .. 1024 b + 1023] of the K and V pools (every block once, as in the probes).
+    B, L = 64, 16384
+    bt = ids[: B * (L // 16)].view(B, L // 16).contiguous()
+    sl = torch.full((B,), L, dtype=torch.int32, device=dev)
+    q = torch.randn(B, 28, 128, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16).to(dev)
+    ks = torch.full((4,), 0.02, device=dev)
+    vs = torch.full((4,), 0.02, device=dev)
+    out = torch.empty_like(q)
+    ws = torch.empty(lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 0), dtype=torch.uint8,
+                     device=dev)
+    dbytes = roofline.decode_bytes(sl.cpu().numpy(), 4, 128, 1, B, 28)
+    plan = _lib.decode_plan(q.dtype, kc.dtype, B, 28, 4, 128, NB, 16, L // 16)
+    for name, flags in (("decode_kernel", _lib.DECODE_MAIN), ("decode_op", _lib.DECODE_ALL)):
+        fn = lambda flags=flags: _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, out, 0, flags, ws)
+        settle(fn, batch=5, min_ms=30.0)
+        ms = time_events(fn, 20, 5)
+        res[name + "_us"] = round(ms * 1e3, 2)
+        res[name + "_TBps"] = round(dbytes / ms / 1e9, 3)
+        log(f"ceiling: {name} (B={B} x {L}, {plan['layout']}, nt={plan['non_temporal']}): "
+            f"{ms * 1e3:.2f} us, {dbytes / ms / 1e9:.3f} TB/s")
+    res["decode_bytes"] = dbytes
+    res["decode_plan"] = plan
+    res["decode_kernel_of_pattern_ceiling"] = round(res["decode_kernel_TBps"] / res["decode_loads_nt_TBps"], 3)
+    del pool
+    torch.cuda.empty_cache()
+    if out_path:
+        Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+        Path(out_path).write_text(json.dumps({"ceiling": res}, indent=1))
+    return res
+
+
 def counter_run(dev, mode: str) -> None:
     """Eager calls for a rocprofv3 counter pass (the profiler serialises counted dispatches, so
     graphs are not used): "warm" = 40 calls on one layer pool; "cold" = 2 x 28 layers of (the
@@ -846,6 +928,8 @@ def main() -> int:
     ap.add_argument("--cold", metavar="JSON", default=None,
                     help="only config 4's per-layer decode call with warm and cold caches (28 "
                          "layer pools rotated, and between the decode step's GEMMs), results to JSON")
+    ap.add_argument("--ceiling", metavar="JSON", default=None,
+                    help="only the read-ceiling probes of the decode's K/V stream, into JSON")
     ap.add_argument("--counter-run", choices=("warm", "cold", "cfg3"), default=None,
                     help="only eager decode calls for a rocprofv3 counter pass (config 4's call on "
                          "a warm pool or between the step's GEMMs, or the headline workload)")
@@ -900,6 +984,9 @@ def main() -> int:
         return 0
     if args.counter_run:
         counter_run(dev, args.counter_run)
+        return 0
+    if args.ceiling:
+        ceiling_legs(dev, args.ceiling)
         return 0
     if args.writes_only:
         res = write_legs(dev, cfg1_graph=False)

@@ -154,6 +154,26 @@ int32_t auto_min_tiles(int64_t batch, int64_t table_width, int32_t block_size, i
 // 4 per CU 44.0 vs 29.5), with 8 from CUs / 2 to CUs workgroups (B = 32 x 1024 27.4 vs 32.4;
 // B = 1 and 8 x 1024 lose 4.1 and 0.6); 16-bit caches up to 2 tiles per wave (B = 1 x 256 10.9
 // vs 14.6), 4 from CUs / 2 workgroups (B = 16 x 512 18.3 vs 22.4; B = 1-8 lose 0.7-0.8).
+// Workgroups per (sequence, kv head) of the split per-sequence layout: one on every CU, at most
+// 64 (one merge lane each) and at most 2 x num_ranges / batch (the records use the range-record
+// rows of the workspace, 2 x num_ranges per query head); at head_dim 128 also at most
+// max(16, tiles / 4) for the longest possible sequence's tiles, so that short sequences do not
+// leave workgroups without tiles: B = 1 x 1024 / 2048 / 4096 tokens (32 / 64 / 128 tiles) measured
+// best at Z = 16-32 / 16-32 / 32 (INT8 9.3-9.4 / 9.7 / 10.5 us, BF16 8.7 / 9.5-9.8 / 10.6 us,
+// HIP-graph replays) against 10.5 / 10.8 / 11.6 (INT8) at Z = 64.  Below 2 it is the plain
+// layout.
+int32_t split_count(int64_t batch, int32_t num_kv_heads, int32_t num_ranges, int64_t cu,
+                    int32_t head_dim, int64_t table_width, int32_t block_size) {
+  int64_t z = cu / (batch * num_kv_heads);
+  z = std::min<int64_t>(z, 64);
+  z = std::min<int64_t>(z, 2 * (int64_t)num_ranges / batch);
+  if (head_dim == 128) {
+    const int64_t tiles = ((int64_t)table_width * block_size + 31) / 32;  // longest sequence
+    z = std::min<int64_t>(z, std::max<int64_t>(16, tiles / 4));
+  }
+  return z >= 2 ? (int32_t)z : 0;
+}
+
 bool use_per_sequence(bool int8_cache, int32_t head_dim, int64_t batch, int32_t num_kv_heads,
                       int64_t table_width, int32_t block_size, int64_t cu) {
   const int64_t wgs = batch * num_kv_heads;
@@ -173,7 +193,16 @@ bool use_per_sequence(bool int8_cache, int32_t head_dim, int64_t batch, int32_t 
     if (!int8_cache) return per_wave <= 4;
     return per_wave <= 6 || (per_wave <= 8 && wgs >= cu / 8);
   }
-  if (!int8_cache) return wgs <= 3 * cu && (per_wave <= 2 || (per_wave <= 4 && 2 * wgs >= cu));
+  if (!int8_cache) {
+    // Few workgroups: the split layout, once each of its workgroups gets a tile, beats the
+    // per-sequence one for 16-bit caches even at 2 tiles per wave (B = 1 / 2 / 4 / 8 x 512:
+    // 8.04 / 8.02 / 8.20 / 8.59 vs 8.99 / 9.02 / 9.10 / 9.19 us).
+    if (8 * wgs <= cu &&
+        tiles >= (double)split_count(batch, num_kv_heads, 1 << 20, cu, head_dim, table_width,
+                                     block_size))
+      return false;
+    return wgs <= 3 * cu && (per_wave <= 2 || (per_wave <= 4 && 2 * wgs >= cu));
+  }
   if (wgs > cu) return false;
   // Few workgroups with 3 or more tiles per wave: the split layout (use_split) spreads them over
   // every CU once each of its workgroups gets a tile (B = 8 x 1024 11.7 -> 9.8 us, 8 x 768 10.5
@@ -183,16 +212,6 @@ bool use_per_sequence(bool int8_cache, int32_t head_dim, int64_t batch, int32_t 
   if (per_wave > 8) return false;
   const int64_t need = (per_wave - 3) * cu / 8;
   return wgs >= (need < cu / 2 ? need : cu / 2);
-}
-
-// Workgroups per (sequence, kv head) of the split per-sequence layout: one on every CU, at most
-// 64 (one merge lane each) and at most 2 x num_ranges / batch (the records use the range-record
-// rows of the workspace, 2 x num_ranges per query head).  Below 2 it is the plain layout.
-int32_t split_count(int64_t batch, int32_t num_kv_heads, int32_t num_ranges, int64_t cu) {
-  int64_t z = cu / (batch * num_kv_heads);
-  z = std::min<int64_t>(z, 64);
-  z = std::min<int64_t>(z, 2 * (int64_t)num_ranges / batch);
-  return z >= 2 ? (int32_t)z : 0;
 }
 
 // The automatic choice of the split per-sequence layout, for few long sequences (when the
@@ -212,7 +231,8 @@ bool use_split(int32_t head_dim, int64_t batch, int32_t num_kv_heads, int64_t ta
                int32_t block_size, int64_t cu) {
   const int64_t wgs = batch * num_kv_heads;
   if (8 * wgs > cu) return false;
-  const int64_t z = std::min<int64_t>(cu / wgs, 64);
+  const int64_t z = split_count(batch, num_kv_heads, 1 << 20, cu, head_dim, table_width, block_size);
+  if (z < 2) return false;
   const double tiles = std::ceil((double)table_width * block_size / 32.0);  // longest sequence
   const int nw = head_dim > 128 ? group_waves<256>() : group_waves<128>();
   return tiles / (double)(z * nw) <= (head_dim == 64 ? 2.0 : 4.0);
@@ -411,7 +431,7 @@ int plan_call(int query_dtype, int cache_dtype, int64_t batch, int32_t num_q_hea
     // A caller's range count fixes the split count (num_ranges / batch workgroups per sequence
     // and kv head, e.g. the reference's num_splits); the automatic one fills the chip.
     p.split = auto_ranges_req
-                  ? split_count(batch, hv, num_ranges, cus)
+                  ? split_count(batch, hv, num_ranges, cus, hd, table_width, block_size)
                   : (int32_t)std::min<int64_t>(64, num_ranges / batch);
     if (p.split < 2) p.split = 0;
   }

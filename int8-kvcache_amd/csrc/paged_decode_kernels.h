@@ -97,6 +97,29 @@ __device__ __forceinline__ HeadMap head_map(const DecodeArgs& a, int vh) {
 }
 
 // ------------------------------------------------------------------------ wave utilities
+// Combines x over the four 16-lane rows of the wave (lanes l, l ^ 16, l ^ 32, l ^ 48: one MFMA
+// column's four lane groups) with gfx950's row swaps, v_permlane32_swap then v_permlane16_swap:
+// two VALU exchanges instead of two LDS permutes (ds_bpermute, whose round trips sat on the
+// critical path of every tile's softmax and of each segment's start).  Every lane gets the same
+// bits: op(op(x0, x2), op(x1, x3)) for rows 0-3 (op commutative).
+template <typename Op>
+__device__ __forceinline__ float across_rows(float x, Op op) {
+  const uint32_t b = __float_as_uint(x);
+  const auto h = __builtin_amdgcn_permlane32_swap(b, b, false, false);  // rows {0,1} <-> {2,3}
+  const float y = op(__uint_as_float(h[0]), __uint_as_float(h[1]));
+  const uint32_t c = __float_as_uint(y);
+  const auto r = __builtin_amdgcn_permlane16_swap(c, c, false, false);  // rows 0 <-> 1, 2 <-> 3
+  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float rows_max(float x) {
+  return across_rows(x, [](float u, float v) { return fmaxf(u, v); });
+}
+
+__device__ __forceinline__ float rows_sum(float x) {
+  return across_rows(x, [](float u, float v) { return u + v; });
+}
+
 __device__ __forceinline__ int64_t wave_sum(int64_t x) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
@@ -148,6 +171,20 @@ __device__ __forceinline__ int64_t readlane64(int64_t x, int lane) {
 __device__ __forceinline__ int64_t seq_len_of(const DecodeArgs& a, int64_t b) {
   if (b >= a.batch) return 0;
   int64_t L = load_index(a.sl, b, a.sl_is64);
+  const int64_t cap = (int64_t)a.width << a.block_shift;
+  return L < 0 ? 0 : (L > cap ? cap : L);
+}
+
+// seq_len_of for a sequence b < batch that the whole workgroup shares (the per-sequence kernels'
+// blockIdx.x), without branches: the low word at b x (4 or 8) bytes and, for 64-bit lengths, the
+// high word after it (else the same word again), both requested at once.  seq_len_of's bounds
+// test and its branch on the index type put two dependent scalar round trips (the type flag,
+// then the length) in front of everything these kernels do.
+__device__ __forceinline__ int64_t seq_len_uniform(const DecodeArgs& a, int64_t b) {
+  const char* p = static_cast<const char*>(a.sl) + (b << (a.sl_is64 ? 3 : 2));
+  const uint32_t lo = *reinterpret_cast<const uint32_t*>(p);
+  const uint32_t hi = *reinterpret_cast<const uint32_t*>(p + (a.sl_is64 ? 4 : 0));
+  const int64_t L = a.sl_is64 ? (int64_t)(((uint64_t)hi << 32) | lo) : (int64_t)(int32_t)lo;
   const int64_t cap = (int64_t)a.width << a.block_shift;
   return L < 0 ? 0 : (L > cap ? cap : L);
 }
@@ -559,8 +596,7 @@ __device__ __forceinline__ void tile_scores(const KTile<CACHE, NB, HD>& r,
   float mx = sv[0];
 #pragma unroll
   for (int e = 1; e < 4 * NB; ++e) mx = fmaxf(mx, sv[e]);
-  mx = fmaxf(mx, __shfl_xor(mx, 16));
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  mx = rows_max(mx);
   const bool need = mx > m_run + kLazyRescale;
   if (__any(need)) {
     const float m_new = need ? mx : m_run;
@@ -749,7 +785,8 @@ __device__ __forceinline__ float round_half_away(float x) {
 //   it (their short calls wait on every exchange: ~0.15 us of a 6.5 us kernel on MI355X).
 template <int CACHE, int QT, bool QQ, int HD, bool PAIR = false, bool HEADWISE = false>
 __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRaw<QT, HD>& raw,
-                                              int kvh, typename MfmaOp<CACHE>::T (&qop)[HD / 32],
+                                              const float (&ksc)[2],
+                                              typename MfmaOp<CACHE>::T (&qop)[HD / 32],
                                               typename MfmaOp<CACHE>::T (&qlo)[HD / 32],
                                               i32x4 (&q8op)[HD / 64]) {
   constexpr int KS = HD / 32;  // 16-bit k-steps
@@ -772,14 +809,13 @@ __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRa
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[ks][e]));
   float s_scale = a.sm_scale_log2e;
   if constexpr (CACHE == kI8) {
-    // PAIR: the lane's column belongs to kv head kvh + 1 from column G on.
-    const int kv = PAIR ? kvh + ((int)(__lane_id() & 15) >= a.group ? 1 : 0) : kvh;
-    s_scale *= fmaxf(a.k_scale[kv], 1e-6f);
+    // ksc: the K scales of the wave's kv head and (PAIR) the next one, whose columns start at G.
+    const float ks = PAIR && (int)(__lane_id() & 15) >= a.group ? ksc[1] : ksc[0];
+    s_scale *= fmaxf(ks, 1e-6f);
   }
   if (a.quantize_q) {
     // absmax over the head's HD elements: the 4 lanes (li, lg = 0..3) of this head column
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    amax = rows_max(amax);
     const float qs = fmaxf(amax / 127.0f, 1e-6f);
     if constexpr (QQ) {
 #pragma unroll
@@ -813,8 +849,7 @@ __device__ __forceinline__ float finish_query(const DecodeArgs& a, const QueryRa
       amax = fmaxf(amax, __shfl_xor(amax, 4));
       amax = fmaxf(amax, __shfl_xor(amax, 8));
     }
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    amax = rows_max(amax);
     if (amax > 0.0f && amax < INFINITY) {
       const int e = 14 - ilogbf(amax);
       qmul = ldexpf(1.0f, e);
@@ -953,10 +988,17 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   i32x4 q8op[HD / 64];
   float s_scale;
   {
+    // The K scale is requested first: loaded where it is used, its scalar load was issued after
+    // the tile loads and its wait sat between the query conversion and the first tile.
+    float ksc[2] = {1.0f, 1.0f};
+    if constexpr (CACHE == kI8) {
+      ksc[0] = a.k_scale[kvh];
+      if constexpr (PAIR) ksc[1] = a.k_scale[kvh + 1];
+    }
     QueryRaw<QT, HD> qraw;
     issue_query<QT, HD, PAIR, PAD>(a, b, hm, li, lg, qraw);
     chunk_prologue();
-    s_scale = finish_query<CACHE, QT, QQ, HD, PAIR, GROUP>(a, qraw, kvh, qop, qlo, q8op);
+    s_scale = finish_query<CACHE, QT, QQ, HD, PAIR, GROUP>(a, qraw, ksc, qop, qlo, q8op);
   }
 
   // Tile t + d (buffer d): scores, refill K with tile t + d + DEPTH, P*V, refill V.  refill is a
@@ -1009,8 +1051,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     chunk_prologue();
   }
 
-  l_part += __shfl_xor(l_part, 16);
-  l_part += __shfl_xor(l_part, 32);
+  l_part = rows_sum(l_part);
   if constexpr (PAIR) {
     // Columns li < 2G; a column's rows are its own kv head's half of the 128 (lg / 2 = 0 for
     // li < G, 1 above: real head_dim elements 32 (lg % 2) + 8 rr + dt); the other half's rows
@@ -1215,9 +1256,9 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
   const int lg = lane >> 4;
   const int64_t b = blockIdx.x;
   const int vh = blockIdx.y;  // grid head (head_map)
+  const int64_t L = seq_len_uniform(a, b);  // first: every later step waits for it
   const HeadMap hm = head_map(a, vh);
   const int G = hm.g;
-  const int64_t L = seq_len_of(a, b);
   const int64_t n = tiles_of(a, L);
   if (n == 0) {  // uniform over the workgroup: every wave leaves before the barrier
     if (!SPLIT && wave == 0) write_zero_rows<QT, HD, PAD>(a, b, hm, lane);
@@ -1230,8 +1271,12 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
     t0 = (int64_t)blockIdx.z * n / gridDim.z;
     span = ((int64_t)blockIdx.z + 1) * n / gridDim.z - t0;
   }
-  const int64_t ta = t0 + wave * span / NW;
-  const int64_t tb = t0 + (wave + 1) * span / NW;
+  // The span's NW equal shares go to the waves SIMD by SIMD (wave w runs on SIMD w % 4): wave w
+  // takes share (w % 4) (NW / 4) + w / 4, so with fewer tiles than waves the waves that get one
+  // sit on different SIMDs.  (In wave order two tiles went to waves 3 and 7, which share SIMD 3.)
+  const int v = NW > 4 ? (wave % 4) * (NW / 4) + wave / 4 : wave;
+  const int64_t ta = t0 + v * span / NW;
+  const int64_t tb = t0 + (v + 1) * span / NW;
   if (ta < tb) {
     run_segment<CACHE, QT, false, QQ, HD, 2, true, false, PAD>(
         a, s_ids[wave], b, L, vh, ta, tb, false, 0, lane, s_acc[wave], s_m[wave], s_l[wave]);
@@ -1314,7 +1359,7 @@ __global__ __launch_bounds__(64) void merge_split_kernel(DecodeArgs a) {
 #pragma unroll
   for (int j = 0; j < D; ++j) O[j] = 0.0f;
   float inv = 0.0f;
-  if (seq_len_of(a, b) > 0) {  // uniform: an empty sequence left no records (zero rows)
+  if (seq_len_uniform(a, b) > 0) {  // uniform: an empty sequence left no records (zero rows)
     const float vscale = (CACHE == kI8) ? fmaxf(a.v_scale[h / a.group], 1e-6f) : 1.0f;
     const int64_t row0 = b * Z * a.num_q_heads + h;  // record z: row0 + z Hq
     const int64_t stride = (int64_t)a.num_q_heads * HD;

@@ -24,7 +24,7 @@ LIB_PATH = PKG_DIR / "libint8kv.so"
 # paged_decode_kernels.h); paged_decode.hip is its host side.
 SOURCES = ["cache_write.hip", "paged_decode.hip", "paged_decode_int8.hip", "paged_decode_bf16.hip",
            "paged_decode_fp16.hip", "paged_decode_int8_pad.hip", "paged_decode_bf16_pad.hip",
-           "paged_decode_fp16_pad.hip", "decode_loop_ops.hip"]
+           "paged_decode_fp16_pad.hip", "decode_loop_ops.hip", "read_probe.hip"]
 # The torch extension over the C ABI (host code only; torch headers, linked to libint8kv.so).
 EXT_SOURCE = "torch_ops.cpp"
 EXT_NAME = "_int8kv_torch"

@@ -31,7 +31,7 @@ def lib():
 
 
 def test_header_declares_expected_entry_points():
-    assert [h.name for h in HEADERS] == ["int8kv.h", "int8kv_decode_loop.h"]
+    assert [h.name for h in HEADERS] == ["int8kv.h", "int8kv_decode_loop.h", "int8kv_probe.h"]
     assert _declared_functions() == [
         "int8kv_add_rms_norm",
         "int8kv_argmax_rows",
@@ -42,6 +42,8 @@ def test_header_declares_expected_entry_points():
         "int8kv_dynamic_cache_write",
         "int8kv_paged_decode",
         "int8kv_paged_decode_noalloc",
+        "int8kv_probe_decode_loads",
+        "int8kv_probe_stream_read",
         "int8kv_rotary_cache_write",
         "int8kv_rotary_inplace",
         "int8kv_silu_mul",
@@ -101,6 +103,19 @@ def _decode_call(lib, **over):
                 min_tiles=0, flags=3, stream=None)
     args.update(over)
     return lib.int8kv_paged_decode(*args.values())
+
+
+def test_probes_reject_bad_arguments_without_launching(lib):
+    P = 16  # fake device pointers: every call fails validation first
+    sink = 1 << 20
+    assert lib.int8kv_probe_stream_read(None, 1024, 0, P, 256, None) == -1
+    assert lib.int8kv_probe_stream_read(P, 1000, 0, P, 256, None) == -4   # not whole 16 B
+    assert lib.int8kv_probe_stream_read(P, 1024, 0, P, 100, None) == -3   # sink of 256s
+    probe = lambda **o: lib.int8kv_probe_decode_loads(*{**dict(
+        kc=P, vc=P, nb=1024, hkv=4, ids=P, nids=2 * 8 * 16, ranges=8, tiles=16, nt=0, sink=P,
+        words=sink, stream=None), **o}.values())
+    assert probe(hkv=8) == -3 and probe(nids=10) == -3 and probe(words=100) == -3
+    assert probe(ranges=0) == -3 and probe(kc=None) == -1 and probe(kc=24) == -4
 
 
 def test_decode_rejects_bad_arguments_without_launching(lib):

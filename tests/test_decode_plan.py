@@ -64,9 +64,14 @@ def test_int8_head_dim_128_longer_sequences_need_workgroups(cus):
 
 @pytest.mark.parametrize("cus", [256, 304, 80])
 def test_16bit_head_dim_128(cus):
-    """16-bit caches at head_dim 128: up to 2 tiles per wave at any count, 4 from CUs / 2
-    workgroups, at most 3 workgroups per CU."""
-    assert layout(cache=BF16, batch=1, width=32, cus=cus) == "per_sequence"
+    """16-bit caches at head_dim 128: the split layout for up to CUs / 8 workgroups once each of
+    its workgroups gets a tile; otherwise the per-sequence layout up to 2 tiles per wave at any
+    count, 4 from CUs / 2 workgroups, at most 3 workgroups per CU."""
+    bmax = cus // 32                                   # 8 x (4 b) <= CUs
+    assert layout(cache=BF16, batch=1, width=32, cus=cus) == "split"       # 16 tiles, Z = 16
+    assert layout(cache=BF16, batch=bmax, width=32, cus=cus) == "split"
+    assert layout(cache=BF16, batch=bmax + 1, width=32, cus=cus) == "per_sequence"
+    assert layout(cache=BF16, batch=1, width=16, cus=cus) == "per_sequence"  # 8 tiles < Z = 16
     assert layout(cache=BF16, batch=3 * cus // 4, width=32, cus=cus) == "per_sequence"
     assert layout(cache=BF16, batch=3 * cus // 4 + 1, width=32, cus=cus) == "ranges"
     half = cus // 2
@@ -127,6 +132,14 @@ def test_split_rule_at_256():
     8 sequences x 8 workgroups stays in the range layout)."""
     p = plan(batch=1, width=2048)
     assert (p["layout"], p["split"], p["merge_waves"]) == ("split", 64, 1)
+    # At head_dim 128 at most max(16, tiles / 4) workgroups per sequence and kv head.
+    for cache in (I8, BF16):
+        for width, z in ((64, 16), (128, 16), (256, 32), (512, 64)):   # 1024-8192 tokens
+            p = plan(cache=cache, batch=1, width=width)
+            assert (p["layout"], p["split"]) == ("split", z), (cache, width, p)
+        assert plan(cache=cache, batch=2, width=64)["split"] == 16
+        assert plan(cache=cache, batch=2, width=256)["split"] == 32
+    assert plan(hq=32, hkv=8, d=64, batch=1, width=256)["split"] == 32  # (no cap at 64)
     assert layout(batch=8, width=2048) == "ranges"
     assert layout(hq=32, hkv=8, d=64, batch=1, width=256) == "split"
     assert layout(hq=32, hkv=8, d=64, batch=4, width=1024) == "ranges"
