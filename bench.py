@@ -396,7 +396,8 @@ def read_traffic(w, nbytes8: int):
 
 def sweep_configs(dev, out_path: str | None) -> dict:
     """INT8 and BF16 decode at B in {1, 2, 4, 8} x uniform ctx in {512, 1024, 2048, 4096}
-    (config 2), automatic layout vs one range per sequence.  The working sets fit the 256 MB
+    (config 2), automatic layout vs the single pass (num_splits=1: one workgroup per sequence
+    and kv head, no merge).  The working sets fit the 256 MB
     Infinity Cache, so their GB/s are cache-resident rates and µs/call is the meaningful figure.
     Times are device times per call from HIP-graph replays (a few-microsecond call is otherwise
     dominated by the host's launch cost)."""
@@ -436,6 +437,8 @@ def sweep_configs(dev, out_path: str | None) -> dict:
                 ("int8_single_pass", lambda: int8kv.int8_paged_attention(q, kc8, vc8, btd, lens, ks_d, vs_d,
                                                                          num_splits=1)),
                 ("bf16_auto", lambda: int8kv.bf16_paged_attention(q, kc16, vc16, btd, lens)),
+                ("bf16_single_pass", lambda: int8kv.bf16_paged_attention(q, kc16, vc16, btd, lens,
+                                                                         num_splits=1)),
             ):
                 ms = time_graph(fn)
                 e = 2 if name.startswith("bf16") else 1
@@ -444,7 +447,8 @@ def sweep_configs(dev, out_path: str | None) -> dict:
                 row[name + "_GBps"] = round(nbytes / ms / 1e6, 1)
             rows.append(row)
             log(f"cfg2 B={B} ctx={ctx}: int8 {row['int8_auto_us']} us (single pass "
-                f"{row['int8_single_pass_us']}), bf16 {row['bf16_auto_us']} us")
+                f"{row['int8_single_pass_us']}), bf16 {row['bf16_auto_us']} us (single pass "
+                f"{row['bf16_single_pass_us']})")
     res["cfg2_sweep"] = rows
     if out_path:
         Path(out_path).parent.mkdir(parents=True, exist_ok=True)
