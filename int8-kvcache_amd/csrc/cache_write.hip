@@ -50,8 +50,28 @@ struct WriteArgs {
   int32_t num_kv_heads;
   int32_t vecs_per_row;  // head_dim / 8
   int32_t block_size;
+  int32_t block_shift;  // log2(block_size) for a power of two, else -1
   int32_t slots_is64;
 };
+
+// A slot's block and row in it: a shift and a mask for a power-of-two block size (every paged
+// cache in practice), a division otherwise (a 64-bit division is ~100 instructions per lane).
+__device__ __forceinline__ void slot_block(const WriteArgs& a, int64_t slot, int64_t& blk,
+                                           int64_t& off) {
+  if (a.block_shift >= 0) {
+    blk = slot >> a.block_shift;
+    off = slot & ((1LL << a.block_shift) - 1);
+  } else {
+    blk = slot / a.block_size;
+    off = slot - blk * a.block_size;
+  }
+}
+
+// gid / n for a wave-uniform n >= 1: a shift when n is a power of two (head_dim / 16 lanes per
+// row at head_dim 64, 128, 256), a division otherwise.
+__device__ __forceinline__ uint32_t div_uniform(uint32_t gid, uint32_t n) {
+  return (n & (n - 1)) == 0 ? gid >> __builtin_ctz(n) : gid / n;
+}
 
 template <int SRC>
 __global__ __launch_bounds__(256) void cache_write_kernel(WriteArgs a) {
@@ -65,8 +85,8 @@ __global__ __launch_bounds__(256) void cache_write_kernel(WriteArgs a) {
 
   const int64_t slot = load_index(a.slots, t, a.slots_is64);
   if (slot < 0 || slot >= a.capacity) return;
-  const int64_t blk = slot / a.block_size;
-  const int64_t off = slot - blk * a.block_size;
+  int64_t blk, off;
+  slot_block(a, slot, blk, off);
 
   constexpr int esize = SRC == kF32 ? 4 : 2;
   const QuantScale ks = quant_scale(fmaxf(a.k_scale[h], 1e-6f));
@@ -129,22 +149,23 @@ __global__ __launch_bounds__(256) void cache_write16_kernel(WriteArgs a) {
   const int h = blockIdx.y;
   const uint32_t lpr = (uint32_t)a.vecs_per_row;
   const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
-  const uint32_t t = gid / lpr;
+  const uint32_t t = div_uniform(gid, lpr);
   if ((int64_t)t >= a.num_tokens) return;
   const int dv = (int)(gid - t * lpr);
   constexpr int esize = SRC == kF32 ? 4 : 2;
-  // The slot first: a skipped row (slot < 0, or past the cache) loads no source bytes.  The
-  // extra dependent load is hidden by the other resident waves (MI355X: 262,144-token write
-  // 155.6 us either way).
+  // The slot and the row's source bytes are requested together (a skipped row, slot < 0 or past
+  // the cache, then stores nothing): with every wave of a small write resident at once (config 1:
+  // 16,384 tokens, 8,192 waves), a slot-first order put a second dependent memory latency on
+  // each wave's path.
   const int64_t slot = load_index(a.slots, t, a.slots_is64);
-  if (slot < 0 || slot >= a.capacity) return;
   float x[16], y[16];
   load16_f32<SRC>(a.key + ((int64_t)t * a.k_st + h * a.k_sh + 16 * dv) * esize, x);
   load16_f32<SRC>(a.value + ((int64_t)t * a.v_st + h * a.v_sh + 16 * dv) * esize, y);
+  if (slot < 0 || slot >= a.capacity) return;
   const QuantScale ks = quant_scale(fmaxf(a.k_scale[h], 1e-6f));
   const QuantScale vs = quant_scale(fmaxf(a.v_scale[h], 1e-6f));
-  const int64_t blk = slot / a.block_size;
-  const int64_t off = slot - blk * a.block_size;
+  int64_t blk, off;
+  slot_block(a, slot, blk, off);
   uint32_t wk[4], wv[4];
   quantise<16, false>(x, ks, wk);
   quantise<16, false>(y, vs, wv);
@@ -204,8 +225,8 @@ __global__ __launch_bounds__(256) void dynamic_write_kernel(DynWriteArgs d) {
   if (!in_range) return;
   const int64_t slot = load_index(a.slots, t, a.slots_is64);
   if (slot < 0 || slot >= a.capacity) return;
-  const int64_t blk = slot / a.block_size;
-  const int64_t off = slot - blk * a.block_size;
+  int64_t blk, off;
+  slot_block(a, slot, blk, off);
   uint32_t wk[2], wv[2];
   quantise<8, true>(x, quant_scale(ks), wk);
   quantise<8, true>(y, quant_scale(vs), wv);
@@ -229,7 +250,7 @@ __global__ __launch_bounds__(256) void dynamic_write16_kernel(DynWriteArgs d) {
   const int h = blockIdx.y;
   const uint32_t lpr = (uint32_t)a.vecs_per_row;
   const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
-  const uint32_t t = gid / lpr;
+  const uint32_t t = div_uniform(gid, lpr);
   const bool in_range = (int64_t)t < a.num_tokens;
   const int dv = (int)(gid - t * lpr);
   constexpr int esize = SRC == kF32 ? 4 : 2;
@@ -256,8 +277,8 @@ __global__ __launch_bounds__(256) void dynamic_write16_kernel(DynWriteArgs d) {
   const float ks = fmaxf(km / 127.0f, 1e-6f);
   const float vs = fmaxf(vm / 127.0f, 1e-6f);
   if (!in_range || slot < 0 || slot >= a.capacity) return;
-  const int64_t blk = slot / a.block_size;
-  const int64_t off = slot - blk * a.block_size;
+  int64_t blk, off;
+  slot_block(a, slot, blk, off);
   uint32_t wk[4], wv[4];
   quantise<16, true>(x, quant_scale(ks), wk);
   quantise<16, true>(y, quant_scale(vs), wv);
@@ -301,8 +322,8 @@ __global__ __launch_bounds__(256) void cache_write16_tm_kernel(WriteArgs a, int 
   float x[16], y[16];
   load16_f32<SRC>(a.key + ((int64_t)L.t * a.k_st + L.h * a.k_sh + 16 * L.dv) * esize, x);
   load16_f32<SRC>(a.value + ((int64_t)L.t * a.v_st + L.h * a.v_sh + 16 * L.dv) * esize, y);
-  const int64_t blk = slot / a.block_size;
-  const int64_t off = slot - blk * a.block_size;
+  int64_t blk, off;
+  slot_block(a, slot, blk, off);
   uint32_t wk[4], wv[4];
   quantise<16, false>(x, quant_scale(fmaxf(a.k_scale[L.h], 1e-6f)), wk);
   quantise<16, false>(y, quant_scale(fmaxf(a.v_scale[L.h], 1e-6f)), wv);
@@ -338,8 +359,8 @@ __global__ __launch_bounds__(256) void dynamic_write16_tm_kernel(DynWriteArgs d,
   }
   const float ks = fmaxf(km / 127.0f, 1e-6f);
   const float vs = fmaxf(vm / 127.0f, 1e-6f);
-  const int64_t blk = slot / a.block_size;
-  const int64_t off = slot - blk * a.block_size;
+  int64_t blk, off;
+  slot_block(a, slot, blk, off);
   uint32_t wk[4], wv[4];
   quantise<16, true>(x, quant_scale(ks), wk);
   quantise<16, true>(y, quant_scale(vs), wv);
@@ -462,6 +483,7 @@ int prepare_write(WriteArgs& a, const void* key, const void* value, int src_dtyp
   a.num_kv_heads = num_kv_heads;
   a.vecs_per_row = head_dim / 8;
   a.block_size = block_size;
+  a.block_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.slots_is64 = slot_dtype == INT8KV_I64;
   return 1;  // launch needed
 }

@@ -177,6 +177,7 @@ struct RopeWriteArgs {
   int64_t table_width;
   int64_t num_blocks;
   int block_size;
+  int block_shift;  // log2(block_size) for a power of two, else -1
   char* kc;
   char* vc;
   int64_t kc_sb, kc_ss, kc_sh;  // element strides
@@ -249,7 +250,8 @@ __global__ __launch_bounds__(kRopeThreads) void rope_write_kernel(RopeWriteArgs 
     }
   }
   // k or v head: write both 8-element pieces to the cache row of this token.
-  const int64_t blk_idx = p / a.block_size;
+  // (A shift for a power-of-two block size: a 64-bit division is ~100 instructions per lane.)
+  const int64_t blk_idx = a.block_shift >= 0 ? p >> a.block_shift : p / a.block_size;
   if (blk_idx >= a.table_width) return;
   const int64_t blk = a.bt[row * a.bt_stride + blk_idx];
   if (blk < 0 || blk >= a.num_blocks) return;
@@ -475,6 +477,7 @@ extern "C" int int8kv_rotary_cache_write(
   a.table_width = table_width;
   a.num_blocks = num_blocks;
   a.block_size = block_size;
+  a.block_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   a.kc = static_cast<char*>(key_cache);
   a.vc = static_cast<char*>(value_cache);
   a.kc_sb = key_cache_strides[0];
