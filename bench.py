@@ -592,8 +592,9 @@ def midsize_legs(dev, out_path: str | None) -> dict:
     return res
 
 
-def graph_us(fns, replays: int = 10, settle_ms: float = 30.0) -> float:
-    """Device time (us) of one replay of a HIP graph that captures ``fns`` once each, in order."""
+def capture_graph(fns):
+    """A HIP graph that captures ``fns`` once each, in order (after one eager warm-up pass on a
+    side stream)."""
     import torch
 
     s = torch.cuda.Stream()
@@ -608,6 +609,14 @@ def graph_us(fns, replays: int = 10, settle_ms: float = 30.0) -> float:
         for fn in fns:
             fn()
     torch.cuda.synchronize()
+    return graph
+
+
+def graph_us(fns, replays: int = 10, settle_ms: float = 30.0) -> float:
+    """Device time (us) of one replay of a HIP graph that captures ``fns`` once each, in order."""
+    import torch
+
+    graph = capture_graph(fns)
     settle(graph.replay, batch=1, min_ms=settle_ms, max_ms=4 * settle_ms)
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
@@ -680,6 +689,51 @@ class ColdSetup:
             torch.mm(self.act, self.wdown[layer].t(), out=self.y[3])
         return run
 
+    def read_weights(self, layer, non_temporal):
+        """The layer's four weight matrices read by the stream probe (16-byte loads, ordinary or
+        non-temporal) instead of multiplied: the GEMMs' bytes without their arithmetic."""
+        import torch
+
+        from int8kv import _lib
+
+        lib = _lib.load()
+        if not hasattr(self, "sink"):
+            self.sink = torch.empty(256 * 8 * 256, dtype=torch.int32, device=self.x.device)
+        ws = [w[layer] for w in (self.wqkv, self.wo, self.wgu, self.wdown)]
+
+        def run():
+            s = torch.cuda.current_stream().cuda_stream
+            for w in ws:
+                _lib.check(lib.int8kv_probe_stream_read(w.data_ptr(), w.numel() * 2, non_temporal,
+                                                        self.sink.data_ptr(), self.sink.numel(), s),
+                           "int8kv_probe_stream_read")
+        return run
+
+    def clock(self, out, ticks):
+        """The clock probe over 1,024 one-wave workgroups (one per SIMD) into out[1024, 2]."""
+        import torch
+
+        from int8kv import _lib
+
+        lib = _lib.load()
+        return lambda: _lib.check(lib.int8kv_probe_clock(out.data_ptr(), 1024, ticks,
+                                                         torch.cuda.current_stream().cuda_stream),
+                                  "int8kv_probe_clock")
+
+    def separator(self):
+        """A one-workgroup stream-probe launch that marks leg boundaries in a kernel trace."""
+        import torch
+
+        from int8kv import _lib
+
+        lib = _lib.load()
+        if not hasattr(self, "sep"):
+            self.sep = torch.zeros(2 * 4096, dtype=torch.int32, device=self.x.device)
+        _lib.check(lib.int8kv_probe_stream_read(self.sep.data_ptr(), 16384, 0,
+                                                self.sep.data_ptr() + 16384, 256,
+                                                torch.cuda.current_stream().cuda_stream),
+                   "separator")
+
 
 def cold_legs(dev, out_path: str | None) -> dict:
     """The decode op (decode + merge) at config 4's per-layer shape with warm and cold caches.
@@ -690,7 +744,14 @@ def cold_legs(dev, out_path: str | None) -> dict:
     * between_gemms: 28 x (layer i's four GEMMs, then the call on layer i's pool), minus the same
       graph without the calls: the attention call in the decode step's traffic (0.5 GB of
       weights streamed between two layers' calls).  Also for the decode kernel alone.
-    Kernel durations inside each graph come from a kernel trace of this same leg."""
+    * after_<predecessor>: the same difference with other work in the GEMMs' place: the GEMMs on
+      layer 0's weights every time (the same 466 MB), the layer's weights read by the stream
+      probe with ordinary or non-temporal loads, a 200 us spin of the clock probe.
+    * clock_after_<leg>: the shader clock (MHz, clock probe over a 5 us window, median over
+      1,024 waves and the 28 positions) right after the call alone, the GEMMs, the GEMMs + call.
+    * trace legs: graphs of 28 x (GEMMs, call), 28 x GEMMs and 28 x call, replayed 12 times each
+      between two separator launches, for a kernel trace (`--trace-table` summarises it)."""
+    import numpy as np
     import torch
 
     from int8kv import _lib
@@ -714,11 +775,84 @@ def cold_legs(dev, out_path: str | None) -> dict:
         res[f"between_gemms_{name}_TBps"] = round(nbytes / us / 1e6, 3)
         log(f"cold: between the GEMMs: {name} {us:.2f} us ({nbytes / us / 1e6:.2f} TB/s)")
     res["gemms_per_layer_us"] = round(base / NL, 2)
+    spin_out = torch.zeros(1024, 2, dtype=torch.int64, device=dev)
+    preds = {
+        "gemms_same_weights": lambda i: cs.gemms(0),
+        "read_weights": lambda i: cs.read_weights(i, 0),
+        "read_weights_nt": lambda i: cs.read_weights(i, 1),
+        "spin_200us": lambda i: cs.clock(spin_out, 20000),
+    }
+    for name, mk in preds.items():
+        pre = [mk(i) for i in range(NL)]
+        without = graph_us(pre)
+        us = (graph_us([f for i in range(NL) for f in (pre[i], cs.op(i))]) - without) / NL
+        res[f"after_{name}_op_us"] = round(us, 2)
+        log(f"cold: after {name}: op {us:.2f} us")
+    clk = torch.zeros(NL, 1024, 2, dtype=torch.int64, device=dev)
+    for name, mk in (("op", lambda i: [cs.op(i)]), ("gemms", lambda i: [cs.gemms(i)]),
+                     ("gemms_op", lambda i: [cs.gemms(i), cs.op(i)])):
+        graph_us([f for i in range(NL) for f in (*mk(i), cs.clock(clk[i], 500))], replays=1,
+                 settle_ms=100.0)
+        o = clk.cpu().numpy().astype(np.float64)
+        mhz = float(np.median(o[..., 1] / (o[..., 0] * 0.01)))
+        res[f"clock_after_{name}_mhz"] = round(mhz, 1)
+        log(f"cold: shader clock after {name}: {mhz:.1f} MHz")
+    for name, fns in (("gemms_op", [f for i in range(NL) for f in (cs.gemms(i), cs.op(i))]),
+                      ("gemms", [cs.gemms(i) for i in range(NL)]),
+                      ("op", [cs.op(i) for i in range(NL)])):
+        g = capture_graph(fns)
+        settle(g.replay, batch=1, min_ms=30.0, max_ms=120.0)
+        cs.separator()
+        for _ in range(12):
+            g.replay()
+        cs.separator()
+        torch.cuda.synchronize()
+        del g
+    res["trace_legs"] = ["gemms_op", "gemms", "op"]
     del cs
     torch.cuda.empty_cache()
     if out_path:
         Path(out_path).parent.mkdir(parents=True, exist_ok=True)
         Path(out_path).write_text(json.dumps({"cold": res}, indent=1))
+    return res
+
+
+def trace_table(csv_path: str, out_path: str | None) -> dict:
+    """Summarises a rocprofv3 kernel trace (``--kernel-trace --output-format csv``) of ``--cold``:
+    the dispatches between each pair of separator launches (one-workgroup stream probes, the
+    last six of the run) are the 12 replays of one trace leg (28 x (GEMMs, call), 28 x GEMMs,
+    28 x call).  Per leg: the span per replay and each kernel class's mean duration (the GEMMs by
+    their position in the layer: qkv, o_proj, gate_up, down).  In a graph each dispatch starts
+    when the previous one ends, so a duration includes the kernel's start-up after it."""
+    import csv
+
+    rows = sorted(csv.DictReader(open(csv_path)), key=lambda r: int(r["Start_Timestamp"]))
+    seps = [i for i, r in enumerate(rows)
+            if "probe_stream_kernel" in r["Kernel_Name"] and int(r["Grid_Size_X"]) == 256][-6:]
+    gemm_names = ("qkv", "o_proj", "gate_up", "down")
+    res = {"csv": csv_path}
+    for k, leg in enumerate(("gemms_op", "gemms", "op")):
+        win = rows[seps[2 * k] + 1: seps[2 * k + 1]]
+        dur: dict = {}
+        n_gemm = 0
+        for r in win:
+            name = r["Kernel_Name"]
+            us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            if "decode_kernel" in name:
+                c = "decode"
+            elif "merge" in name:
+                c = "merge"
+            else:
+                c = "gemm_" + gemm_names[n_gemm % 4]
+                n_gemm += 1
+            dur.setdefault(c, []).append(us)
+        span = (int(win[-1]["End_Timestamp"]) - int(win[0]["Start_Timestamp"])) / 1e3 / 12
+        res[leg] = {"dispatches": len(win), "span_per_replay_us": round(span, 1),
+                    **{c: round(sum(v) / len(v), 2) for c, v in sorted(dur.items())}}
+        log(f"trace {leg}: {res[leg]}")
+    if out_path:
+        Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+        Path(out_path).write_text(json.dumps({"trace_table": res}, indent=1))
     return res
 
 
@@ -932,6 +1066,8 @@ def main() -> int:
     ap.add_argument("--cold", metavar="JSON", default=None,
                     help="only config 4's per-layer decode call with warm and cold caches (28 "
                          "layer pools rotated, and between the decode step's GEMMs), results to JSON")
+    ap.add_argument("--trace-table", nargs=2, metavar=("CSV", "JSON"), default=None,
+                    help="summarise a rocprofv3 kernel trace of --cold (CPU only) into JSON")
     ap.add_argument("--ceiling", metavar="JSON", default=None,
                     help="only the read-ceiling probes of the decode's K/V stream, into JSON")
     ap.add_argument("--counter-run", choices=("warm", "cold", "cfg3"), default=None,
@@ -963,6 +1099,9 @@ def main() -> int:
               "decode op needs no exchange to shard (sequences and kv heads split across GPUs "
               "independently); run with --gpus 1.", file=sys.stderr)
         return 2
+    if args.trace_table:
+        trace_table(*args.trace_table)
+        return 0
 
     import torch
 

@@ -1,10 +1,11 @@
 /*
- * Read-ceiling probes of libint8kv.so: measurement only, no counterpart in the reference.
+ * Measurement probes of libint8kv.so: measurement only, no counterpart in the reference.
  *
- * bench.py --ceiling times them beside the INT8 decode to give the ceiling of the decode's own
- * K/V load pattern on the GPU it runs on (the decode kernel's achieved rate is read against it as
- * well as against the HBM peak).  They read device memory and write one word per thread into
- * `sink`; nothing else.  Status codes as in int8kv.h (INT8KV_OK = 0).
+ * bench.py --ceiling times the two read probes beside the INT8 decode to give the ceiling of the
+ * decode's own K/V load pattern on the GPU it runs on (the decode kernel's achieved rate is read
+ * against it as well as against the HBM peak).  They read device memory and write one word per
+ * thread into `sink`; nothing else.  bench.py --cold uses the clock probe to read the shader
+ * clock between the decode step's kernels.  Status codes as in int8kv.h (INT8KV_OK = 0).
  */
 #ifndef INT8KV_PROBE_H
 #define INT8KV_PROBE_H
@@ -37,6 +38,15 @@ int int8kv_probe_decode_loads(const void* key_cache, const void* value_cache, in
                               int64_t block_id_count, int32_t num_ranges,
                               int32_t tiles_per_range, int32_t non_temporal, uint32_t* sink,
                               int64_t sink_words, void* stream);
+
+/*
+ * Shader clock: `workgroups` one-wave workgroups each spin for `ticks` ticks of the GPU's
+ * constant 100 MHz real-time counter (s_memrealtime; at most 200,000 iterations) and store, in
+ * out[2 w] and out[2 w + 1], the real-time ticks and the shader-clock cycles (s_memtime) that
+ * elapsed meanwhile: cycles / (ticks x 10 ns) is the clock in cycles per ns.  workgroups in
+ * [1, 65535], ticks in [1, 1000000] (10 ms); out holds 2 x workgroups uint64.
+ */
+int int8kv_probe_clock(uint64_t* out, int32_t workgroups, uint32_t ticks, void* stream);
 
 #ifdef __cplusplus
 }

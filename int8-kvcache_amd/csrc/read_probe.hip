@@ -1,6 +1,7 @@
-// Read-ceiling probes (measurement only, include/int8kv_probe.h): what this chip delivers for the
-// INT8 decode's K/V stream with the arithmetic taken out, so that the decode kernel's rate can be
-// read against the ceiling of its own load pattern rather than against the HBM peak alone.
+// Measurement probes (include/int8kv_probe.h).  The read-ceiling probes give what this chip
+// delivers for the INT8 decode's K/V stream with the arithmetic taken out, so that the decode
+// kernel's rate can be read against the ceiling of its own load pattern rather than against the
+// HBM peak alone; the clock probe reads the shader clock against the real-time counter.
 //
 //   probe_stream_kernel   a plain streaming read: 16-byte loads, four in flight per lane,
 //                         grid-stride over a flat buffer (the best a simple reader gets).
@@ -122,6 +123,22 @@ probe_decode_kernel(DecodeArgs a, int32_t tiles, uint32_t* sink) {
   sink[blockIdx.x * blockDim.x + threadIdx.x] = acc;
 }
 
+// One wave per workgroup: shader-clock cycles (s_memtime) over a window of the 100 MHz real-time
+// counter (s_memrealtime), the loop bounded by an iteration cap as well as by the window.
+__global__ __launch_bounds__(64) void probe_clock_kernel(uint64_t* out, uint32_t ticks) {
+  const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+  const uint64_t c0 = __builtin_amdgcn_s_memtime();
+  uint64_t r = r0, c = c0;
+  for (int i = 0; i < 200000 && r - r0 < ticks; ++i) {
+    r = __builtin_amdgcn_s_memrealtime();
+    c = __builtin_amdgcn_s_memtime();
+  }
+  if (threadIdx.x == 0) {
+    out[2 * blockIdx.x] = r - r0;
+    out[2 * blockIdx.x + 1] = c - c0;
+  }
+}
+
 }  // namespace
 }  // namespace int8kv
 
@@ -179,5 +196,15 @@ extern "C" int int8kv_probe_decode_loads(const void* key_cache, const void* valu
     hipLaunchKernelGGL((probe_decode_kernel<true>), grid, block, 0, s, a, tiles_per_range, sink);
   else
     hipLaunchKernelGGL((probe_decode_kernel<false>), grid, block, 0, s, a, tiles_per_range, sink);
+  return (int)hipGetLastError();
+}
+
+extern "C" int int8kv_probe_clock(uint64_t* out, int32_t workgroups, uint32_t ticks,
+                                  void* stream) {
+  if (!out) return INT8KV_E_NULL;
+  if (workgroups < 1 || workgroups > 65535 || ticks < 1 || ticks > 1000000) return INT8KV_E_SHAPE;
+  if (((uintptr_t)out % 8) != 0) return INT8KV_E_STRIDE;
+  hipLaunchKernelGGL(probe_clock_kernel, dim3((unsigned)workgroups), dim3(kWave), 0,
+                     static_cast<hipStream_t>(stream), out, ticks);
   return (int)hipGetLastError();
 }

@@ -124,9 +124,11 @@ def load() -> ctypes.CDLL:
     lib.int8kv_argmax_rows.argtypes = [_vp, i64, i64, i64, _vp, _vp]
     lib.int8kv_version.restype = ctypes.c_char_p
     lib.int8kv_version.argtypes = []
-    # include/int8kv_probe.h (measurement only: bench.py --ceiling)
+    # include/int8kv_probe.h (measurement only: bench.py --ceiling and --cold)
     lib.int8kv_probe_stream_read.restype = ctypes.c_int
     lib.int8kv_probe_stream_read.argtypes = [_vp, sz, i32, _vp, i32, _vp]
+    lib.int8kv_probe_clock.restype = ctypes.c_int
+    lib.int8kv_probe_clock.argtypes = [_vp, i32, ctypes.c_uint32, _vp]
     lib.int8kv_probe_decode_loads.restype = ctypes.c_int
     lib.int8kv_probe_decode_loads.argtypes = [_vp, _vp, i64, i32, _vp, i64, i32, i32, i32, _vp, i64,
                                               _vp]

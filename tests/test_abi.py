@@ -42,6 +42,7 @@ def test_header_declares_expected_entry_points():
         "int8kv_dynamic_cache_write",
         "int8kv_paged_decode",
         "int8kv_paged_decode_noalloc",
+        "int8kv_probe_clock",
         "int8kv_probe_decode_loads",
         "int8kv_probe_stream_read",
         "int8kv_rotary_cache_write",
@@ -116,6 +117,10 @@ def test_probes_reject_bad_arguments_without_launching(lib):
         words=sink, stream=None), **o}.values())
     assert probe(hkv=8) == -3 and probe(nids=10) == -3 and probe(words=100) == -3
     assert probe(ranges=0) == -3 and probe(kc=None) == -1 and probe(kc=24) == -4
+    assert lib.int8kv_probe_clock(None, 4, 100, None) == -1
+    assert lib.int8kv_probe_clock(P, 0, 100, None) == -3 and lib.int8kv_probe_clock(P, 65536, 100, None) == -3
+    assert lib.int8kv_probe_clock(P, 4, 0, None) == -3 and lib.int8kv_probe_clock(P, 4, 1000001, None) == -3
+    assert lib.int8kv_probe_clock(P + 4, 4, 100, None) == -4
 
 
 def test_decode_rejects_bad_arguments_without_launching(lib):

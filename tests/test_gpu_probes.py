@@ -1,7 +1,8 @@
-"""The read-ceiling probes of include/int8kv_probe.h (measurement only, bench.py --ceiling) on a
-small pool: both kernels run, every word of the sink they own is written, and the decode-load
+"""The probes of include/int8kv_probe.h (measurement only, bench.py --ceiling and --cold) on small
+inputs: the read probes run, every word of the sink they own is written, and the decode-load
 probe's result depends only on the bytes it reads (the xor of every loaded dword per lane is
-recomputed on the CPU for the ordinary and the non-temporal variant)."""
+recomputed on the CPU for the ordinary and the non-temporal variant); the clock probe reports a
+window at least as long as asked and a shader clock in a plausible range."""
 
 from __future__ import annotations
 
@@ -70,3 +71,17 @@ def test_decode_load_probe(cuda):
                                              stream), "int8kv_probe_decode_loads")
     torch.cuda.synchronize()
     assert torch.equal(sink.cpu(), outs[0])
+
+
+def test_clock_probe(cuda):
+    lib = _lib.load()
+    W, ticks = 64, 300  # 3 us windows
+    out = torch.zeros(2 * W, dtype=torch.int64, device=cuda)
+    _lib.check(lib.int8kv_probe_clock(out.data_ptr(), W, ticks, _lib.stream_handle(cuda)),
+               "int8kv_probe_clock")
+    torch.cuda.synchronize()
+    o = out.cpu().numpy().reshape(W, 2)
+    assert (o[:, 0] >= ticks).all() and (o[:, 0] < 100 * ticks).all(), o[:4]
+    mhz = o[:, 1] / (o[:, 0] * 0.01)  # cycles per microsecond
+    print(f"clock probe: {np.median(mhz):.1f} MHz (min {mhz.min():.1f}, max {mhz.max():.1f})", flush=True)
+    assert ((mhz > 100) & (mhz < 5000)).all(), mhz
