@@ -4,6 +4,8 @@ The numpy oracle covers the whole batch in a few seconds, so every sequence is c
 * INT8: the oracle bar (max-abs <= 2e-2, cos >= 0.9999) on each of the 64 sequences;
 * BF16 (the same K/V in a bf16 cache, bf16_paged_attention): the same bar against the oracle run
   on the bf16 cache values, each of the 64 sequences;
+* quantize_q=True (per-(sequence, head) int8 query, INT8 x INT8 scores on the streaming 4-deep
+  kernel this size takes): the oracle's quantize_q branch, each of the 64 sequences;
 and, through properties that do not depend on size:
 * relabelling the physical blocks (a permuted pool with the tables remapped) gives bit-identical
   outputs for all 64 sequences -- every block is fetched through its table entry;
@@ -52,6 +54,22 @@ def test_config3_every_sequence_matches_oracle(workload):
         worst = (max(worst[0], err), min(worst[1], cos))
         assert err <= MAX_ABS and cos >= MIN_COS, (b, int(lens[b]), err, cos)
     print(f"64 sequences: worst max|diff|={worst[0]:.2e} worst cos={worst[1]:.7f}", flush=True)
+
+
+def test_config3_quantize_q_every_sequence_matches_oracle(workload):
+    w = workload
+    lens = w["lens"].numpy()
+    out = _attn(w, quantize_q=True).float().cpu().numpy()
+    ref = O.paged_attention_ref(w["q"].float().cpu().numpy(), w["kc"].cpu().numpy(),
+                                w["vc"].cpu().numpy(), w["bt_cpu"].numpy(), lens,
+                                w["ks"].cpu().numpy(), w["vs"].cpu().numpy(), quantize_q=True)
+    worst = (0.0, 1.0)
+    for b in range(len(lens)):
+        err, cos, _ = metrics(out[b:b + 1], ref[b:b + 1])
+        worst = (max(worst[0], err), min(worst[1], cos))
+        assert err <= MAX_ABS and cos >= MIN_COS, (b, int(lens[b]), err, cos)
+    print(f"quantize_q, 64 sequences: worst max|diff|={worst[0]:.2e} worst cos={worst[1]:.7f}",
+          flush=True)
 
 
 def _sequence_blocks(cache, bt_row, L):
