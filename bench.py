@@ -856,6 +856,47 @@ def trace_table(csv_path: str, out_path: str | None) -> dict:
     return res
 
 
+def step_table(csv_path: str, out_path: str | None) -> dict:
+    """Summarises a rocprofv3 kernel trace of ``--tpot-only``: the dispatches of the INT8 run's
+    last eight graph-replayed decode steps (each step ends with the library's argmax kernel), per
+    kernel: dispatches per step, µs per step and mean duration (template arguments dropped).  In
+    a graph each dispatch starts when the previous one ends, so a duration includes its start-up;
+    the smallest ones show the per-dispatch floor."""
+    import csv
+    import re
+
+    rows = sorted(csv.DictReader(open(csv_path)), key=lambda r: int(r["Start_Timestamp"]))
+    dec = [i for i, r in enumerate(rows)
+           if "decode_kernel" in r["Kernel_Name"] and "true" in r["Kernel_Name"].split(",")[2]]
+    ends = [i for i, r in enumerate(rows)
+            if "argmax_kernel" in r["Kernel_Name"] and dec[0] < i <= dec[-1] + 64]
+    steps = list(zip(ends[:-1], ends[1:]))[-8:]
+    per: dict = {}
+    span = 0.0
+    for a, b in steps:
+        win = rows[a + 1: b + 1]
+        span += (int(win[-1]["End_Timestamp"]) - int(win[0]["Start_Timestamp"])) / 1e3
+        for r in win:
+            name = re.sub(r"\(.*", "", r["Kernel_Name"]).replace("void ", "")
+            name = re.sub(r"<.*", "", name)[:80]
+            d = per.setdefault(name, [0, 0.0])
+            d[0] += 1
+            d[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    n = len(steps)
+    table = sorted(({"kernel": k, "per_step": round(c / n, 1), "us_per_step": round(t / n, 1),
+                     "mean_us": round(t / c, 2)} for k, (c, t) in per.items()),
+                   key=lambda e: -e["us_per_step"])
+    res = {"csv": csv_path, "steps": n, "span_per_step_us": round(span / n, 1),
+           "dispatches_per_step": round(sum(c for c, _ in per.values()) / n, 1), "kernels": table}
+    log(f"steps {n}: span {res['span_per_step_us']} us, {res['dispatches_per_step']} dispatches")
+    for e in table:
+        log(f"  {e['per_step']:6.1f} x {e['us_per_step']:9.1f} us/step  mean {e['mean_us']:7.2f}  {e['kernel']}")
+    if out_path:
+        Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+        Path(out_path).write_text(json.dumps({"step_table": res}, indent=1))
+    return res
+
+
 def ceiling_legs(dev, out_path: str | None) -> dict:
     """Read ceilings of the INT8 decode's K/V stream on this GPU (include/int8kv_probe.h), next to
     the decode itself, all on one 1 GiB shuffled pool (65,536 INT8 blocks of 16 tokens x 4 kv
@@ -1068,6 +1109,8 @@ def main() -> int:
                          "layer pools rotated, and between the decode step's GEMMs), results to JSON")
     ap.add_argument("--trace-table", nargs=2, metavar=("CSV", "JSON"), default=None,
                     help="summarise a rocprofv3 kernel trace of --cold (CPU only) into JSON")
+    ap.add_argument("--step-table", nargs=2, metavar=("CSV", "JSON"), default=None,
+                    help="summarise a rocprofv3 kernel trace of --tpot-only (CPU only) into JSON")
     ap.add_argument("--ceiling", metavar="JSON", default=None,
                     help="only the read-ceiling probes of the decode's K/V stream, into JSON")
     ap.add_argument("--counter-run", choices=("warm", "cold", "cfg3"), default=None,
@@ -1101,6 +1144,9 @@ def main() -> int:
         return 2
     if args.trace_table:
         trace_table(*args.trace_table)
+        return 0
+    if args.step_table:
+        step_table(*args.step_table)
         return 0
 
     import torch
