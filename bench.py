@@ -159,15 +159,17 @@ def time_graph(fn, calls: int = 20, replays: int = 10, settle_ms: float = 30.0) 
 def settle(fn, batch: int = 20, min_ms: float = 100.0, tol: float = 0.01,
            max_ms: float = 4000.0) -> dict:
     """Runs ``fn`` back to back in event-timed batches of ``batch`` calls until the device has
-    been busy with it for at least ``min_ms`` and two consecutive batches agree within ``tol``
+    been busy with it for at least ``min_ms`` and the last three batches agree within ``tol``
     (or ``max_ms`` have passed).  Batches are enqueued eight at a time between host
     synchronisations, so the load is continuous.
 
     Why: on MI355X the first few ms of a sustained HBM-bound load run at full speed, then every
     launch slows by up to ~25 % for about 10 ms and recovers (rocprofv3 traces of this bench:
     calls 11-65 after the workload build, while the earlier calls and everything after run at
-    the steady-state duration).  A short warm-up leaves the timed loop inside that dip.  The
-    figures returned describe it: the first, slowest and last batch averages in microseconds."""
+    the steady-state duration); on some boxes the recovery takes longer (the headline call was
+    still at 199 us after 129 ms busy, then ran at 190 us).  A short warm-up leaves the timed loop
+    inside that dip.  The figures returned describe it: the first, slowest and last batch
+    averages in microseconds, and every eighth batch's."""
     import torch
 
     means, busy, calls = [], 0.0, 0
@@ -184,12 +186,14 @@ def settle(fn, batch: int = 20, min_ms: float = 100.0, tol: float = 0.01,
             busy += ms
             calls += batch
             means.append(ms / batch)
-        settled = busy >= min_ms and abs(means[-1] - means[-2]) <= tol * means[-2]
+        last = means[-3:]
+        settled = busy >= min_ms and max(last) - min(last) <= tol * min(last)
         if settled or busy >= max_ms:
             break
     return {"calls": calls, "busy_ms": round(busy, 2), "settled": bool(settled),
             "first_batch_us": round(means[0] * 1e3, 2), "slowest_batch_us": round(max(means) * 1e3, 2),
-            "last_batch_us": round(means[-1] * 1e3, 2)}
+            "last_batch_us": round(means[-1] * 1e3, 2),
+            "every_8th_batch_us": [round(m * 1e3, 1) for m in means[7::8]]}
 
 
 def write_legs(dev, cfg1_graph: bool = True) -> dict:
@@ -897,6 +901,171 @@ def step_table(csv_path: str, out_path: str | None) -> dict:
     return res
 
 
+def stamps_legs(dev, out_path: str | None) -> dict:
+    """Per-wave timelines from the measurement build (libint8kv_stamps.so, -DINT8KV_STAMPS; main()
+    points the ctypes binding at it): s_memrealtime stamps (10 ns ticks) at fixed points of each
+    wave (entry, plan or sequence length, first segment's block ids + first requests, query
+    operand, first tile's scores and P*V, segment done, end), read back after single calls.
+    Each figure is the median over 10 calls of a per-call statistic over the waves, in ns from the
+    call's first wave entry unless it is a phase length.  Legs:
+    * cfg3: the headline INT8 call (range layout): dispatch spread, plan, first tile, exits;
+    * ceiling: the load-only decode probe and the INT8 decode on the read-ceiling pool (256
+      equal ranges x 128 tiles; 64 sequences of 16,384 tokens): their exit spreads;
+    * cfg4 call: config 4's per-layer call, the last of 28 in a HIP graph, alone (pools
+      rotated) and after its layer's GEMMs;
+    * cfg2 B=1 x 512: the INT8 and BF16 split layout at 16 workgroups per (sequence, kv head)
+      and INT8's single-pass per-sequence layout: the phases of a one-tile wave.
+    The stamps change each kernel's schedule a little; they show where time goes, not the
+    product build's durations."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    import int8kv
+    from int8kv import _decode, _lib
+    from int8kv import synthetic as syn
+
+    lib = _lib.load()
+    buf = np.zeros(16384 * 10, np.uint64)
+
+    def collect(unit, run, reps=10):
+        out = []
+        for _ in range(reps):
+            _lib.check(getattr(lib, f"int8kv_stamps_clear_{unit}")(), "stamps_clear")
+            run()
+            torch.cuda.synchronize()
+            _lib.check(getattr(lib, f"int8kv_stamps_read_{unit}")(
+                buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "stamps_read")
+            st = buf.reshape(-1, 10).astype(np.int64)
+            out.append(st[st[:, 7] > 0].copy())
+        return out
+
+    def med(calls, fn):
+        return round(float(np.median([fn(st) for st in calls])), 0)
+
+    def timeline(calls):
+        """Range layout / probe: spreads and exits in ns."""
+        def rel(st, i):
+            return (st[:, i] - st[:, 0].min()) * 10
+        r = {"waves": med(calls, len),
+             "entry_last": med(calls, lambda st: rel(st, 0).max()),
+             "exit_first": med(calls, lambda st: rel(st, 7).min()),
+             "exit_p50": med(calls, lambda st: np.percentile(rel(st, 7), 50)),
+             "exit_last": med(calls, lambda st: rel(st, 7).max())}
+        r["finish_spread"] = r["exit_last"] - r["exit_p50"]
+        if calls[0][:, 1].any():
+            r["plan"] = med(calls, lambda st: np.median((st[:, 1] - st[:, 0]) * 10))
+        seg = [st[st[:, 9] > 0] for st in calls]
+        if len(seg[0]):
+            r["first_segment_entered"] = med(seg, lambda st: np.median((st[:, 9] - st[:, 0]) * 10))
+            r["first_scores_done"] = med(seg, lambda st: np.median((st[:, 4] - st[:, 0]) * 10))
+            r["body_p50"] = med(seg, lambda st: np.median((st[:, 7] - st[:, 9]) * 10))
+        # Entry per XCD (median over its waves, relative to the earliest XCD's): the XCDs' clock
+        # offsets and dispatch order.
+        def xcd(st):
+            m = [np.median(st[st[:, 8] == x, 0]) for x in range(8) if (st[:, 8] == x).any()]
+            return (max(m) - min(m)) * 10
+        r["xcd_entry_median_spread"] = med(calls, xcd)
+        return r
+
+    def phases(calls):
+        """Per-sequence / split layout: the phases of the median wave (ns)."""
+        seg = [st[st[:, 9] > 0] for st in calls]
+        names = (("sequence_length", 1, 0), ("stage_and_issue", 2, 9), ("query", 3, 2),
+                 ("k_scores_softmax", 4, 3), ("v_pv", 5, 4), ("rest_of_segment", 6, 5),
+                 ("state_to_barrier", 7, 6), ("entry_to_barrier", 7, 0))
+        return {n: med(seg, lambda st, a=a, b=b: np.median((st[:, a] - st[:, b]) * 10))
+                for n, a, b in names}
+
+    res = {"library": str(_lib.LIB_PATH.name)}
+    # cfg3
+    w = build_workload(dev)
+    call = lambda: int8kv.int8_paged_attention(w["q"], w["kc"], w["vc"], w["bt"], w["sl"], w["ks"], w["vs"])
+    settle(call, batch=5, min_ms=50.0)
+    res["cfg3_int8"] = timeline(collect("i8", call))
+    log(f"stamps cfg3: {res['cfg3_int8']}")
+    del w
+    torch.cuda.empty_cache()
+    # ceiling pool: load-only probe and the decode over the same blocks
+    R, T = 256, 128
+    NB = R * T * 2
+    pool = torch.empty(2, NB, 16, 4, 128, dtype=torch.int8, device=dev)
+    pool.view(-1).copy_(torch.randint(-127, 128, (pool.numel(),), device=dev, dtype=torch.int8,
+                                      generator=torch.Generator(device=dev).manual_seed(5)))
+    ids = torch.randperm(NB, generator=torch.Generator().manual_seed(6)).to(torch.int32).to(dev)
+    sink = torch.empty(1 << 20, dtype=torch.int32, device=dev)
+    stream = _lib.stream_handle(dev)
+    probe = lambda: _lib.check(lib.int8kv_probe_decode_loads(
+        pool[0].data_ptr(), pool[1].data_ptr(), NB, 4, ids.data_ptr(), ids.numel(), R, T, 1,
+        sink.data_ptr(), sink.numel(), stream), "probe_decode_loads")
+    settle(probe, batch=5, min_ms=30.0)
+    res["ceiling_probe"] = timeline(collect("probe", probe))
+    B, L = 64, 16384
+    bt = ids[: B * (L // 16)].view(B, L // 16).contiguous()
+    sl = torch.full((B,), L, dtype=torch.int32, device=dev)
+    q = torch.randn(B, 28, 128, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16).to(dev)
+    sc = torch.full((4,), 0.02, device=dev)
+    dec = lambda: int8kv.int8_paged_attention(q, pool[0], pool[1], bt, sl, sc, sc)
+    settle(dec, batch=5, min_ms=30.0)
+    res["ceiling_decode"] = timeline(collect("i8", dec))
+    log(f"stamps ceiling: probe {res['ceiling_probe']}, decode {res['ceiling_decode']}")
+    del pool, ids, sink, bt
+    torch.cuda.empty_cache()
+    # config 4's call, the last of 28 in a graph, alone and after its layer's GEMMs
+    cs = ColdSetup(dev)
+    for name, fns in (("cfg4_call_alone", [cs.op(i) for i in range(cs.NL)]),
+                      ("cfg4_call_after_gemms",
+                       [f for i in range(cs.NL) for f in (cs.gemms(i), cs.op(i))])):
+        g = capture_graph(fns)
+        settle(g.replay, batch=1, min_ms=30.0, max_ms=120.0)
+        res[name] = timeline(collect("i8", g.replay))
+        log(f"stamps {name}: {res[name]}")
+        del g
+    del cs
+    torch.cuda.empty_cache()
+    # config 2, B=1 x 512: one tile per wave
+    dist = syn.make_distribution(11)
+    ks, vs = syn.calibrate_scales(dist, seed=12)
+    ks_d, vs_d = ks.to(dev), vs.to(dev)
+    B, ctx = 1, 512
+    gq = torch.Generator().manual_seed(B * 7 + ctx)
+    pool_n = 2 * B * ctx // 16
+    bt = syn.random_block_tables([ctx] * B, pool_n, gq)
+    slots = syn.slot_mapping_for(bt, [ctx] * B)
+    kk, vv = syn.sample_kv(B * ctx, dist, gq)
+    q = syn.sample_query(B, gq).to(dev)
+    kc8 = torch.zeros(pool_n, 16, 4, 128, dtype=torch.int8, device=dev)
+    vc8 = torch.zeros_like(kc8)
+    int8kv.int8_kv_cache_write(kk.to(dev), vv.to(dev), kc8, vc8, slots.to(dev), ks_d, vs_d)
+    kc16 = torch.zeros(pool_n * 16, 4, 128, dtype=torch.bfloat16, device=dev)
+    vc16 = torch.zeros_like(kc16)
+    kc16[slots.to(dev)] = kk.to(dev)
+    vc16[slots.to(dev)] = vv.to(dev)
+    kc16, vc16 = kc16.view(pool_n, 16, 4, 128), vc16.view(pool_n, 16, 4, 128)
+    btd = bt.to(dev)
+    lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    ws = torch.empty(lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 64), dtype=torch.uint8,
+                     device=dev)
+    split = _lib.DECODE_ALL | _lib.DECODE_SPLIT_SEQUENCES
+    for name, unit, kc, vc, ksc, vsc, fl in (
+            ("cfg2_b1x512_int8_split16", "i8", kc8, vc8, ks_d, vs_d, split),
+            ("cfg2_b1x512_bf16_split16", "bf16", kc16, vc16, None, None, split)):
+        run = lambda: _decode.paged_decode(q, kc, vc, btd, lens, ksc, vsc, out, 16 * B, fl, ws, 0)
+        settle(run, batch=20, min_ms=20.0)
+        res[name] = phases(collect(unit, run))
+        log(f"stamps {name}: {res[name]}")
+    run = lambda: int8kv.int8_paged_attention(q, kc8, vc8, btd, lens, ks_d, vs_d)
+    settle(run, batch=20, min_ms=20.0)
+    res["cfg2_b1x512_int8_per_sequence"] = phases(collect("i8", run))
+    log(f"stamps cfg2_b1x512_int8_per_sequence: {res['cfg2_b1x512_int8_per_sequence']}")
+    if out_path:
+        Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+        Path(out_path).write_text(json.dumps({"stamps": res}, indent=1))
+    return res
+
+
 def ceiling_legs(dev, out_path: str | None) -> dict:
     """Read ceilings of the INT8 decode's K/V stream on this GPU (include/int8kv_probe.h), next to
     the decode itself, all on one 1 GiB shuffled pool (65,536 INT8 blocks of 16 tokens x 4 kv
@@ -1111,6 +1280,9 @@ def main() -> int:
                     help="summarise a rocprofv3 kernel trace of --cold (CPU only) into JSON")
     ap.add_argument("--step-table", nargs=2, metavar=("CSV", "JSON"), default=None,
                     help="summarise a rocprofv3 kernel trace of --tpot-only (CPU only) into JSON")
+    ap.add_argument("--stamps", metavar="JSON", default=None,
+                    help="only the per-wave timelines of the measurement build "
+                         "(libint8kv_stamps.so), into JSON")
     ap.add_argument("--ceiling", metavar="JSON", default=None,
                     help="only the read-ceiling probes of the decode's K/V stream, into JSON")
     ap.add_argument("--counter-run", choices=("warm", "cold", "cfg3"), default=None,
@@ -1148,6 +1320,8 @@ def main() -> int:
     if args.step_table:
         step_table(*args.step_table)
         return 0
+    if args.stamps:
+        os.environ["INT8KV_CTYPES"] = "1"  # the torch extension is linked to the product build
 
     import torch
 
@@ -1155,6 +1329,10 @@ def main() -> int:
     from int8kv import _decode, _lib, roofline
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.stamps:
+        from int8kv import _build
+
+        _lib.LIB_PATH = _build.STAMPS_LIB_PATH
     _lib.load()
     dev = torch.device("cuda:0")
     tpot_args = [int(x) for x in args.tpot_shape.split(",")]
@@ -1170,6 +1348,9 @@ def main() -> int:
         return 0
     if args.cold:
         cold_legs(dev, args.cold)
+        return 0
+    if args.stamps:
+        stamps_legs(dev, args.stamps)
         return 0
     if args.counter_run:
         counter_run(dev, args.counter_run)
@@ -1212,7 +1393,7 @@ def main() -> int:
 
     out = int8_call()
     torch.cuda.synchronize()
-    st = settle(int8_call)
+    st = settle(int8_call, min_ms=400.0)
     log(f"settle: {st}")
     ms = time_loop(int8_call, args.steps, args.warmup)
     ms_main = time_events(main_kernel, args.steps, args.warmup)

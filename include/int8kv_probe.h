@@ -6,6 +6,11 @@
  * against it as well as against the HBM peak).  They read device memory and write one word per
  * thread into `sink`; nothing else.  bench.py --cold uses the clock probe to read the shader
  * clock between the decode step's kernels.  Status codes as in int8kv.h (INT8KV_OK = 0).
+ *
+ * The measurement build libint8kv_stamps.so (never loaded by the operators) also exports
+ * int8kv_stamps_read_<unit>(void* dst, size_t bytes) and int8kv_stamps_clear_<unit>(void) for
+ * unit i8, bf16 and probe: the per-wave s_memrealtime stamps of paged_decode_kernels.h
+ * (bench.py --stamps).  libint8kv.so has neither.
  */
 #ifndef INT8KV_PROBE_H
 #define INT8KV_PROBE_H

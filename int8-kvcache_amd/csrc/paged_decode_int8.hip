@@ -11,3 +11,6 @@ int launch_cache_int8(const DecodeArgs& a, const HostPlan& hp, int query_dtype, 
 }
 
 }  // namespace int8kv
+
+// Measurement build only (empty otherwise): this unit's stamp buffer.
+INT8KV_STAMPS_ACCESSORS(i8)

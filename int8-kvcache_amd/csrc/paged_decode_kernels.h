@@ -28,6 +28,78 @@ constexpr int tile_blocks() {
 constexpr float kLazyRescale = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 
+// ---- Measurement build only: libint8kv_stamps.so, every source compiled with -DINT8KV_STAMPS
+// (bench.py --stamps).  Each wave of decode_kernel, group_kernel and probe_decode_kernel keeps
+// s_memrealtime stamps (the GPU's constant 100 MHz counter) in registers at fixed points and
+// stores them once, at its end, into its translation unit's g_stamps (slot = workgroup x waves
+// per workgroup + wave); int8kv_stamps_read_<unit> copies them out.  Stamps:
+//   0 entry; 1 sequence lengths read (group) / plan made (ranges); 2 first segment: its block
+//   ids staged and its first tiles requested; 3 its query operand built; 4 its first tile's
+//   scores done (K arrived and dequantised); 5 that tile's P*V done (V arrived); 6 the
+//   segment's tiles done; 7 end (ranges, probe) / after the workgroup barrier (group); 8 the
+//   wave's XCD (HW_REG_XCC_ID); 9 first segment entered.
+// In the product build (no INT8KV_STAMPS) every macro below is empty.
+#ifdef INT8KV_STAMPS
+constexpr int kStampSlots = 10;
+constexpr int kStampWaves = 16384;
+struct Stamps {
+  unsigned long long t[kStampSlots];
+};
+__device__ unsigned long long g_stamps[kStampWaves * kStampSlots];
+__device__ __forceinline__ unsigned long long stamp_now() {
+  __builtin_amdgcn_sched_barrier(0);
+  const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+  __builtin_amdgcn_sched_barrier(0);
+  return t;
+}
+__device__ __forceinline__ void store_stamps(Stamps& st, int waves_per_wg, int wave, int lane) {
+  // HW_REG_XCC_ID (hardware register 20), bits [3:0]: the XCD the wave runs on.
+  st.t[8] = (unsigned)__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u;
+  const long long slot =
+      (((long long)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * waves_per_wg +
+      wave;
+  if (lane == 0 && slot < kStampWaves) {
+#pragma unroll
+    for (int i = 0; i < kStampSlots; ++i) g_stamps[slot * kStampSlots + i] = st.t[i];
+  }
+}
+#define INT8KV_STAMPS_DECL Stamps stamps_{};
+#define INT8KV_STAMP(i) (stamps_.t[i] = stamp_now())
+#define INT8KV_STAMP_ONCE(i) \
+  do {                       \
+    if (stamps_.t[i] == 0) stamps_.t[i] = stamp_now(); \
+  } while (0)
+#define INT8KV_STAMP_SEG(i)                                        \
+  do {                                                             \
+    if (stamps_p && stamps_p->t[i] == 0) stamps_p->t[i] = stamp_now(); \
+  } while (0)
+#define INT8KV_STAMPS_PARAM , Stamps* stamps_p = nullptr
+#define INT8KV_STAMPS_ARG , &stamps_
+#define INT8KV_STAMPS_ARG_NO_GROUP , nullptr, nullptr, nullptr, &stamps_
+#define INT8KV_STAMPS_STORE(waves_per_wg, wave, lane) store_stamps(stamps_, waves_per_wg, wave, lane)
+#define INT8KV_STAMPS_ACCESSORS(unit)                                                          \
+  extern "C" int int8kv_stamps_read_##unit(void* dst, size_t bytes) {                         \
+    if (bytes > sizeof(int8kv::g_stamps)) return 1;                                            \
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(int8kv::g_stamps), bytes, 0,               \
+                                    hipMemcpyDeviceToHost);                                    \
+  }                                                                                            \
+  extern "C" int int8kv_stamps_clear_##unit() {                                                \
+    static unsigned long long zero[int8kv::kStampWaves * int8kv::kStampSlots];                 \
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(int8kv::g_stamps), zero, sizeof(zero), 0,        \
+                                  hipMemcpyHostToDevice);                                      \
+  }
+#else
+#define INT8KV_STAMPS_DECL
+#define INT8KV_STAMP(i) ((void)0)
+#define INT8KV_STAMP_ONCE(i) ((void)0)
+#define INT8KV_STAMP_SEG(i) ((void)0)
+#define INT8KV_STAMPS_PARAM
+#define INT8KV_STAMPS_ARG
+#define INT8KV_STAMPS_ARG_NO_GROUP
+#define INT8KV_STAMPS_STORE(waves_per_wg, wave, lane) ((void)0)
+#define INT8KV_STAMPS_ACCESSORS(unit)
+#endif
+
 struct DecodeArgs {
   const char* q;
   int64_t q_sb, q_sh;  // element strides
@@ -919,7 +991,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
                                             int64_t L, int vh, int64_t ta, int64_t tb,
                                             bool full, int64_t rec, int lane,
                                             float* g_acc = nullptr, float* g_m = nullptr,
-                                            float* g_l = nullptr) {
+                                            float* g_l = nullptr INT8KV_STAMPS_PARAM) {
   typedef typename MfmaOp<CACHE>::T OpT;
   const int li = lane & 15;
   const int lg = lane >> 4;
@@ -998,7 +1070,9 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     QueryRaw<QT, HD> qraw;
     issue_query<QT, HD, PAIR, PAD>(a, b, hm, li, lg, qraw);
     chunk_prologue();
+    INT8KV_STAMP_SEG(2);
     s_scale = finish_query<CACHE, QT, QQ, HD, PAIR, GROUP>(a, qraw, ksc, qop, qlo, q8op);
+    INT8KV_STAMP_SEG(3);
   }
 
   // Tile t + d (buffer d): scores, refill K with tile t + d + DEPTH, P*V, refill V.  refill is a
@@ -1011,12 +1085,14 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     const int valid = valid_of(t + d);
     tile_scores<CACHE, NB, QQ, HD, QSPLIT>(kt[d], qop, qlo, q8op,
                                            acc, m_run, l_part, valid, lg, s_scale, pop);
+    INT8KV_STAMP_SEG(4);
     if (refill) {
       blocks_of(t + d + DEPTH, ph[d]);
       issue_k<CACHE, NB, NT, HD, PAD>(kt[d], kb, ph[d], a, li, lg);
     }
     __builtin_amdgcn_sched_barrier(0);
     tile_pv<CACHE, NB, HD>(vt[d], pop, acc, valid, lg);
+    INT8KV_STAMP_SEG(5);
     if (refill) issue_v<CACHE, NB, NT, HD, PAD>(vt[d], vb, ph[d], a, li, lg);
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -1042,7 +1118,9 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
         tile_scores<CACHE, NB, QQ, HD, QSPLIT>(kt[d], qop, qlo,
                                                q8op, acc, m_run, l_part, valid, lg, s_scale,
                                        pop);
+        INT8KV_STAMP_SEG(4);
         tile_pv<CACHE, NB, HD>(vt[d], pop, acc, valid, lg);
+        INT8KV_STAMP_SEG(5);
       }
     }
     if (c1 >= tb) break;
@@ -1051,6 +1129,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     chunk_prologue();
   }
 
+  INT8KV_STAMP_SEG(6);
   l_part = rows_sum(l_part);
   if constexpr (PAIR) {
     // Columns li < 2G; a column's rows are its own kv head's half of the 128 (lg / 2 = 0 for
@@ -1155,9 +1234,12 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(de
   const int kvh = blockIdx.y * W + (HALVES == 1 ? wave : wave % W);  // the wave's (pair of) kv heads
   const int kv0 = PAIR ? 2 * kvh : kvh;  // first kv head of the wave
   const int half = HALVES == 1 ? 0 : wave / W;
+  INT8KV_STAMPS_DECL
+  INT8KV_STAMP(0);
 
   const int64_t L0 = seq_len_of(a, lane);
   const Plan plan = make_plan(a, lane, L0);
+  INT8KV_STAMP(1);
   // One range per workgroup, or two: ranges 2x and 2x + 1 when paired, else x and x + grid.x
   // (the second only when the batch needs more ranges than there are workgroups).
   int64_t r = blockIdx.x;
@@ -1219,13 +1301,17 @@ __global__ __launch_bounds__(256 * HALVES) __attribute__((amdgpu_waves_per_eu(de
           a.ws_cut[4 * r] = base + j;
           a.ws_cut[4 * r + 1] = first + nb - 1;
         }
+        INT8KV_STAMP_ONCE(9);
         run_segment<CACHE, QT, NT, QQ, HD, DEPTH, false, PAIR, PAD>(
-            a, s_ids[wave], base + j, Lb, kv0, ta, te, full, 2 * r + cut_slot(ta), lane);
+            a, s_ids[wave], base + j, Lb, kv0, ta, te, full, 2 * r + cut_slot(ta),
+            lane INT8KV_STAMPS_ARG_NO_GROUP);
       }
     }
     if (chunk_end >= u1 && !last_range) break;
     cum = chunk_end;
   }
+  INT8KV_STAMP(7);
+  INT8KV_STAMPS_STORE(HALVES * W, wave, lane);
 }
 
 // Short sequences, one workgroup per (sequence b = blockIdx.x, kv head blockIdx.y): its
@@ -1256,7 +1342,10 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
   const int lg = lane >> 4;
   const int64_t b = blockIdx.x;
   const int vh = blockIdx.y;  // grid head (head_map)
+  INT8KV_STAMPS_DECL
+  INT8KV_STAMP(0);
   const int64_t L = seq_len_uniform(a, b);  // first: every later step waits for it
+  INT8KV_STAMP(1);
   const HeadMap hm = head_map(a, vh);
   const int G = hm.g;
   const int64_t n = tiles_of(a, L);
@@ -1278,8 +1367,10 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
   const int64_t ta = t0 + v * span / NW;
   const int64_t tb = t0 + (v + 1) * span / NW;
   if (ta < tb) {
+    INT8KV_STAMP(9);
     run_segment<CACHE, QT, false, QQ, HD, 2, true, false, PAD>(
-        a, s_ids[wave], b, L, vh, ta, tb, false, 0, lane, s_acc[wave], s_m[wave], s_l[wave]);
+        a, s_ids[wave], b, L, vh, ta, tb, false, 0, lane, s_acc[wave], s_m[wave],
+        s_l[wave] INT8KV_STAMPS_ARG);
   } else if (li < G) {  // no tiles for this wave: the neutral state
 #pragma unroll
     for (int j = 0; j < HD / 4; ++j) s_acc[wave][j * kWave + lane] = 0.0f;
@@ -1289,6 +1380,8 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
     }
   }
   __syncthreads();
+  INT8KV_STAMP(7);
+  INT8KV_STAMPS_STORE(NW, wave, lane);
   // Online-softmax merge of the NW states (exp2 domain), as merge_kernel does for records.  The
   // four row groups rr of the accumulator layout are independent, so waves 0..3 take one each
   // (head_dim elements HD/4 lg + HD/16 rr + [0, HD/16) of lane (li, lg)): wave 0 merging all

@@ -54,6 +54,8 @@ probe_decode_kernel(DecodeArgs a, int32_t tiles, uint32_t* sink) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int li = lane & 15, lg = lane >> 4;
   const int64_t r = blockIdx.x;  // range: row r of the block-id table, 2 x tiles entries
+  INT8KV_STAMPS_DECL
+  INT8KV_STAMP(0);
   const char* kb = a.kc + (int64_t)wave * a.kc_sh;
   const char* vb = a.vc + (int64_t)wave * a.vc_sh;
   int32_t* ids = s_ids[wave];
@@ -78,6 +80,7 @@ probe_decode_kernel(DecodeArgs a, int32_t tiles, uint32_t* sink) {
       issue_k<kI8, NB, NT, HD>(kt[d], kb, ph[d], a, li, lg);
       issue_v<kI8, NB, NT, HD>(vt[d], vb, ph[d], a, li, lg);
     }
+    INT8KV_STAMP_ONCE(2);
     int64_t t = c0;
     for (; t + kProbeDepth - 1 < c1; t += kProbeDepth) {
 #pragma unroll
@@ -121,6 +124,8 @@ probe_decode_kernel(DecodeArgs a, int32_t tiles, uint32_t* sink) {
     for (int d = 0; d < kProbeDepth; ++d) acc ^= kt[d].k[0][0][1] ^ vt[d].v[0][0][1];
   }
   sink[blockIdx.x * blockDim.x + threadIdx.x] = acc;
+  INT8KV_STAMP(7);
+  INT8KV_STAMPS_STORE(kProbeWaves, wave, lane);
 }
 
 // One wave per workgroup: shader-clock cycles (s_memtime) over a window of the 100 MHz real-time
@@ -143,6 +148,8 @@ __global__ __launch_bounds__(64) void probe_clock_kernel(uint64_t* out, uint32_t
 }  // namespace int8kv
 
 using namespace int8kv;
+
+INT8KV_STAMPS_ACCESSORS(probe)
 
 extern "C" int int8kv_probe_stream_read(const void* src, size_t bytes, int32_t non_temporal,
                                         uint32_t* sink, int32_t sink_words, void* stream) {

@@ -86,19 +86,28 @@ def _torch_ext_flags():
 
 OBJ_CACHE = PKG_DIR.parent / "build"  # objects kept by incremental builds (git-ignored)
 
+# The measurement build: the library with the units below compiled with -DINT8KV_STAMPS (per-wave
+# s_memrealtime stamps in the INT8 and BF16 decode kernels and the load probe, read back through
+# int8kv_stamps_read_<unit>; bench.py --stamps) and every other unit shared with the product
+# build.  Never loaded by the operators.
+STAMPS_LIB_PATH = PKG_DIR / "libint8kv_stamps.so"
+STAMPS_SOURCES = ["paged_decode_int8.hip", "paged_decode_bf16.hip", "read_probe.hip"]
 
-def build_library(verbose: bool = False, torch_ext: bool = True, incremental: bool = False) -> Path:
+
+def build_library(verbose: bool = False, torch_ext: bool = True, incremental: bool = False,
+                  stamps: bool = True) -> Path:
     """Compiles every HIP source into LIB_PATH and the torch extension into EXT_PATH: one
     compiler process per source, in parallel, then the links.  By default everything is rebuilt
     in a temporary directory; ``incremental`` keeps the objects in OBJ_CACHE and recompiles only
     the sources older than their object or than any header they may include (a developer's
-    edit-build loop)."""
+    edit-build loop).  ``stamps``: also link the measurement build, STAMPS_LIB_PATH (its
+    STAMPS_SOURCES compiled once more, in the same parallel batch)."""
     from concurrent.futures import ThreadPoolExecutor
 
     hipcc = hipcc_path()
     if incremental:
-        OBJ_CACHE.mkdir(parents=True, exist_ok=True)
         obj_dir = OBJ_CACHE
+        obj_dir.mkdir(parents=True, exist_ok=True)
     else:
         obj_dir = Path(tempfile.mkdtemp(prefix="int8kv_build_"))
     headers = [*CSRC_DIR.glob("*.h"), *INCLUDE_DIR.glob("*.h")]
@@ -114,6 +123,11 @@ def build_library(verbose: bool = False, torch_ext: bool = True, incremental: bo
         objs = [obj_dir / (Path(s).stem + ".o") for s in SOURCES]
         cmds = [[hipcc, *compile_flags, f"-I{INCLUDE_DIR}", "-c", str(CSRC_DIR / s), "-o", str(o)]
                 for s, o in zip(SOURCES, objs) if stale(CSRC_DIR / s, o)]
+        stamp_objs = {s: obj_dir / (Path(s).stem + "_stamps.o") for s in STAMPS_SOURCES}
+        if stamps:
+            cmds += [[hipcc, *compile_flags, "-DINT8KV_STAMPS", f"-I{INCLUDE_DIR}", "-c",
+                      str(CSRC_DIR / s), "-o", str(o)]
+                     for s, o in stamp_objs.items() if stale(CSRC_DIR / s, o)]
         ext_obj = obj_dir / "torch_ops.o"
         if torch_ext:
             cflags, lflags = _torch_ext_flags()
@@ -127,6 +141,12 @@ def build_library(verbose: bool = False, torch_ext: bool = True, incremental: bo
         _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)],
              verbose)
         os.replace(tmp, LIB_PATH)
+        if stamps:
+            mixed = [stamp_objs.get(s, o) for s, o in zip(SOURCES, objs)]
+            tmp = STAMPS_LIB_PATH.with_suffix(".so.tmp")
+            _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, mixed), "-o",
+                  str(tmp)], verbose)
+            os.replace(tmp, STAMPS_LIB_PATH)
         if torch_ext:
             tmp = EXT_PATH.with_suffix(".so.tmp")
             _run(["g++", "-shared", str(ext_obj), *lflags, "-o", str(tmp)], verbose)
@@ -138,4 +158,5 @@ def build_library(verbose: bool = False, torch_ext: bool = True, incremental: bo
 
 
 if __name__ == "__main__":
-    print(build_library(verbose="-v" in sys.argv, incremental="--incremental" in sys.argv))
+    print(build_library(verbose="-v" in sys.argv, incremental="--incremental" in sys.argv,
+                        stamps="--no-stamps" not in sys.argv))

@@ -71,12 +71,19 @@ def load() -> ctypes.CDLL:
     global _lib
     if _lib is not None:
         return _lib
-    if not LIB_PATH.exists():
+    _lib = bind(LIB_PATH)
+    return _lib
+
+
+def bind(path: Path) -> ctypes.CDLL:
+    """Loads a build of the library (libint8kv.so, or the measurement build) and declares the
+    C ABI's argument types on it."""
+    if not path.exists():
         raise RuntimeError(
-            f"{LIB_PATH} is not built; run `python -m int8kv._build` or "
+            f"{path} is not built; run `python -m int8kv._build` or "
             "__graft_entry__.build() first (there is no non-HIP implementation)"
         )
-    lib = ctypes.CDLL(str(LIB_PATH))
+    lib = ctypes.CDLL(str(path))
     i32, i64, u32, f32, sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_float, ctypes.c_size_t
     lib.int8kv_cache_write.restype = ctypes.c_int
     lib.int8kv_cache_write.argtypes = [
@@ -132,7 +139,12 @@ def load() -> ctypes.CDLL:
     lib.int8kv_probe_decode_loads.restype = ctypes.c_int
     lib.int8kv_probe_decode_loads.argtypes = [_vp, _vp, i64, i32, _vp, i64, i32, i32, i32, _vp, i64,
                                               _vp]
-    _lib = lib
+    if hasattr(lib, "int8kv_stamps_read_i8"):  # the measurement build
+        for unit in ("i8", "bf16", "probe"):
+            getattr(lib, f"int8kv_stamps_read_{unit}").restype = ctypes.c_int
+            getattr(lib, f"int8kv_stamps_read_{unit}").argtypes = [_vp, sz]
+            getattr(lib, f"int8kv_stamps_clear_{unit}").restype = ctypes.c_int
+            getattr(lib, f"int8kv_stamps_clear_{unit}").argtypes = []
     return lib
 
 
