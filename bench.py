@@ -907,8 +907,10 @@ def stamps_legs(dev, out_path: str | None) -> dict:
     wave (entry, plan or sequence length, first segment's block ids + first requests, query
     operand, first tile's scores and P*V, segment done, end), read back after single calls.
     Each figure is the median over 10 calls of a per-call statistic over the waves, in ns from the
-    call's first wave entry unless it is a phase length.  Legs:
-    * cfg3: the headline INT8 call (range layout): dispatch spread, plan, first tile, exits;
+    median entry of the wave's XCD unless it is a phase length.  Legs:
+    * cfg3: the headline INT8 call (range layout): dispatch spread, plan, first tile, exits (by
+      XCD, and their call-to-call correlation); and with a caller's 512 ranges (two per
+      workgroup), the exits of each workgroup's first and second range;
     * ceiling: the load-only decode probe and the INT8 decode on the read-ceiling pool (256
       equal ranges x 128 tiles; 64 sequences of 16,384 tokens): their exit spreads;
     * cfg4 call: config 4's per-layer call, the last of 28 in a HIP graph, alone (pools
@@ -938,17 +940,26 @@ def stamps_legs(dev, out_path: str | None) -> dict:
             _lib.check(getattr(lib, f"int8kv_stamps_read_{unit}")(
                 buf.ctypes.data_as(ctypes.c_void_p), buf.nbytes), "stamps_read")
             st = buf.reshape(-1, 10).astype(np.int64)
+            st = np.concatenate([st, np.arange(len(st))[:, None]], axis=1)  # column 10: slot
             out.append(st[st[:, 7] > 0].copy())
         return out
 
     def med(calls, fn):
         return round(float(np.median([fn(st) for st in calls])), 0)
 
-    def timeline(calls):
-        """Range layout / probe: spreads and exits in ns."""
+    def timeline(calls, halves=False):
+        """Range layout / probe: spreads and exits in ns.  The XCDs' real-time counters are
+        offset from each other by up to ~2 us, so cross-wave times are taken from the median
+        entry of the wave's own XCD (all XCDs receive their first workgroups within a few hundred
+        ns of each other); the offsets' spread is reported as xcd_entry_median_spread."""
         def rel(st, i):
-            return (st[:, i] - st[:, 0].min()) * 10
+            origin = np.zeros(len(st), np.int64)
+            for x in np.unique(st[:, 8]):
+                sel = st[:, 8] == x
+                origin[sel] = int(np.median(st[sel, 0]))
+            return (st[:, i] - origin) * 10
         r = {"waves": med(calls, len),
+             "entry_first": med(calls, lambda st: rel(st, 0).min()),
              "entry_last": med(calls, lambda st: rel(st, 0).max()),
              "exit_first": med(calls, lambda st: rel(st, 7).min()),
              "exit_p50": med(calls, lambda st: np.percentile(rel(st, 7), 50)),
@@ -967,6 +978,22 @@ def stamps_legs(dev, out_path: str | None) -> dict:
             m = [np.median(st[st[:, 8] == x, 0]) for x in range(8) if (st[:, 8] == x).any()]
             return (max(m) - min(m)) * 10
         r["xcd_entry_median_spread"] = med(calls, xcd)
+        # Exit (ns from the XCD's median entry) by XCD, and how well one call's per-wave exits
+        # predict the next call's (Pearson correlation over the waves both stored).
+        r["exit_median_by_xcd"] = [med(calls, lambda st, x=x: np.median(rel(st, 7)[st[:, 8] == x]))
+                                   for x in range(8)]
+        corr = []
+        for a, b in zip(calls[:-1], calls[1:]):
+            ea = dict(zip(a[:, 10], rel(a, 7)))
+            eb = dict(zip(b[:, 10], rel(b, 7)))
+            both = sorted(set(ea) & set(eb))
+            corr.append(np.corrcoef([ea[k] for k in both], [eb[k] for k in both])[0, 1])
+        r["exit_call_to_call_corr"] = round(float(np.median(corr)), 3)
+        if halves:
+            # Two ranges per workgroup (waves 0-3: the first, 4-7: the second, which holds the
+            # pair's smaller share): median exit of each.
+            for h, name in ((0, "exit_p50_first_range"), (1, "exit_p50_second_range")):
+                r[name] = med(calls, lambda st, h=h: np.median(rel(st, 7)[(st[:, 10] % 8 >= 4) == bool(h)]))
         return r
 
     def phases(calls):
@@ -985,6 +1012,17 @@ def stamps_legs(dev, out_path: str | None) -> dict:
     settle(call, batch=5, min_ms=50.0)
     res["cfg3_int8"] = timeline(collect("i8", call))
     log(f"stamps cfg3: {res['cfg3_int8']}")
+    # The paired layout (a caller's 512 ranges: two ranges per 8-wave workgroup, the first taking
+    # 62.5 % of the pair's units): how the pair's two ranges finish.
+    out = torch.empty_like(w["q"])
+    ws = torch.empty(lib.int8kv_decode_workspace_bytes(28, 4, 128, 16, 512), dtype=torch.uint8,
+                     device=dev)
+    pcall = lambda: _decode.paged_decode(w["q"], w["kc"], w["vc"], w["bt"], w["sl"], w["ks"],
+                                         w["vs"], out, 512, _lib.DECODE_ALL, ws)
+    settle(pcall, batch=5, min_ms=50.0)
+    res["cfg3_int8_paired_512"] = timeline(collect("i8", pcall), halves=True)
+    log(f"stamps cfg3 paired: {res['cfg3_int8_paired_512']}")
+    del out, ws
     del w
     torch.cuda.empty_cache()
     # ceiling pool: load-only probe and the decode over the same blocks
