@@ -152,3 +152,18 @@ def test_random_configuration_split_layout(cuda, seed):
                                       v16.float().numpy(), c.block_tables.numpy(),
                                       c.seq_lens.numpy())
         _check(out16, ref16, lens, "split bf16 " + what)
+
+
+@pytest.mark.parametrize("seed", range(400, 416))
+def test_random_configuration_padded_head_dims_and_wide_groups(cuda, seed):
+    """The random draws at head_dims between the kernels' 64 / 128 / 256 (any multiple of 16, run
+    on the next kernel with the padding masked) and GQA groups above 16 (several MFMA column tiles
+    per kv head), with the drawn block size, dtypes, split count, impl and quantize_q."""
+    p = _draw(seed)
+    d = [16, 32, 48, 80, 96, 112, 144, 160, 176, 192, 208, 224, 240][seed % 13]
+    hq, hkv = [(28, 4), (34, 2), (20, 1), (48, 3), (71, 1), (40, 8), (16, 16), (64, 2)][seed % 8]
+    p.update(hq=hq, hkv=hkv, d=d)
+    p["lens"] = [min(n, 3000) for n in p["lens"]][:24]
+    if d > 128 and p["qdtype"] == torch.float32 and p["bf16"]:
+        p["qdtype"] = torch.bfloat16
+    _run(cuda, p, seed)
