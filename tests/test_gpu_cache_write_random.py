@@ -2,7 +2,7 @@
 
 Each case draws the token count (0-3000, some slots -1 or past the cache, which the writes skip),
 kv heads (1, 2, 3, 4 or 8), head_dim (64, 128, 256, and 72 / 136 for the static write's narrow
-kernels), the cache block size (16-64), the source dtype (bf16, fp16, fp32; K and V of one
+kernels; a second set at the other multiples of 16 from 16 to 240), the cache block size (16-64), the source dtype (bf16, fp16, fp32; K and V of one
 dtype), the slot dtype (int32 / int64), source views with padded token or head strides, and the
 value scale (data spanning small and large magnitudes, so some quotients clamp), then runs the
 static write (``int8_kv_cache_write``) and the dynamic per-(token, head) write
@@ -49,7 +49,20 @@ def _source(T, hkv, d, dtype, view, g):
 
 @pytest.mark.parametrize("seed", range(20))
 def test_random_writes(cuda, seed):
+    _run(cuda, _draw(seed), seed)
+
+
+@pytest.mark.parametrize("seed", range(50, 62))
+def test_random_writes_other_head_dims(cuda, seed):
+    """The random draws at the other multiples of 16 the decode takes (16-240): wide kernels with
+    1-15 lanes per row (not a power of two: the head-major map at every size), and the dynamic
+    write where head_dim / 8 is a power of two (16, 32)."""
     p = _draw(seed)
+    p["d"] = [16, 32, 48, 80, 96, 112, 144, 160, 176, 192, 208, 240][seed % 12]
+    _run(cuda, p, seed)
+
+
+def _run(cuda, p, seed):
     what = f"seed {seed}: {p}"
     T, hkv, d, bs = p["T"], p["hkv"], p["d"], p["bs"]
     g = torch.Generator().manual_seed(seed)
