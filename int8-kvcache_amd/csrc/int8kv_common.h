@@ -61,12 +61,17 @@ __device__ __forceinline__ void load8_f32(const void* p, float (&x)[8]) {
 // about ten VALU instructions, so the kernels take a shortcut that provably gives the same code:
 //   q0 = RN(x * r) with r = RN(1 / s):  |r - 1/s| <= 2^-24 / s, so with the rounding of the product
 //   and of the divide  |q0 - RN(x/s)| <= 3.0000002 * 2^-24 |x/s|  (r normal: s < 2^100).
-//   qc = q0 clamped to [-256, 256].  When qc lies more than 2^-20 |qc| from every half-integer,
-//   RN(x/s) lies in the same open interval between half-integers and rounds to rint(qc) under either
-//   rounding rule (they differ only at half-integers); quotients past +-256, infinities included,
-//   clamp to +-127 either way, and a NaN gives -127 on both paths (fmaxf first returns the bound).
-// The rest (about 1e-4 of the elements, all of them when s >= 2^100) are divided.  The argument and
-// an exhaustive check over every bf16 and fp16 value: tests/test_quant_fast_path.py.
+//   qc = q0 clamped to [-127, 127], n = rint(qc), and |qc - n| is exact (Sterbenz).
+//   * |q0| > 127 (infinities included): qc = n = +-127, and RN(x/s) lies beyond +-126.5, so the
+//     code is +-127 either way; a NaN gives -127 on both paths (fmaxf first returns the bound).
+//   * |q0| <= 127: |q0 - RN(x/s)| <= 2.28e-5 < 127 * 2^-20.  When |qc - n| < 0.5 - 127 * 2^-20, qc
+//     lies farther than that from every half-integer, so RN(x/s) lies in the same open interval
+//     between half-integers and rounds to n under either rounding rule (they differ only at
+//     half-integers).
+// The rest (about 2.4e-4 of the elements, all of them when s >= 2^100) are divided.  Clamping
+// before rounding and a constant window keep this to five VALU instructions per element before
+// packing (the relative window 2^-20 |qc| and a second clamp after rounding took two more).  The
+// argument and an exhaustive check over every bf16 and fp16 value: tests/test_quant_fast_path.py.
 struct QuantScale {
   float s;    // the scale (already floored at 1e-6)
   float r;    // RN(1 / s)
@@ -75,15 +80,17 @@ struct QuantScale {
 
 __device__ __forceinline__ QuantScale quant_scale(float s) { return {s, 1.0f / s, s < 0x1p100f}; }
 
+// Distance from rint(qc) below which the shortcut keeps it: 0.5 - 127 * 2^-20 (exact in fp32).
+constexpr float kKeepBelow = 0.5f - 127.0f * 0x1p-20f;
+
 // The shortcut code of x (as a float in [-127, 127]); sets `divide` when x needs the divide.
 __device__ __forceinline__ float code_shortcut(float x, float r, bool& divide) {
 #pragma clang fp contract(off)
   const float q0 = x * r;
-  const float qc = fminf(fmaxf(q0, -256.0f), 256.0f);
+  const float qc = fminf(fmaxf(q0, -127.0f), 127.0f);
   const float n = rintf(qc);
-  const float t = __builtin_fmaf(fabsf(qc), 0x1p-20f, fabsf(qc - n));
-  divide = !(t < 0.5f);
-  return fminf(fmaxf(n, -127.0f), 127.0f);
+  divide = !(fabsf(qc - n) < kKeepBelow);
+  return n;
 }
 
 // The codes through the correctly rounded divide (the definition the shortcut reproduces).

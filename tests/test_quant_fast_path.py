@@ -1,23 +1,24 @@
 """The cache-write kernels' quantisation shortcut, checked exhaustively on the CPU.
 
 The kernels need clamp(rint(RN(x / s)), -127, 127), with RN the correctly rounded fp32 divide.
-They compute q0 = RN(x * r) with r = RN(1 / s), clamp it to qc in [-256, 256], and keep
-rint(qc) unless qc lies within 2^-20 |qc| of a half-integer, in which case they divide (and for
-every element when s >= 2^100, where r could be subnormal).
+They compute q0 = RN(x * r) with r = RN(1 / s), clamp it to qc in [-127, 127], and keep
+n = rint(qc) unless |qc - n| >= 0.5 - 127 * 2^-20 (qc within 127 * 2^-20 of a half-integer), in
+which case they divide (and for every element when s >= 2^100, where r could be subnormal).
 
 Why that is exact: |r - 1/s| <= 2^-24 / s, so |x r - x/s| <= 2^-24 |x/s|; the product and the
 divide each round by at most 2^-24 relative; hence |q0 - RN(x/s)| <= 3.0000002 * 2^-24 |x/s|,
-well inside 2^-20 |q0|.  When no half-integer lies that close to q0, RN(x/s) is in the same open
-interval between consecutive half-integers as q0 and rounds to the same integer.  Quotients
-beyond +-256 (infinities included) clamp to +-127 either way, and a NaN becomes -127 on both
-paths: fmaxf/fminf return the non-NaN operand, and the lower bound is applied first.  The same boundary argument holds for the dynamic
-write's half-away-from-zero rounding (rint and half-away differ only at half-integers).
+at most 2.28e-5 while |q0| <= 127, well inside 127 * 2^-20 = 1.21e-4.  When no half-integer lies
+that close to qc, RN(x/s) is in the same open interval between consecutive half-integers and
+rounds to the same integer.  When |q0| > 127 (infinities included) qc = n = +-127 and RN(x/s) lies
+beyond +-126.5, so the code is +-127 either way; a NaN becomes -127 on both paths: fmaxf/fminf
+return the non-NaN operand, and the lower bound is applied first.  |qc - n| is exact (Sterbenz).
+The same boundary argument holds for the dynamic write's half-away-from-zero rounding (rint and
+half-away differ only at half-integers).
 
 This file restates the kernels' steps in numpy float32 (each numpy float32 operation is one
-correctly rounded IEEE operation, like the GPU's; the kernels' single FMA is evaluated in float64,
-where it is exact whenever the comparison can be affected) and compares them with the divide for
-every finite bf16 and fp16 value against a few hundred scales, including the reference's
-calibrated Qwen scales and scales chosen to put quotients on and next to half-integers.
+correctly rounded IEEE operation, like the GPU's) and compares them with the divide for every
+finite bf16 and fp16 value against a few hundred scales, including the reference's calibrated
+Qwen scales and scales chosen to put quotients on and next to half-integers.
 """
 
 from __future__ import annotations
@@ -59,12 +60,12 @@ def _fast_codes(x, s):
     r = (F32(1) / s).astype(F32)
     with np.errstate(over="ignore", invalid="ignore"):
         q0 = (x * r).astype(F32)
-    qc = _clamp(q0, -256, 256)
+    qc = _clamp(q0, -127, 127)
     n = np.rint(qc)
     d = np.abs(qc - n).astype(F32)
-    t = (d.astype(np.float64) + np.abs(qc).astype(np.float64) * 2.0 ** -20).astype(F32)
-    slow = ~(t < F32(0.5)) | (s >= F32(2.0 ** 100))
-    return _clamp(n, -127, 127), slow
+    keep_below = F32(0.5) - F32(127 * 2.0 ** -20)  # exact in float32, as in the kernels
+    slow = ~(d < keep_below) | (s >= F32(2.0 ** 100))
+    return n, slow
 
 
 def _scales(seed=0):
@@ -122,3 +123,18 @@ def test_special_values():
     assert np.array_equal(fast, _exact_codes(x, s, half_away=True))
     _, slow = _fast_codes(np.array([1.0, 2.0], F32), F32(2.0 ** 101))
     assert slow.all()  # reciprocal could be subnormal: always divide
+
+
+def test_the_window_is_needed():
+    """Without the window (keeping rint(qc) whenever |qc - n| < 0.5) some bf16 values and scales
+    round differently from the divide: the window is what makes the shortcut exact."""
+    x = _all_finite(torch.bfloat16)
+    wrong = 0
+    for s in _scales():
+        r = (F32(1) / s).astype(F32)
+        with np.errstate(over="ignore", invalid="ignore"):
+            q0 = (x * r).astype(F32)
+        n = np.rint(_clamp(q0, -127, 127))
+        want = _exact_codes(x, s)
+        wrong += int((n != want).sum())
+    assert wrong > 0
