@@ -486,6 +486,47 @@ def test_batches_beyond_eight_chunks(cuda, splits):
     _check(out, ref, f"B=600 splits={splits}")
 
 
+@pytest.mark.parametrize("how", ["auto", "single_pass", "ranges_auto", "ranges_512", "ranges_x2",
+                                 "bf16"])
+def test_thousands_of_short_sequences(cuda, how):
+    """B = 5000 ragged sequences of 0-40 tokens (79 chunks of 64 in every batch walk, a fifth of
+    them empty): the automatic call, the single pass (5000 x 4 per-sequence workgroups), the range
+    layout at its automatic count, at 512 ranges (paired ranges) and at 2 ranges per sequence
+    (10,000 ranges, the merge indexed by range), and the BF16 kernel, against the oracle."""
+    g = torch.Generator().manual_seed(5000)
+    lens = torch.randint(1, 41, (5000,), generator=g)
+    lens[torch.rand(5000, generator=g) < 0.2] = 0
+    lens = lens.tolist()
+    c = decode_case(lens, seed=5000, extra_blocks=9)
+    t = to_dev(c, cuda)
+    q, kc, vc, bt, sl, ks, vs = t
+    if how == "bf16":
+        k16, v16 = (x.to(cuda) for x in bf16_caches(c))
+        out = int8kv.bf16_paged_attention(q, k16, v16, bt, sl)
+        torch.cuda.synchronize()
+        ref = O.paged_attention_ref(c.query.float().numpy(), k16.float().cpu().numpy(),
+                                    v16.float().cpu().numpy(), c.block_tables.numpy(),
+                                    c.seq_lens.numpy())
+    else:
+        if how == "auto":
+            out = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs)
+        elif how == "single_pass":
+            out = int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs, num_splits=1)
+        elif how == "ranges_auto":
+            out = ranges_call(t, cuda)
+        elif how == "ranges_512":
+            from int8kv import _decode
+            out = torch.full_like(q, float("nan"))
+            _decode.paged_decode(q, kc, vc, bt, sl, ks, vs, out, 512)
+        else:
+            out = ranges_call(t, cuda, 2)
+        torch.cuda.synchronize()
+        ref = oracle_int8(c)
+    empty = [b for b, n in enumerate(lens) if n == 0]
+    assert (out[empty] == 0).all()
+    _check(out, ref, f"B=5000 {how}")
+
+
 @pytest.mark.parametrize("splits", [None, 3])
 def test_wide_tables_take_the_64bit_unit_scan(cuda, splits):
     """A table wide enough that one sequence could hold 2^25 tiles (4096-token blocks, 2^18
