@@ -527,6 +527,37 @@ def test_thousands_of_short_sequences(cuda, how):
     _check(out, ref, f"B=5000 {how}")
 
 
+@pytest.mark.parametrize("lens", [[300_000], [200_000, 70_000, 0, 5]])
+def test_sequences_beyond_the_range_cap(cuda, lens):
+    """Sequences longer than the automatic range count can cut finely (300,000 tokens: ~9,400
+    tiles, 37 per range at 256 ranges): the automatic call, the single pass (one workgroup per
+    kv head streams the whole sequence), 64 split workgroups per (sequence, kv head), the range
+    layout at its automatic count, and the BF16 kernel, against the oracle."""
+    c = decode_case(lens, seed=len(lens), extra_blocks=3)
+    t = to_dev(c, cuda)
+    q, kc, vc, bt, sl, ks, vs = t
+    ref = oracle_int8(c)
+    for what, fn in (
+            ("auto", lambda: int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs)),
+            ("single pass", lambda: int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs,
+                                                                num_splits=1)),
+            ("64 splits", lambda: int8kv.int8_paged_attention(q, kc, vc, bt, sl, ks, vs,
+                                                              num_splits=64)),
+            ("ranges", lambda: ranges_call(t, cuda))):
+        out = fn()
+        torch.cuda.synchronize()
+        if 0 in lens:
+            assert (out[lens.index(0)] == 0).all(), what
+        _check(out, ref, f"lens={lens} {what}")
+    k16, v16 = (x.to(cuda) for x in bf16_caches(c))
+    out16 = int8kv.bf16_paged_attention(q, k16, v16, bt, sl)
+    torch.cuda.synchronize()
+    ref16 = O.paged_attention_ref(c.query.float().numpy(), k16.float().cpu().numpy(),
+                                  v16.float().cpu().numpy(), c.block_tables.numpy(),
+                                  c.seq_lens.numpy())
+    _check(out16, ref16, f"lens={lens} bf16")
+
+
 @pytest.mark.parametrize("splits", [None, 3])
 def test_wide_tables_take_the_64bit_unit_scan(cuda, splits):
     """A table wide enough that one sequence could hold 2^25 tiles (4096-token blocks, 2^18
