@@ -996,12 +996,19 @@ def stamps_legs(dev, out_path: str | None) -> dict:
                 r[name] = med(calls, lambda st, h=h: np.median(rel(st, 7)[(st[:, 10] % 8 >= 4) == bool(h)]))
         return r
 
-    def phases(calls):
-        """Per-sequence / split layout: the phases of the median wave (ns)."""
+    def phases(calls, query_first=False):
+        """Per-sequence / split layout: the phases of the median wave (ns).  query_first: the
+        per-sequence layout, which requests the query at entry and builds it while the first
+        block ids are in flight (stamp 3 before stamp 2)."""
         seg = [st[st[:, 9] > 0] for st in calls]
-        names = (("sequence_length", 1, 0), ("stage_and_issue", 2, 9), ("query", 3, 2),
-                 ("k_scores_softmax", 4, 3), ("v_pv", 5, 4), ("rest_of_segment", 6, 5),
-                 ("state_to_barrier", 7, 6), ("entry_to_barrier", 7, 0))
+        if query_first:
+            names = (("sequence_length", 1, 0), ("ids_requested_query_built", 3, 9),
+                     ("ids_staged_and_issue", 2, 3), ("k_scores_softmax", 4, 2))
+        else:
+            names = (("sequence_length", 1, 0), ("stage_and_issue", 2, 9), ("query", 3, 2),
+                     ("k_scores_softmax", 4, 3))
+        names += (("v_pv", 5, 4), ("rest_of_segment", 6, 5), ("state_to_barrier", 7, 6),
+                  ("entry_to_barrier", 7, 0))
         return {n: med(seg, lambda st, a=a, b=b: np.median((st[:, a] - st[:, b]) * 10))
                 for n, a, b in names}
 
@@ -1096,7 +1103,7 @@ def stamps_legs(dev, out_path: str | None) -> dict:
         log(f"stamps {name}: {res[name]}")
     run = lambda: int8kv.int8_paged_attention(q, kc8, vc8, btd, lens, ks_d, vs_d)
     settle(run, batch=20, min_ms=20.0)
-    res["cfg2_b1x512_int8_per_sequence"] = phases(collect("i8", run))
+    res["cfg2_b1x512_int8_per_sequence"] = phases(collect("i8", run), query_first=True)
     log(f"stamps cfg2_b1x512_int8_per_sequence: {res['cfg2_b1x512_int8_per_sequence']}")
     if out_path:
         Path(out_path).parent.mkdir(parents=True, exist_ok=True)

@@ -75,7 +75,7 @@ __device__ __forceinline__ void store_stamps(Stamps& st, int waves_per_wg, int w
   } while (0)
 #define INT8KV_STAMPS_PARAM , Stamps* stamps_p = nullptr
 #define INT8KV_STAMPS_ARG , &stamps_
-#define INT8KV_STAMPS_ARG_NO_GROUP , nullptr, nullptr, nullptr, &stamps_
+#define INT8KV_STAMPS_ARG_NO_GROUP , nullptr, nullptr, nullptr, nullptr, &stamps_
 #define INT8KV_STAMPS_STORE(waves_per_wg, wave, lane) store_stamps(stamps_, waves_per_wg, wave, lane)
 #define INT8KV_STAMPS_ACCESSORS(unit)                                                          \
   extern "C" int int8kv_stamps_read_##unit(void* dst, size_t bytes) {                         \
@@ -985,13 +985,17 @@ __device__ __forceinline__ void write_zero_rows(const DecodeArgs& a, int64_t b, 
 // for the workgroup to merge, instead of an output row or a partial record.
 // vh: the grid head (head_map); with PAIR the first kv head of the pair.  PAD: head_dim below HD
 // (issue_k); the output columns at or past head_dim are not stored.
+// QPRE: the caller requested the query (issue_query into *qpre) before the sequence length was
+// known; its operand is then built while the first block ids are in flight (below).
 template <int CACHE, int QT, bool NT, bool QQ, int HD, int DEPTH, bool GROUP = false,
-          bool PAIR = false, bool PAD = false>
+          bool PAIR = false, bool PAD = false, bool QPRE = false>
 __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, int64_t b,
                                             int64_t L, int vh, int64_t ta, int64_t tb,
                                             bool full, int64_t rec, int lane,
                                             float* g_acc = nullptr, float* g_m = nullptr,
-                                            float* g_l = nullptr INT8KV_STAMPS_PARAM) {
+                                            float* g_l = nullptr,
+                                            const QueryRaw<QT, HD>* qpre = nullptr
+                                                INT8KV_STAMPS_PARAM) {
   typedef typename MfmaOp<CACHE>::T OpT;
   const int li = lane & 15;
   const int lg = lane >> 4;
@@ -1040,14 +1044,17 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
   VTile<CACHE, NB, HD> vt[DEPTH];
   TileRows<NB> ph[DEPTH];
   OpT pop[NB / 2][2];
-  auto chunk_prologue = [&]() {
-    stage_block_ids<NB>(a, ids, b, c0, c1, nblk, lane);
+  auto issue_first_tiles = [&]() {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       blocks_of(c0 + d < c1 ? c0 + d : c1 - 1, ph[d]);
       issue_k<CACHE, NB, NT, HD, PAD>(kt[d], kb, ph[d], a, li, lg);
       issue_v<CACHE, NB, NT, HD, PAD>(vt[d], vb, ph[d], a, li, lg);
     }
+  };
+  auto chunk_prologue = [&]() {
+    stage_block_ids<NB>(a, ids, b, c0, c1, nblk, lane);
+    issue_first_tiles();
   };
 
   // The query, the first chunk's block ids and its first DEPTH tiles are requested back to
@@ -1067,12 +1074,44 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
       ksc[0] = a.k_scale[kvh];
       if constexpr (PAIR) ksc[1] = a.k_scale[kvh + 1];
     }
-    QueryRaw<QT, HD> qraw;
-    issue_query<QT, HD, PAIR, PAD>(a, b, hm, li, lg, qraw);
-    chunk_prologue();
-    INT8KV_STAMP_SEG(2);
-    s_scale = finish_query<CACHE, QT, QQ, HD, PAIR, GROUP>(a, qraw, ksc, qop, qlo, q8op);
-    INT8KV_STAMP_SEG(3);
+    if constexpr (QPRE) {
+      // The query arrived (or is arriving) while the sequence length was read, so its operand is
+      // built between the first round of block-id loads and their wait: one unconditional pair
+      // of 32-bit loads per lane (the index clamped into the sequence's blocks, the low word and,
+      // for 64-bit tables, the high word) keeps the compiler's wait before the build down to the
+      // query loads.  Built after the first tile requests instead, it sat between the first
+      // tiles' arrival and their scores (0.12 us for a 16-bit query of a 16-bit cache, 0.24 us
+      // with the fp16 query scaling of an INT8 cache, at one tile per wave).  The first tiles are
+      // requested at the top of the chunk loop below, the one place every chunk's are.
+      const int n = (int)(NB * (c1 - c0));  // >= NB: this segment has a tile
+      const int64_t hi = a.num_blocks - 1;
+      const int gshift = a.block_shift - 4;
+      const int64_t blk = (NB * c0 + (lane < n ? lane : n - 1)) >> gshift;
+      const int64_t blkc = blk < nblk ? blk : nblk - 1;
+      const char* ip = static_cast<const char*>(a.bt) +
+                       ((b * a.bt_sb + blkc * a.bt_sl) << (a.bt_is64 ? 3 : 2));
+      const uint32_t wlo = *reinterpret_cast<const uint32_t*>(ip);
+      const uint32_t whi = *reinterpret_cast<const uint32_t*>(ip + (a.bt_is64 ? 4 : 0));
+      s_scale = finish_query<CACHE, QT, QQ, HD, PAIR, GROUP>(a, *qpre, ksc, qop, qlo, q8op);
+      INT8KV_STAMP_SEG(3);
+      const int64_t p = blk >= nblk ? 0
+                        : a.bt_is64 ? (int64_t)(((uint64_t)whi << 32) | wlo)
+                                    : (int64_t)(int32_t)wlo;
+      if (lane < n) ids[lane] = (int32_t)(p < 0 ? 0 : (p > hi ? hi : p));
+      for (int j = lane + kWave; j < n; j += kWave) {  // chunks of more than 64 row groups
+        const int64_t bj = (NB * c0 + j) >> gshift;
+        int64_t pj = 0;
+        if (bj < nblk) pj = load_index(a.bt, b * a.bt_sb + bj * a.bt_sl, a.bt_is64);
+        ids[j] = (int32_t)(pj < 0 ? 0 : (pj > hi ? hi : pj));
+      }
+    } else {
+      QueryRaw<QT, HD> qraw;
+      issue_query<QT, HD, PAIR, PAD>(a, b, hm, li, lg, qraw);
+      chunk_prologue();
+      INT8KV_STAMP_SEG(2);
+      s_scale = finish_query<CACHE, QT, QQ, HD, PAIR, GROUP>(a, qraw, ksc, qop, qlo, q8op);
+      INT8KV_STAMP_SEG(3);
+    }
   }
 
   // Tile t + d (buffer d): scores, refill K with tile t + d + DEPTH, P*V, refill V.  refill is a
@@ -1097,7 +1136,16 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     __builtin_amdgcn_sched_barrier(0);
   };
 
+  bool staged = QPRE;  // QPRE: the first chunk's ids are staged, its tiles not yet requested
   while (true) {
+    if constexpr (QPRE) {
+      // One request site for every chunk's first tiles: with a second one before the loop, hipcc
+      // merged the two into the loop header behind a wait for every load in flight.
+      if (!staged) stage_block_ids<NB>(a, ids, b, c0, c1, nblk, lane);
+      staged = false;
+      issue_first_tiles();
+      INT8KV_STAMP_SEG(2);
+    }
     int64_t t = c0;
     // Every refill of these blocks lies inside the chunk.
     for (; t + 2 * DEPTH - 1 < c1; t += DEPTH) {
@@ -1126,7 +1174,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     if (c1 >= tb) break;
     c0 = c1;
     c1 = (tb - c0 > kChunkTiles) ? c0 + kChunkTiles : tb;
-    chunk_prologue();
+    if constexpr (!QPRE) chunk_prologue();
   }
 
   INT8KV_STAMP_SEG(6);
@@ -1329,6 +1377,15 @@ constexpr int group_waves() {
   return HD > 128 ? 4 : 8;
 }
 
+// Whether share v of nw equal shares of a span (share v of s tiles: [v s / nw, (v + 1) s / nw))
+// is non-empty for some span of at most smax tiles.
+__device__ __forceinline__ bool share_may_hold(int v, int smax, int nw) {
+  if (smax >= nw) return true;
+  for (int s = 1; s <= smax; ++s)
+    if ((v + 1) * s / nw > v * s / nw) return true;
+  return false;
+}
+
 template <int CACHE, int QT, bool QQ, int HD, bool SPLIT, bool PAD = false>
 __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves_per_eu(HD > 128 ? 1 : 2))) void group_kernel(DecodeArgs a) {
   constexpr int NW = group_waves<HD>();
@@ -1344,7 +1401,34 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
   const int vh = blockIdx.y;  // grid head (head_map)
   INT8KV_STAMPS_DECL
   INT8KV_STAMP(0);
-  const int64_t L = seq_len_uniform(a, b);  // first: every later step waits for it
+  // The span's NW equal shares go to the waves SIMD by SIMD (wave w runs on SIMD w % 4): wave w
+  // takes share (w % 4) (NW / 4) + w / 4, so with fewer tiles than waves the waves that get one
+  // sit on different SIMDs.  (In wave order two tiles went to waves 3 and 7, which share SIMD 3.)
+  const int v = NW > 4 ? (wave % 4) * (NW / 4) + wave / 4 : wave;
+  QueryRaw<QT, HD> qraw;
+  bool early_q = false;
+  int64_t L;
+  if constexpr (SPLIT) {
+    L = seq_len_uniform(a, b);  // first: every later step waits for it
+  } else {
+    // The query rows do not depend on the length, so the waves whose share can hold a tile (for
+    // the longest sequence the table holds) request them right behind it: their operand is then
+    // built while the block ids are in flight (run_segment, QPRE).  The length's load goes
+    // first (a query load ahead of it delayed it by ~0.7 us); in the split layout, whose waves
+    // hold one tile each at these sizes, the waiting length outweighed the gain (0.2-0.6 us
+    // slower per call), so its kernel keeps the query in run_segment.
+    const char* slp = static_cast<const char*>(a.sl) + (b << (a.sl_is64 ? 3 : 2));
+    const uint32_t sl_lo = *reinterpret_cast<const uint32_t*>(slp);
+    const uint32_t sl_hi = *reinterpret_cast<const uint32_t*>(slp + (a.sl_is64 ? 4 : 0));
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t nmax = tiles_of(a, (int64_t)a.width << a.block_shift);
+    early_q = share_may_hold(v, nmax < (int64_t)NW ? (int)nmax : NW, NW);
+    if (early_q) issue_query<QT, HD, false, PAD>(a, b, head_map(a, vh), li, lg, qraw);
+    const int64_t Lr =
+        a.sl_is64 ? (int64_t)(((uint64_t)sl_hi << 32) | sl_lo) : (int64_t)(int32_t)sl_lo;
+    const int64_t cap = (int64_t)a.width << a.block_shift;
+    L = Lr < 0 ? 0 : (Lr > cap ? cap : Lr);
+  }
   INT8KV_STAMP(1);
   const HeadMap hm = head_map(a, vh);
   const int G = hm.g;
@@ -1360,17 +1444,16 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
     t0 = (int64_t)blockIdx.z * n / gridDim.z;
     span = ((int64_t)blockIdx.z + 1) * n / gridDim.z - t0;
   }
-  // The span's NW equal shares go to the waves SIMD by SIMD (wave w runs on SIMD w % 4): wave w
-  // takes share (w % 4) (NW / 4) + w / 4, so with fewer tiles than waves the waves that get one
-  // sit on different SIMDs.  (In wave order two tiles went to waves 3 and 7, which share SIMD 3.)
-  const int v = NW > 4 ? (wave % 4) * (NW / 4) + wave / 4 : wave;
   const int64_t ta = t0 + v * span / NW;
   const int64_t tb = t0 + (v + 1) * span / NW;
   if (ta < tb) {
     INT8KV_STAMP(9);
-    run_segment<CACHE, QT, false, QQ, HD, 2, true, false, PAD>(
-        a, s_ids[wave], b, L, vh, ta, tb, false, 0, lane, s_acc[wave], s_m[wave],
-        s_l[wave] INT8KV_STAMPS_ARG);
+    // (Without SPLIT early_q holds whenever the share is non-empty; requested here, the query
+    // still precedes the block-id loads, which is all run_segment's waits assume.)
+    if (!SPLIT && !early_q) issue_query<QT, HD, false, PAD>(a, b, hm, li, lg, qraw);
+    run_segment<CACHE, QT, false, QQ, HD, 2, true, false, PAD, !SPLIT>(
+        a, s_ids[wave], b, L, vh, ta, tb, false, 0, lane, s_acc[wave], s_m[wave], s_l[wave],
+        &qraw INT8KV_STAMPS_ARG);
   } else if (li < G) {  // no tiles for this wave: the neutral state
 #pragma unroll
     for (int j = 0; j < HD / 4; ++j) s_acc[wave][j * kWave + lane] = 0.0f;

@@ -2,8 +2,10 @@
 s_memrealtime stamps.  Its outputs must be bit-identical to the product library's (the stamps only
 read a clock and store at each wave's end), and every stored timeline must be ordered: entry <=
 plan / sequence length <= first segment entered <= block ids staged <= query built <= first
-scores <= first P*V <= segment done <= end.  Covered: the INT8 range layout (several segments
-per wave), the BF16 split per-sequence layout, and the load-only probe."""
+scores <= first P*V <= segment done <= end (the per-sequence layout requests the query at entry
+and builds it while the block ids are in flight: query built <= block ids staged there).
+Covered: the INT8 range layout (several segments per wave), the INT8 per-sequence layout, the
+BF16 split per-sequence layout, and the load-only probe."""
 
 from __future__ import annotations
 
@@ -93,6 +95,20 @@ def test_split_layout_bf16(cuda, slib):
     seg = st[st[:, 9] > 0]
     print(f"split layout: {len(st)} waves stored, {len(seg)} with tiles", flush=True)
     assert len(seg) > 0 and _ordered(seg, [0, 1, 9, 2, 3, 4, 5, 6, 7])
+
+
+def test_per_sequence_layout_int8(cuda, slib):
+    c = decode_case([512, 300, 0, 1000], seed=73)
+    t = to_dev(c, cuda)
+    flags = _lib.DECODE_ALL | _lib.DECODE_PER_SEQUENCE
+    _lib.check(slib.int8kv_stamps_clear_i8(), "clear")
+    got = _noalloc(slib, *t, flags=flags)
+    want = _product(*t, flags=flags)
+    assert torch.equal(got, want)
+    st = _read(slib, "i8")
+    seg = st[st[:, 9] > 0]
+    print(f"per-sequence layout: {len(st)} waves stored, {len(seg)} with tiles", flush=True)
+    assert len(seg) > 0 and _ordered(seg, [0, 1, 9, 3, 2, 4, 5, 6, 7])
 
 
 def test_load_probe(cuda, slib):
