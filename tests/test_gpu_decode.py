@@ -691,6 +691,28 @@ def test_per_sequence_mode(cuda, hq, hkv, d):
            f"per-sequence bf16 {hq}/{hkv}/{d}")
 
 
+@pytest.mark.parametrize("block_size,table64,qdtype", [(64, True, torch.float32),
+                                                      (32, True, torch.bfloat16),
+                                                      (256, False, torch.float16)])
+def test_per_sequence_mode_first_chunk_forms(cuda, block_size, table64, qdtype):
+    """The per-sequence layout's first chunk: its waves load the first round of block ids as raw
+    32-bit words (the high word of a 64-bit table too), build the query operand before those
+    loads' wait, then stage any further rounds (a 9000-token sequence gives a wave 35 tiles,
+    70 row groups: one more round).  Oracle parity with 64-bit and 32-bit tables, 32-256-token
+    blocks (several row groups per block id), empty, one-token and block-boundary lengths."""
+    lens = [0, 1, 9000, block_size, block_size + 1, 700]
+    c = decode_case(lens, seed=block_size + 7, extra_blocks=7, block_size=block_size)
+    ref = O.paged_attention_ref(c.query.to(qdtype).float().numpy(), c.kc, c.vc,
+                                c.block_tables.numpy(), c.seq_lens.numpy(), c.k_scale.numpy(),
+                                c.v_scale.numpy())
+    q, kc, vc, bt, sl, ks, vs = to_dev(c, cuda)
+    if table64:
+        bt = bt.to(torch.int64)
+    out = _group(q.to(qdtype), kc, vc, bt, sl, ks, vs)
+    assert (out[0] == 0).all()
+    _check(out, ref, f"per-sequence bs={block_size} table64={table64} {qdtype}")
+
+
 @pytest.mark.parametrize("ranges", [100, 200, 201, 640])
 def test_merge_grids_on_both_sides_of_the_rule(cuda, ranges):
     """The merge indexed by range (one workgroup per range, from the decode kernel's cut-sequence
