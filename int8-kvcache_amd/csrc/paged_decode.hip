@@ -490,13 +490,17 @@ int plan_call(int query_dtype, int cache_dtype, int64_t batch, int32_t num_q_hea
                 min_tiles, num_ranges, &p.merge_waves, &p.merge_fold);
   }
   // Non-temporal K/V loads when the call may stream more than kNonTemporalMinBytes: the most it
-  // can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).  Only
-  // INT8 caches use the hint (stream_load); their lanes read K in 32-byte runs at every head_dim
-  // (k_run).  With one 64-byte run per lane at head_dim 256 the hint had made those calls 13-15 %
-  // slower; with two 32-byte runs it makes them 10 % faster (Gemma-2-9B shape, B = 64 x
-  // U[1, 16384]: 347 -> 313 us, 6.44 TB/s).  The per-sequence kernels read without it.
+  // can read is min(pool, batch x table width) blocks of K and V (host-side sizes only).  INT8
+  // lanes read K in 32-byte runs at every head_dim (k_run).  With one 64-byte run per lane at
+  // head_dim 256 the hint had made those calls 13-15 % slower; with two 32-byte runs it makes
+  // them 10 % faster (Gemma-2-9B shape, B = 64 x U[1, 16384]: 347 -> 313 us, 6.44 TB/s).
+  // 16-bit caches take it at head_dim 128 only, where their K loads follow k_spread (a 64-byte
+  // half line per token and instruction): cfg3 BF16 404 -> 360 us, B = 32 x 8256 99.0 -> 89.5,
+  // B = 16 x 16384 99.7 -> 90.2 (in runs of k_run the hint made the same calls 10-11 % slower);
+  // at head_dim 256 it measured 1 % slower (659 -> 666 us), and padded head_dims and kv-head
+  // pairs (k_run order) are not measured with it.  The per-sequence kernels read without it.
   const int64_t touch_blocks = batch * table_width < num_blocks ? batch * table_width : num_blocks;
-  p.nt = i8 && !p.group_mode &&
+  p.nt = (i8 || (hd == 128 && !p.pad && !p.kv_pair)) && !p.group_mode &&
          (double)touch_blocks * block_size * num_kv_heads * head_dim * ce * 2 >
              (double)kNonTemporalMinBytes;
   *hp = p;

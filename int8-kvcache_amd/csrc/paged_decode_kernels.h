@@ -517,7 +517,7 @@ __device__ __forceinline__ void store_n(char* p, const float (&x)[N]) {
 // slower with the hint.
 template <int CACHE, bool NT, typename T>
 __device__ __forceinline__ T stream_load(const T* p) {
-  if constexpr (CACHE == kI8 && NT)
+  if constexpr (NT)
     return __builtin_nontemporal_load(p);
   else
     return *p;
@@ -540,10 +540,21 @@ __device__ __forceinline__ constexpr int k_run(int run, int lg) {
   return HD > 128 ? run * (HD / 2) + lg * (HD / 8) : lg * (HD / 4);
 }
 
+// SPREAD (16-bit caches outside kv-head pairs): k-step j of lane group lg holds head_dim
+// elements 32 j + 8 lg .. + 7 instead of the runs of k_run, so the four lane groups of a token
+// read one contiguous 64-byte half line per load instruction (its 16-byte piece j at byte
+// 64 j + 16 lg); in runs of HD/4 (64 bytes per lane) each 16-byte load of the four touched both
+// 128-byte lines of a 256-byte row, and with the non-temporal hint the kernel ran 10-11 % slower
+// instead of 11 % faster.  An INT8 row is one 128-byte line, which each of its loads already
+// meets as one line: the same order measured within noise there (cfg3 191.7 vs 191.5 us).  Any
+// assignment of head_dim elements to k-steps gives the same dot products as long as K and the
+// query use the same one.
+__device__ __forceinline__ constexpr int k_spread(int j, int lg) { return 32 * j + 8 * lg; }
+
 // PAD (head_dim D < HD): a lane's 16-byte pieces at or past element D read the row's first piece
 // instead, which keeps every access inside the row; their products meet query elements that are
 // zero, and the V columns at or past D feed output columns that are never stored.
-template <int CACHE, int NB, bool NT, int HD, bool PAD = false>
+template <int CACHE, int NB, bool NT, int HD, bool PAD = false, bool SPREAD = false>
 __device__ __forceinline__ void issue_k(KTile<CACHE, NB, HD>& r, const char* kb,
                                         const TileRows<NB>& ph, const DecodeArgs& a, int li,
                                         int lg) {
@@ -553,6 +564,16 @@ __device__ __forceinline__ void issue_k(KTile<CACHE, NB, HD>& r, const char* kb,
 #pragma unroll
   for (int s = 0; s < NB; ++s) {
     const char* row = kb + ph.id[s] * a.kc_sb + (ph.row[s] + li) * a.kc_ss;
+    if constexpr (SPREAD) {
+      static_assert(E == 2, "16-bit caches: one 16-byte piece per k-step");
+#pragma unroll
+      for (int j = 0; j < k_pieces<CACHE, HD>(); ++j) {
+        const int e = k_spread(j, lg);
+        r.k[s][j] = stream_load<CACHE, NT>(reinterpret_cast<const u32x4*>(
+            row + (!PAD || e < a.head_dim ? e * E : 0)));
+      }
+      continue;
+    }
 #pragma unroll
     for (int run = 0; run < kRuns; ++run) {
       if constexpr (PAD) {
@@ -776,7 +797,7 @@ struct QueryRaw<kF32, HD> {
 //   li < G, 1 above) and the other half's lanes hold zeros, so each column's scores use only its
 //   own kv head's K elements.
 //   hm: the grid head's query heads (head_map).  PAD: elements at or past head_dim are zero.
-template <int QT, int HD, bool PAIR = false, bool PAD = false>
+template <int QT, int HD, bool PAIR = false, bool PAD = false, bool SPREAD = false>
 __device__ __forceinline__ void issue_query(const DecodeArgs& a, int64_t b, const HeadMap& hm,
                                             int li, int lg, QueryRaw<QT, HD>& raw) {
   constexpr int QE = esize<QT>();
@@ -784,6 +805,27 @@ __device__ __forceinline__ void issue_query(const DecodeArgs& a, int64_t b, cons
   constexpr int N = sizeof(raw.w) / sizeof(raw.w[0]);
   constexpr int kRuns = HD > 128 ? 2 : 1;
   const int kvh = hm.kv;
+  if constexpr (SPREAD) {  // k-step j: elements k_spread(j, lg) .. + 7 (issue_k)
+    static_assert(!PAIR, "kv-head pairs keep the runs of k_run");
+    constexpr int VE = sizeof(Vec) / QE;  // elements per vector: 8 (16-bit) or 4 (fp32)
+    constexpr int PV = 8 / VE;            // vectors per k-step
+    if (li < hm.g) {
+      const char* qrow = a.q + ((int64_t)b * a.q_sb + (int64_t)(hm.q0 + li) * a.q_sh) * QE;
+#pragma unroll
+      for (int j = 0; j < HD / 32; ++j)
+#pragma unroll
+        for (int h = 0; h < PV; ++h) {
+          const int e = k_spread(j, lg) + h * VE;
+          raw.w[j * PV + h] = !PAD || e < a.head_dim
+                                  ? *reinterpret_cast<const Vec*>(qrow + e * QE)
+                                  : (Vec)(0);
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) raw.w[i] = (Vec)(0);
+    }
+    return;
+  }
   if constexpr (PAIR) {
     static_assert(HD == 128, "pairs of 64-wide kv heads");
     if (li < 2 * a.group && (lg >> 1) == (li >= a.group ? 1 : 0)) {
@@ -997,6 +1039,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
                                             const QueryRaw<QT, HD>* qpre = nullptr
                                                 INT8KV_STAMPS_PARAM) {
   typedef typename MfmaOp<CACHE>::T OpT;
+  constexpr bool kSpread = CACHE != kI8 && !PAIR;  // k_spread (issue_k, issue_query)
   const int li = lane & 15;
   const int lg = lane >> 4;
   const HeadMap hm = head_map(a, vh);
@@ -1048,7 +1091,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       blocks_of(c0 + d < c1 ? c0 + d : c1 - 1, ph[d]);
-      issue_k<CACHE, NB, NT, HD, PAD>(kt[d], kb, ph[d], a, li, lg);
+      issue_k<CACHE, NB, NT, HD, PAD, kSpread>(kt[d], kb, ph[d], a, li, lg);
       issue_v<CACHE, NB, NT, HD, PAD>(vt[d], vb, ph[d], a, li, lg);
     }
   };
@@ -1106,7 +1149,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
       }
     } else {
       QueryRaw<QT, HD> qraw;
-      issue_query<QT, HD, PAIR, PAD>(a, b, hm, li, lg, qraw);
+      issue_query<QT, HD, PAIR, PAD, kSpread>(a, b, hm, li, lg, qraw);
       chunk_prologue();
       INT8KV_STAMP_SEG(2);
       s_scale = finish_query<CACHE, QT, QQ, HD, PAIR, GROUP>(a, qraw, ksc, qop, qlo, q8op);
@@ -1127,7 +1170,7 @@ __device__ __forceinline__ void run_segment(const DecodeArgs& a, int32_t* ids, i
     INT8KV_STAMP_SEG(4);
     if (refill) {
       blocks_of(t + d + DEPTH, ph[d]);
-      issue_k<CACHE, NB, NT, HD, PAD>(kt[d], kb, ph[d], a, li, lg);
+      issue_k<CACHE, NB, NT, HD, PAD, kSpread>(kt[d], kb, ph[d], a, li, lg);
     }
     __builtin_amdgcn_sched_barrier(0);
     tile_pv<CACHE, NB, HD>(vt[d], pop, acc, valid, lg);
@@ -1423,7 +1466,8 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
     __builtin_amdgcn_sched_barrier(0);
     const int64_t nmax = tiles_of(a, (int64_t)a.width << a.block_shift);
     early_q = share_may_hold(v, nmax < (int64_t)NW ? (int)nmax : NW, NW);
-    if (early_q) issue_query<QT, HD, false, PAD>(a, b, head_map(a, vh), li, lg, qraw);
+    if (early_q)
+      issue_query<QT, HD, false, PAD, CACHE != kI8>(a, b, head_map(a, vh), li, lg, qraw);
     const int64_t Lr =
         a.sl_is64 ? (int64_t)(((uint64_t)sl_hi << 32) | sl_lo) : (int64_t)(int32_t)sl_lo;
     const int64_t cap = (int64_t)a.width << a.block_shift;
@@ -1450,7 +1494,8 @@ __global__ __launch_bounds__(group_waves<HD>() * 64) __attribute__((amdgpu_waves
     INT8KV_STAMP(9);
     // (Without SPLIT early_q holds whenever the share is non-empty; requested here, the query
     // still precedes the block-id loads, which is all run_segment's waits assume.)
-    if (!SPLIT && !early_q) issue_query<QT, HD, false, PAD>(a, b, hm, li, lg, qraw);
+    if (!SPLIT && !early_q)
+      issue_query<QT, HD, false, PAD, CACHE != kI8>(a, b, hm, li, lg, qraw);
     run_segment<CACHE, QT, false, QQ, HD, 2, true, false, PAD, !SPLIT>(
         a, s_ids[wave], b, L, vh, ta, tb, false, 0, lane, s_acc[wave], s_m[wave], s_l[wave],
         &qraw INT8KV_STAMPS_ARG);
@@ -1837,6 +1882,14 @@ void launch_ranges(const DecodeArgs& a, dim3 grid, int W, bool nt, hipStream_t s
     else
       launch_main<CACHE, QT, false, false, KH, PAIR, PAD>(a, grid, W, s);
   } else {
+    // 16-bit caches: non-temporal loads at head_dim 128 (plan_call decides), plain loads
+    // elsewhere.
+    if constexpr (HD == 128 && !PAIR && !PAD) {
+      if (nt) {
+        launch_main<CACHE, QT, true, false, KH, PAIR, PAD>(a, grid, W, s);
+        return;
+      }
+    }
     launch_main<CACHE, QT, false, false, KH, PAIR, PAD>(a, grid, W, s);
   }
 }

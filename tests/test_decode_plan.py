@@ -16,7 +16,7 @@ import torch
 
 from int8kv import _lib
 
-I8, BF16 = torch.int8, torch.bfloat16
+I8, BF16, F16 = torch.int8, torch.bfloat16, torch.float16
 Q = torch.bfloat16
 
 
@@ -240,14 +240,25 @@ def test_merge_kernel_choice():
 
 def test_non_temporal_threshold():
     """Non-temporal K/V loads when the call can read more than 128 MiB of K and V (min(pool,
-    batch x width) blocks), INT8 range layout only."""
+    batch x width) blocks), range layout only: INT8 caches at every head_dim, 16-bit caches at
+    head_dim 128 without padding or kv-head pairs (their K loads in the k_spread order)."""
     per_block = 16 * 4 * 128 * 2
     n = (128 << 20) // per_block  # 8192 blocks
     kw = dict(batch=64, ranges=256)  # the range layout at every width
     assert plan(width=n // 64, nb=n + 1000, **kw)["non_temporal"] == 0
     assert plan(width=n // 64 + 1, nb=n + 1000, **kw)["non_temporal"] == 1
     assert plan(width=4096, nb=n, **kw)["non_temporal"] == 0         # the pool bounds it
-    assert plan(cache=BF16, width=4096, nb=10 * n, **kw)["non_temporal"] == 0
+    # 16-bit caches: twice the bytes per block, so half the blocks reach the bound.
+    assert plan(cache=BF16, width=n // 128, nb=n + 1000, **kw)["non_temporal"] == 0
+    assert plan(cache=BF16, width=n // 128 + 1, nb=n + 1000, **kw)["non_temporal"] == 1
+    assert plan(cache=F16, width=4096, nb=10 * n, **kw)["non_temporal"] == 1
+    big = dict(width=4096, nb=10 * n, **kw)
+    assert plan(cache=BF16, d=256, hq=16, hkv=8, **big)["non_temporal"] == 0   # head_dim 256
+    assert plan(cache=BF16, d=96, **big)["non_temporal"] == 0                  # padded
+    assert plan(cache=BF16, d=64, hq=32, hkv=8, **big)["non_temporal"] == 0    # kv-head pairs
+    assert plan(cache=BF16, d=64, hq=12, hkv=3, **big)["non_temporal"] == 0    # head_dim 64
+    assert plan(d=256, hq=16, hkv=8, **big)["non_temporal"] == 1               # INT8: all
+    assert plan(cache=BF16, batch=1, width=256, nb=10 * n)["non_temporal"] == 0  # per-sequence
 
 
 def test_kv_head_pairs():
