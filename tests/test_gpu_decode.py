@@ -713,6 +713,35 @@ def test_per_sequence_mode_first_chunk_forms(cuda, block_size, table64, qdtype):
     _check(out, ref, f"per-sequence bs={block_size} table64={table64} {qdtype}")
 
 
+@pytest.mark.parametrize("cache_dtype", [torch.bfloat16, torch.float16])
+def test_sixteen_bit_cache_non_temporal_path(cuda, cache_dtype):
+    """16-bit caches above the 128 MiB bound (8 sequences, 600-block tables over a pool of ~4,570
+    blocks: ~150 MB of possible K/V reads) take the range kernel with non-temporal loads and K in
+    the k_spread order (the plan reports it).  Oracle parity for a BF16 and an fp32 query, ragged lengths, one empty
+    sequence and one sequence at the table's full width."""
+    from int8kv import _lib
+
+    lens = [9000, 0, 4097, 9600, 31, 7000, 2500, 8191]
+    c = decode_case(lens, seed=77, width=600, extra_blocks=2000)
+    k16, v16 = (x.to(cuda) for x in bf16_caches(c, cache_dtype))
+    q, _, _, bt, sl, _, _ = to_dev(c, cuda)
+    plan = _lib.decode_plan(q.dtype, cache_dtype, len(lens), 28, 4, 128, k16.shape[0], 16,
+                            bt.shape[1])
+    assert plan["layout"] == "ranges" and plan["non_temporal"] == 1, plan
+    ref = O.paged_attention_ref(c.query.float().numpy(), k16.float().cpu().numpy(),
+                                v16.float().cpu().numpy(), c.block_tables.numpy(),
+                                c.seq_lens.numpy())
+    op = int8kv.bf16_paged_attention
+    out = op(q, k16, v16, bt, sl)
+    torch.cuda.synchronize()
+    assert (out[1] == 0).all()
+    _check(out, ref, f"{cache_dtype} cache, bf16 query, non-temporal")
+    out32 = op(q.float(), k16, v16, bt, sl)
+    torch.cuda.synchronize()
+    err, _, _ = metrics(out32.cpu().numpy(), ref)
+    assert err <= 1e-3, err
+
+
 @pytest.mark.parametrize("ranges", [100, 200, 201, 640])
 def test_merge_grids_on_both_sides_of_the_rule(cuda, ranges):
     """The merge indexed by range (one workgroup per range, from the decode kernel's cut-sequence
