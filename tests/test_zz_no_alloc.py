@@ -3,9 +3,9 @@
 It must give exactly what int8kv_paged_decode gives with a caller's workspace (same kernels,
 same plan, partials in the library's fixed scratch array instead).  Two calls in a row on the
 same GPU, the second with a smaller input, both bit-identical to the workspace entry point and
-within the oracle bar; then the INT8 x BF16-cache and forced-range variants, the merge indexed by
-range, head_dim 256, head_dim 64 (kv-head pairs, per-sequence layout) and the split
-per-sequence layout, a padded head_dim and a group above 16.
+within the oracle bar; then the INT8 x BF16-cache and forced-range variants, a BF16 cache above the
+non-temporal bound, the merge indexed by range, head_dim 256, head_dim 64 (kv-head pairs,
+per-sequence layout) and the split per-sequence layout, a padded head_dim and a group above 16.
 """
 
 from __future__ import annotations
@@ -78,6 +78,22 @@ def test_bf16_cache_and_paired_ranges(cuda):
     got = _noalloc(q, k16, v16, bt, sl, None, None, torch.full_like(q, float("nan")))
     torch.cuda.synchronize()
     assert torch.equal(got, want), "bf16 cache"
+
+
+def test_bf16_cache_above_the_non_temporal_bound(cuda):
+    """A BF16 cache whose call may read ~150 MB (600-block tables over a ~4,570-block pool): the
+    range kernel with non-temporal loads, the same from both entry points."""
+    c = decode_case([9000, 0, 4097, 9600, 31, 7000, 2500, 8191], seed=78, width=600,
+                    extra_blocks=2000)
+    q, _, _, bt, sl, _, _ = to_dev(c, cuda)
+    k16, v16 = (t.to(cuda) for t in bf16_caches(c))
+    plan = _lib.decode_plan(q.dtype, k16.dtype, q.shape[0], 28, 4, 128, k16.shape[0], 16,
+                            bt.shape[1], no_alloc=True)
+    assert plan["non_temporal"] == 1, plan
+    want = _with_workspace(q, k16, v16, bt, sl, None, None)
+    got = _noalloc(q, k16, v16, bt, sl, None, None, torch.full_like(q, float("nan")))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), "bf16 cache, non-temporal"
 
 
 def test_range_indexed_merge_and_head_dim_256(cuda):
